@@ -1,0 +1,197 @@
+"""Benchmark of the quantized expert-GEMV path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fp4|all]
+
+A step is one launch of the hot path over one batch of synthetic input. The headline workload is
+one FP4 (e2m1, E8M0 per 32) GEMV, W [2048 x 7168], x bf16 [1 x 7168],
+y bf16 [1 x 2048]. Weights are seeded N(0, 0.02) quantized on the GPU; the timed launches cycle
+through enough distinct weight copies (>= 512 MB) that the 256 MB Infinity Cache cannot serve
+repeats, so every step reads its weights from HBM. Launches are replayed from a HIP graph so that
+the GPU runs them back to back; HIP events on the launch stream bracket exactly K steps.
+
+`value` = algorithmic bytes per step (codes + scales + x + y, each once) / measured time per step.
+One JSON line is printed; other configurations appear under "extra".
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+ROTATE_BYTES = 512 << 20
+METRIC = "HBM GB/s (% of peak) for FP8/FP4 expert GEMV; MoE-layer decode tokens/s"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", default="all", help="fp4 = the headline workload only")
+    ap.add_argument("--eager", action="store_true", help="also time launches issued one by one from Python")
+    return ap.parse_args()
+
+
+def timed_steps(torch, launch, copies, steps, warmup, use_graph=True):
+    """Runs `steps` launches (launch(i) issues step i on the current stream) after `warmup`, and
+    returns ms per step measured with events on the launch stream."""
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        if use_graph:
+            for i in range(copies):  # warm the code path before capture
+                launch(i)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(copies):
+                    launch(i)
+            reps = max(1, round(steps / copies))
+            wreps = max(1, round(warmup / copies))
+            for _ in range(wreps):
+                graph.replay()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(reps):
+                graph.replay()
+            b.record(stream)
+            torch.cuda.synchronize()
+            n = reps * copies
+        else:
+            for i in range(warmup):
+                launch(i % copies)
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for i in range(steps):
+                launch(i % copies)
+            b.record(stream)
+            torch.cuda.synchronize()
+            n = steps
+    return a.elapsed_time(b) / n, n
+
+
+def gemv_workload(torch, fmt, rows, k, m, steps, warmup, use_graph=True):
+    from stblarge_amd import data, ops
+
+    dev = torch.device("cuda:0")
+    w = data.weight(rows, k, seed=1, device=dev)
+    if fmt == "fp4":
+        codes, scales = ops.quant_fp4(w)
+        alg = data.algorithmic_bytes_fp4(rows, k, m)
+        wbytes = codes.numel() + scales.numel()
+    else:
+        codes, scales = ops.quant_fp8_b128(w)
+        alg = data.algorithmic_bytes_fp8(rows, k, m)
+        wbytes = codes.numel() + scales.numel() * 4
+    del w
+    copies = max(2, math.ceil(ROTATE_BYTES / wbytes))
+    cs = [codes.clone() for _ in range(copies)]
+    ss = [scales.clone() for _ in range(copies)]
+    x = data.activation(m, k, seed=2, device=dev)
+    y = torch.empty((m, rows), dtype=torch.bfloat16, device=dev)
+    fn = ops.gemv_fp4 if fmt == "fp4" else ops.gemv_fp8
+
+    def launch(i):
+        fn(cs[i], ss[i], x, out=y)
+
+    ms, n = timed_steps(torch, launch, copies, steps, warmup, use_graph)
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"workload": f"{fmt}_gemv_{rows}x{k}_m{m}", "rows": rows, "k": k, "m": m, "ms_per_step": ms,
+            "steps": n, "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS, "weight_copies": copies,
+            "graph": use_graph}
+
+
+def cpu_baseline(seconds):
+    """The oracle's scalar C GEMV (oracle/stbl_oracle.c orc_gemv_fp4) on the headline workload's
+    shape, one thread, repeated for about `seconds`."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from stblarge_amd import data
+
+    rows, k = 2048, 7168
+    w = data.weight(rows, k, seed=1)
+    codes, scales = oracle.quant_fp4(w.numpy())
+    x = data.activation(1, k, seed=2).float().numpy()
+    alg = data.algorithmic_bytes_fp4(rows, k, 1)
+    oracle.gemv_fp4(codes, scales, x)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.gemv_fp4(codes, scales, x)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    del torch
+    return {"value": alg * reps / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} x fp4 GEMV 2048x7168 m=1 (oracle orc_gemv_fp4, scalar C, fp64 accumulate) in {el:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the path is single-GPU; see the sharding notes): --gpus {args.gpus} "
+              "is not supported", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    from stblarge_amd import _lib
+
+    _lib.load()  # fails loudly when the library was not built
+
+    head = gemv_workload(torch, "fp4", 2048, 7168, 1, args.steps, args.warmup)
+    print(f"# {head['workload']}: {head['ms_per_step'] * 1e3:.3f} us/step, {head['GB_s']:.0f} GB/s", file=sys.stderr,
+          flush=True)
+    extra = {}
+    if args.only != "fp4":
+        for fmt, rows, k, m in (("fp4", 7168, 2048, 1), ("fp8", 2048, 7168, 1), ("fp8", 7168, 2048, 1),
+                                ("fp4", 2048, 7168, 4), ("fp8", 2048, 7168, 4)):
+            r = gemv_workload(torch, fmt, rows, k, m, args.steps, args.warmup)
+            extra[r["workload"]] = r
+            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
+                  flush=True)
+    if args.eager:
+        r = gemv_workload(torch, "fp4", 2048, 7168, 1, args.steps, args.warmup, use_graph=False)
+        extra["fp4_gemv_2048x7168_m1_eager"] = r
+        print(f"# eager launches: {r['ms_per_step'] * 1e3:.3f} us/step", file=sys.stderr, flush=True)
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    gbs = head["GB_s"]
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": head["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "e2m1 weights x bf16 activations, f32 accumulate",
+        "data": "synthetic (seeded N(0,0.02) weights quantized on the GPU, N(0,1) bf16 x)",
+        "config": {"workload": head["workload"], "rows": 2048, "k": 7168, "m": 1,
+                   "weight_copies": head["weight_copies"], "rotation_MB": round(head["weight_copies"] * 7.8, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

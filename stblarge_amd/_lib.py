@@ -1,0 +1,76 @@
+"""ctypes binding of libstbl_amd.so (the C ABI declared in include/stbl_amd.h).
+
+The library is loaded from the package directory, where stblarge_amd.build puts it. There is no
+fallback: if the library is missing, load() raises, and every op in stblarge_amd.ops fails loudly.
+"""
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libstbl_amd.so")
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+F = ctypes.c_float
+PP = ctypes.POINTER(ctypes.c_void_p)
+PF = ctypes.POINTER(ctypes.c_float)
+
+# name -> (restype, argtypes). Every function of include/stbl_amd.h appears here.
+SIGNATURES = {
+    # reference surface (stbl/kernels.h)
+    "stbl_act_quant_fp8": (None, [P, I, P]),
+    "stbl_round_bf16": (None, [P, I, P]),
+    "stbl_gemv_fp8": (None, [P, P, P, P, I, I, I, P]),
+    "stbl_gemv_mxfp4": (None, [P, P, P, I, I, P]),
+    "stbl_gemv_mxfp4_batch": (None, [PP, PP, PP, I, I, I, P]),
+    "stbl_swiglu": (None, [P, P, P, F, F, I, P]),
+    "stbl_swiglu_batch": (None, [P, P, P, PF, I, F, I, P]),
+    "stbl_axpy": (None, [P, P, F, I, P]),
+    # v2
+    "stbl_amd_gemv_fp4": (I, [P, P, P, P, I, I, I, I, P]),
+    "stbl_amd_gemv_fp8": (I, [P, P, P, P, I, I, I, I, P]),
+    "stbl_amd_act_quant": (I, [P, I, I, I, I, P, P, P, P]),
+    "stbl_amd_quant_fp4": (I, [P, P, P, I, I, P]),
+    "stbl_amd_quant_fp8_b128": (I, [P, P, P, I, I, P]),
+    "stbl_amd_dequant_fp4": (I, [P, P, P, I, I, P]),
+    "stbl_amd_dequant_gguf17": (I, [P, P, I, I, P]),
+    "stbl_amd_dequant_fp8": (I, [P, P, P, I, I, I, P]),
+    "stbl_amd_last_error": (I, [ctypes.c_char_p, I]),
+    "stbl_amd_version": (I, []),
+}
+
+_lib = None
+
+
+class StblError(RuntimeError):
+    pass
+
+
+def load():
+    """The bound library (loaded once). Raises if it was not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise StblError(f"{LIB_PATH} is missing: build it with `python -m stblarge_amd.build`")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def last_error():
+    """(code, message) of the calling thread's last recorded failure; clears it."""
+    buf = ctypes.create_string_buffer(256)
+    code = load().stbl_amd_last_error(buf, 256)
+    return code, buf.value.decode(errors="replace")
+
+
+def check(status, what):
+    """Raise StblError for a non-zero v2 status (or a recorded failure of a void entry point)."""
+    code, msg = last_error()
+    if status not in (0, None) or code:
+        raise StblError(f"{what} failed: status {status}, hipError {code}: {msg}")

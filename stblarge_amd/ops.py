@@ -1,0 +1,231 @@
+"""Torch-facing wrappers over the C ABI: device tensors in, device tensors out.
+
+PyTorch only allocates memory and supplies the current stream; every computation runs in
+libstbl_amd.so. Shapes and dtypes are checked here so that a wrong call raises instead of launching a
+kernel on a buffer of the wrong size.
+
+Names follow the reference:
+  * act_quant / gemv_fp8 / gemv_fp4 restate ref/kernel.py's act_quant, fp8_gemm and fp4_gemm for
+    activation rows M <= 4 (the decode case), with bf16 activations;
+  * stbl_* functions keep the reference engine's operator surface (stbl/kernels.h): fp32 activation
+    buffers, results written into caller-provided tensors.
+"""
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+P = ctypes.c_void_p
+
+
+def _ptr(t):
+    return P(t.data_ptr()) if t is not None else None
+
+
+def _stream(stream=None):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return P(s.cuda_stream)
+
+
+def _need(t, dtype, name, dims=None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if dims is not None and t.dim() != dims:
+        raise ValueError(f"{name} must have {dims} dims, got shape {tuple(t.shape)}")
+
+
+def _rows2(x):
+    return x if x.dim() == 2 else x.view(1, -1)
+
+
+# ---- quantizers / dequantizers --------------------------------------------------------------------
+
+def quant_fp4(w):
+    """fp32 [N, K] -> (codes uint8 [N, K/2], E8M0 scales uint8 [N, K/32])."""
+    _need(w, torch.float32, "w", 2)
+    n, k = w.shape
+    codes = torch.empty((n, k // 2), dtype=torch.uint8, device=w.device)
+    scales = torch.empty((n, k // 32), dtype=torch.uint8, device=w.device)
+    _lib.check(_lib.load().stbl_amd_quant_fp4(_ptr(codes), _ptr(scales), _ptr(w), n, k, _stream()), "quant_fp4")
+    return codes, scales
+
+
+def quant_fp8_b128(w):
+    """fp32 [N, K] -> (e4m3 codes uint8 [N, K], fp32 scales [ceil(N/128), ceil(K/128)])."""
+    _need(w, torch.float32, "w", 2)
+    n, k = w.shape
+    codes = torch.empty((n, k), dtype=torch.uint8, device=w.device)
+    scales = torch.empty(((n + 127) // 128, (k + 127) // 128), dtype=torch.float32, device=w.device)
+    _lib.check(_lib.load().stbl_amd_quant_fp8_b128(_ptr(codes), _ptr(scales), _ptr(w), n, k, _stream()),
+               "quant_fp8_b128")
+    return codes, scales
+
+
+def dequant_fp4(codes, scales):
+    _need(codes, torch.uint8, "codes", 2)
+    _need(scales, torch.uint8, "scales", 2)
+    n, k = codes.shape[0], codes.shape[1] * 2
+    if scales.shape != (n, k // 32):
+        raise ValueError(f"scales must be {(n, k // 32)}, got {tuple(scales.shape)}")
+    out = torch.empty((n, k), dtype=torch.float32, device=codes.device)
+    _lib.check(_lib.load().stbl_amd_dequant_fp4(_ptr(out), _ptr(codes), _ptr(scales), n, k, _stream()), "dequant_fp4")
+    return out
+
+
+def dequant_gguf17(w, rows, k):
+    _need(w, torch.uint8, "w")
+    if w.numel() != rows * (k // 32) * 17:
+        raise ValueError("w must hold rows * k/32 17-byte blocks")
+    out = torch.empty((rows, k), dtype=torch.float32, device=w.device)
+    _lib.check(_lib.load().stbl_amd_dequant_gguf17(_ptr(out), _ptr(w), rows, k, _stream()), "dequant_gguf17")
+    return out
+
+
+def dequant_fp8(codes, scales, e8m0=False):
+    _need(codes, torch.uint8, "codes", 2)
+    n, k = codes.shape
+    if e8m0:
+        _need(scales, torch.uint8, "scales", 2)
+        want = ((n + 31) // 32, k // 32)
+    else:
+        _need(scales, torch.float32, "scales", 2)
+        want = ((n + 127) // 128, (k + 127) // 128)
+    if tuple(scales.shape) != want:
+        raise ValueError(f"scales must be {want}, got {tuple(scales.shape)}")
+    out = torch.empty((n, k), dtype=torch.float32, device=codes.device)
+    _lib.check(_lib.load().stbl_amd_dequant_fp8(_ptr(out), _ptr(codes), _ptr(scales), n, k, int(e8m0), _stream()),
+               "dequant_fp8")
+    return out
+
+
+def act_quant(x, block_size=128, pow2=True, want_deq=False):
+    """ref/kernel.py:35-45 on bf16 x [..., n]: (codes uint8 [..., n], fp32 scales [..., n/block]);
+    with want_deq also the in-place form bf16(e4m3 * s)."""
+    _need(x, torch.bfloat16, "x")
+    n = x.shape[-1]
+    rows = x.numel() // n
+    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    scales = torch.empty((*x.shape[:-1], n // block_size), dtype=torch.float32, device=x.device)
+    deq = torch.empty_like(x) if want_deq else None
+    _lib.check(_lib.load().stbl_amd_act_quant(_ptr(x), rows, n, block_size, int(pow2), _ptr(codes), _ptr(scales),
+                                              _ptr(deq), _stream()), "act_quant")
+    return (codes, scales, deq) if want_deq else (codes, scales)
+
+
+# ---- GEMV ---------------------------------------------------------------------------------------------
+
+def gemv_fp4(codes, scales, x, out_f32=False, out=None):
+    """y [M, N] = x [M, K] . (e2m1(codes) * 2^(scales-127))^T, M <= 4; bf16 (or fp32) output."""
+    _need(codes, torch.uint8, "codes", 2)
+    _need(scales, torch.uint8, "scales", 2)
+    _need(x, torch.bfloat16, "x")
+    x2 = _rows2(x)
+    n, k = codes.shape[0], codes.shape[1] * 2
+    m = x2.shape[0]
+    if x2.shape[1] != k or tuple(scales.shape) != (n, k // 32):
+        raise ValueError(f"shape mismatch: codes {tuple(codes.shape)}, scales {tuple(scales.shape)}, x {tuple(x.shape)}")
+    y = out if out is not None else torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16,
+                                                device=codes.device)
+    _lib.check(_lib.load().stbl_amd_gemv_fp4(_ptr(y), _ptr(codes), _ptr(scales), _ptr(x2), m, n, k, int(out_f32),
+                                             _stream()), "gemv_fp4")
+    return y
+
+
+def gemv_fp8(codes, scales, x, out_f32=False, out=None):
+    """y [M, N] = x [M, K] . (e4m3(codes) * scales[r/128][k/128])^T, M <= 4; bf16 (or fp32) output."""
+    _need(codes, torch.uint8, "codes", 2)
+    _need(scales, torch.float32, "scales", 2)
+    _need(x, torch.bfloat16, "x")
+    x2 = _rows2(x)
+    n, k = codes.shape
+    m = x2.shape[0]
+    if x2.shape[1] != k or tuple(scales.shape) != ((n + 127) // 128, (k + 127) // 128):
+        raise ValueError(f"shape mismatch: codes {tuple(codes.shape)}, scales {tuple(scales.shape)}, x {tuple(x.shape)}")
+    y = out if out is not None else torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16,
+                                                device=codes.device)
+    _lib.check(_lib.load().stbl_amd_gemv_fp8(_ptr(y), _ptr(codes), _ptr(scales), _ptr(x2), m, n, k, int(out_f32),
+                                             _stream()), "gemv_fp8")
+    return y
+
+
+# ---- the reference engine's operator surface (stbl/kernels.h), fp32 activation buffers ---------------
+
+def stbl_act_quant_fp8(x):
+    _need(x, torch.float32, "x")
+    _lib.load().stbl_act_quant_fp8(_ptr(x), x.numel(), _stream())
+    _lib.check(None, "stbl_act_quant_fp8")
+    return x
+
+
+def stbl_round_bf16(x):
+    _need(x, torch.float32, "x")
+    _lib.load().stbl_round_bf16(_ptr(x), x.numel(), _stream())
+    _lib.check(None, "stbl_round_bf16")
+    return x
+
+
+def stbl_gemv_fp8(y, w, scale, x, rows, k, round_out):
+    _need(y, torch.float32, "y")
+    _need(w, torch.uint8, "w")
+    _need(scale, torch.uint8, "scale")
+    _need(x, torch.float32, "x")
+    if y.numel() < rows or w.numel() != rows * k or x.numel() < k or scale.numel() != ((rows + 31) // 32) * (k // 32):
+        raise ValueError("stbl_gemv_fp8: buffer sizes do not match rows/k")
+    _lib.load().stbl_gemv_fp8(_ptr(y), _ptr(w), _ptr(scale), _ptr(x), rows, k, int(round_out), _stream())
+    _lib.check(None, "stbl_gemv_fp8")
+    return y
+
+
+def stbl_gemv_mxfp4(y, w, x, rows, k):
+    return stbl_gemv_mxfp4_batch([y], [w], [x], rows, k)
+
+
+def stbl_gemv_mxfp4_batch(ys, ws, xs, rows, k):
+    n = len(ys)
+    if not (len(ws) == n == len(xs)) or n == 0 or n > 16:
+        raise ValueError("stbl_gemv_mxfp4_batch: need 1..16 matching y/w/x tensors")
+    for y, w, x in zip(ys, ws, xs):
+        _need(y, torch.float32, "y")
+        _need(w, torch.uint8, "w")
+        _need(x, torch.float32, "x")
+        if y.numel() < rows or w.numel() != rows * (k // 32) * 17 or x.numel() < k:
+            raise ValueError("stbl_gemv_mxfp4_batch: buffer sizes do not match rows/k")
+    arr = ctypes.c_void_p * n
+    _lib.load().stbl_gemv_mxfp4_batch(arr(*[y.data_ptr() for y in ys]), arr(*[w.data_ptr() for w in ws]),
+                                      arr(*[x.data_ptr() for x in xs]), n, rows, k, _stream())
+    _lib.check(None, "stbl_gemv_mxfp4_batch")
+    return ys
+
+
+def stbl_swiglu(out, g, u, weight, limit, n):
+    return stbl_swiglu_batch(out, g, u, [weight], limit, n)
+
+
+def stbl_swiglu_batch(out, g, u, weights, limit, n):
+    count = len(weights)
+    for t, nm in ((out, "out"), (g, "g"), (u, "u")):
+        _need(t, torch.float32, nm)
+        if t.numel() < count * n:
+            raise ValueError(f"{nm} holds fewer than count * n values")
+    w = (ctypes.c_float * count)(*weights)
+    _lib.load().stbl_swiglu_batch(_ptr(out), _ptr(g), _ptr(u), w, count, float(limit), n, _stream())
+    _lib.check(None, "stbl_swiglu_batch")
+    return out
+
+
+def stbl_axpy(y, x, a, n):
+    _need(y, torch.float32, "y")
+    _need(x, torch.float32, "x")
+    if y.numel() < n or x.numel() < n:
+        raise ValueError("stbl_axpy: buffers shorter than n")
+    _lib.load().stbl_axpy(_ptr(y), _ptr(x), float(a), n, _stream())
+    _lib.check(None, "stbl_axpy")
+    return y

@@ -1,0 +1,70 @@
+"""The C-ABI library without a GPU: it loads, exports every function include/stbl_amd.h declares,
+the ctypes table covers exactly that list, and argument checks fail before any device call."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from stblarge_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    src = ""
+    for name in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if name.endswith(".h"):
+            src += open(os.path.join(ROOT, "include", name)).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return set(re.findall(r"^\s*(?:void|int|void\s*\*|uint64_t|const\s+char\s*\*)\s*\**\s*(stbl_\w+)\s*\(", src, re.M))
+
+
+def test_library_exists():
+    assert os.path.exists(_lib.LIB_PATH), "build the library first: python -m stblarge_amd.build"
+
+
+def test_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    declared = header_functions()
+    assert len(declared) >= 15
+    missing = [n for n in sorted(declared) if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_ctypes_table_matches_header():
+    assert set(_lib.SIGNATURES) == header_functions()
+
+
+def test_load_binds_all():
+    lib = _lib.load()
+    assert lib.stbl_amd_version() >= 1
+
+
+def test_argument_checks_fail_without_touching_the_device():
+    lib = _lib.load()
+    _lib.last_error()  # clear
+    P = ctypes.c_void_p
+    # k not a multiple of 32
+    st = lib.stbl_amd_gemv_fp4(P(16), P(16), P(16), P(16), 1, 8, 33, 0, None)
+    assert st < 0
+    code, msg = _lib.last_error()
+    assert code != 0 and "k % 32" in msg
+    # m out of range
+    assert lib.stbl_amd_gemv_fp8(P(16), P(16), P(16), P(16), 5, 8, 64, 0, None) < 0
+    assert "m must be" in _lib.last_error()[1]
+    # misaligned codes
+    assert lib.stbl_amd_gemv_fp4(P(16), P(17), P(16), P(16), 1, 8, 64, 0, None) < 0
+    assert "aligned" in _lib.last_error()[1]
+    # void reference entry point records its failure
+    lib.stbl_gemv_mxfp4(P(16), P(16), P(16), 8, 100, None)
+    code, msg = _lib.last_error()
+    assert code != 0 and "stbl_gemv_mxfp4" in msg
+    assert _lib.last_error() == (0, "")
+
+
+def test_check_raises():
+    lib = _lib.load()
+    with pytest.raises(_lib.StblError):
+        _lib.check(lib.stbl_amd_quant_fp4(None, None, None, 1, 32, None), "quant_fp4")

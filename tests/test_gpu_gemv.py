@@ -1,0 +1,135 @@
+"""GPU parity of the quantized GEMVs against the oracle (ref/kernel.py:85-102, stbl/kernels.cu:92-191).
+
+The bar: fp32 outputs within 1e-3 normwise relative error of the oracle's exact-product double sum
+(the GPU sums in a different order, so a few ulp of fp32); bf16 outputs at most one bf16 step from
+bf16(oracle), with flips rare. The weights are seeded N(0, 0.02) quantized by the GPU quantizers,
+which test_gpu_quant.py pins bit-exactly to the oracle's.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from stblarge_amd import data, ops
+from util import assert_gemv, np_
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(8, 32), (13, 96), (64, 2048), (100, 2080), (2048, 7168), (7168, 2048)]
+
+
+def _fp4(gpu, rows, k, seed):
+    w = data.weight(rows, k, seed)
+    codes, scales = oracle.quant_fp4(w.numpy())
+    return codes, scales, torch.from_numpy(codes).to(gpu), torch.from_numpy(scales).to(gpu)
+
+
+def _fp8(gpu, rows, k, seed):
+    w = data.weight(rows, k, seed)
+    codes, scales = oracle.quant_fp8_b128(w.numpy())
+    return codes, scales, torch.from_numpy(codes).to(gpu), torch.from_numpy(scales).to(gpu)
+
+
+@pytest.mark.parametrize("rows,k", SHAPES)
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_gemv_fp4(gpu, rows, k, m):
+    if m > 1 and rows * k > 2048 * 7168 // 4:
+        m = 4 if m == 4 else 1  # full shapes: M = 1 and 4 only (oracle time)
+    codes, scales, dc, ds = _fp4(gpu, rows, k, seed=rows * 31 + k)
+    x = data.activation(m, k, seed=m + k)
+    want = oracle.gemv_fp4(codes, scales, x.float().numpy())
+    y32 = ops.gemv_fp4(dc, ds, x.to(gpu), out_f32=True)
+    y16 = ops.gemv_fp4(dc, ds, x.to(gpu))
+    assert tuple(y16.shape) == (m, rows) and y16.dtype == torch.bfloat16
+    assert_gemv(np_(y32), np_(y16), want)
+
+
+@pytest.mark.parametrize("rows,k", SHAPES)
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_gemv_fp8(gpu, rows, k, m):
+    if m > 1 and rows * k > 2048 * 7168 // 4:
+        m = 4 if m == 4 else 1
+    codes, scales, dc, ds = _fp8(gpu, rows, k, seed=rows * 17 + k)
+    x = data.activation(m, k, seed=2 * m + k)
+    want = oracle.gemv_fp8_b128(codes, scales, x.float().numpy())
+    y32 = ops.gemv_fp8(dc, ds, x.to(gpu), out_f32=True)
+    y16 = ops.gemv_fp8(dc, ds, x.to(gpu))
+    assert_gemv(np_(y32), np_(y16), want)
+
+
+def test_gemv_official_mode(gpu):
+    # the reference engine quantizes the activation first (stbl/model.cu:236-242): act_quant per 32
+    # then the GEMV on the dequantized activation
+    rows, k = 2048, 7168
+    codes, scales, dc, ds = _fp4(gpu, rows, k, seed=5)
+    x = data.activation(1, k, seed=6)
+    _, _, xq = ops.act_quant(x.to(gpu), 32, True, want_deq=True)
+    xo = oracle.act_quant(x.float().numpy(), 32, True)[2]
+    assert np.array_equal(np_(xq), xo)
+    want = oracle.gemv_fp4(codes, scales, xo)
+    assert_gemv(np_(ops.gemv_fp4(dc, ds, xq, out_f32=True)), np_(ops.gemv_fp4(dc, ds, xq)), want)
+
+
+def test_gemv_fp4_zero_and_extreme_inputs(gpu):
+    rows, k = 64, 256
+    codes, scales, dc, ds = _fp4(gpu, rows, k, seed=9)
+    x = torch.zeros(1, k, dtype=torch.bfloat16)
+    assert float(ops.gemv_fp4(dc, ds, x.to(gpu), out_f32=True).abs().max()) == 0.0
+    x = data.activation(1, k, seed=10) * 1e30
+    want = oracle.gemv_fp4(codes, scales, x.float().numpy())
+    assert_gemv(np_(ops.gemv_fp4(dc, ds, x.to(gpu), out_f32=True)), None, want)
+
+
+# ---- the reference engine's ABI ------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,k,round_out", [(1000, 1280, 1), (2048, 7168, 0), (64, 96, 1)])
+def test_stbl_gemv_fp8_e8m0(gpu, rows, k, round_out):
+    # stbl/test_kernels.py:82-98 input idiom: e4m3 weights, E8M0 scales 2^U[-14,-7] per 32x32
+    rng = np.random.default_rng(rows)
+    w = np.clip(rng.standard_normal((rows, k)) * 100, -448, 448).astype(np.float32)
+    codes = oracle.e4m3_encode(w)
+    sc = rng.integers(127 - 14, 127 - 6, ((rows + 31) // 32, k // 32), dtype=np.uint8)
+    x = data.activation(1, k, seed=rows).float().numpy()[0]
+    xq = oracle.act_quant(x[None], 32, True)[2][0]
+    want = oracle.gemm(xq[None], oracle.dequant_fp8_e8m0_b32(codes, sc))[0]
+    y = torch.empty(rows, device=gpu)
+    ops.stbl_gemv_fp8(y, torch.from_numpy(codes).to(gpu), torch.from_numpy(sc).to(gpu), torch.from_numpy(xq).to(gpu),
+                      rows, k, round_out)
+    got = np_(y)
+    if round_out:
+        assert_gemv(got, got, want, tol=1e-2 / 4)
+    else:
+        assert_gemv(got, None, want)
+
+
+@pytest.mark.parametrize("rows,k", [(512, 2560), (2048, 7168), (7168, 2048)])
+def test_stbl_gemv_mxfp4_gguf(gpu, rows, k):
+    # stbl/test_kernels.py:101-117: random codes, scale bytes 118..125, repacked to GGUF blocks
+    rng = np.random.default_rng(k)
+    codes = rng.integers(0, 256, (rows, k // 2), dtype=np.uint8)
+    sc = rng.integers(118, 126, (rows, k // 32), dtype=np.uint8)
+    blocks = oracle.ocp_to_gguf17(codes, sc)
+    x = data.activation(1, k, seed=rows).float().numpy()[0]
+    want = oracle.gemv_fp4(codes, sc, x[None])[0]
+    y = torch.empty(rows, device=gpu)
+    ops.stbl_gemv_mxfp4(y, torch.from_numpy(blocks).to(gpu), torch.from_numpy(x).to(gpu), rows, k)
+    got = np_(y)
+    assert_gemv(got, got, want, tol=2.0 ** -8)
+
+
+def test_stbl_gemv_mxfp4_batch(gpu):
+    rows, k, n = 256, 1024, 16
+    rng = np.random.default_rng(3)
+    ys, ws, xs, wants = [], [], [], []
+    for j in range(n):
+        codes = rng.integers(0, 256, (rows, k // 2), dtype=np.uint8)
+        sc = rng.integers(118, 126, (rows, k // 32), dtype=np.uint8)
+        x = data.activation(1, k, seed=100 + j).float().numpy()[0]
+        wants.append(oracle.gemv_fp4(codes, sc, x[None])[0])
+        ws.append(torch.from_numpy(oracle.ocp_to_gguf17(codes, sc)).to(gpu))
+        xs.append(torch.from_numpy(x).to(gpu))
+        ys.append(torch.empty(rows, device=gpu))
+    ops.stbl_gemv_mxfp4_batch(ys, ws, xs, rows, k)
+    for y, want in zip(ys, wants):
+        assert_gemv(np_(y), np_(y), want, tol=2.0 ** -8)

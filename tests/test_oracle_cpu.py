@@ -1,0 +1,373 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it.
+
+Each oracle function is checked against (a) the golden vectors of tests/golden/golden.json, which
+restate the reference's own inline known-answer tests (ref/test_kernel.py:12-57) and the closed forms
+the path depends on, computed by exact rational arithmetic and brute force without the oracle, and
+(b) library routines that fix the same rounding (torch's float8/bfloat16 casts, numpy float64 matrix
+products). A few tests plant a plausible mistake in an oracle input and require that the golden
+vectors catch it.
+"""
+
+import base64
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+G = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "golden.json")))
+
+
+def hexf(s):
+    return float.fromhex(s)
+
+
+def b64(s, dtype):
+    return np.frombuffer(base64.b64decode(s), dtype=np.dtype(dtype).newbyteorder("<")).astype(dtype)
+
+
+def f32(vals):
+    return np.array(vals, dtype=np.float32)
+
+
+# ---- scalar codecs ---------------------------------------------------------------------------------
+
+def test_e4m3_decode_all_codes():
+    want = np.array([np.nan if v is None else hexf(v) for v in G["e4m3_table"]], np.float32)
+    got = oracle.e4m3_decode(np.arange(256))
+    assert np.array_equal(got, want, equal_nan=True)
+    # and as torch reads float8_e4m3fn bytes
+    lib = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(got, lib, equal_nan=True)
+
+
+def test_e4m3_encode_golden_rne():
+    for xh, code in G["e4m3_round"]:
+        assert oracle.e4m3_encode(f32([hexf(xh)]))[0] == code, xh
+
+
+def test_e4m3_encode_matches_torch_cast():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-4, 3, 20000),
+        np.linspace(-448, 448, 20001, dtype=np.float32),
+        f32([0.0, -0.0, 2.0 ** -10, -(2.0 ** -10), 2.0 ** -9, 3 * 2.0 ** -11, 2.0 ** -7 * 1.0625]),
+    ]).astype(np.float32)
+    x = np.clip(x, -448, 448)
+    got = oracle.e4m3_encode(x)
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(got, want)
+
+
+def test_pow2_ceil_kat():
+    # ref/test_kernel.py:12-15
+    for xh, wh in G["pow2_ceil"]:
+        assert oracle.pow2_ceil(f32([hexf(xh)]))[0] == np.float32(hexf(wh))
+
+
+def test_e2m1_table_and_codes():
+    tab = oracle.e2m1_table()
+    assert tab.tolist() == [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
+    assert np.array_equal(np.signbit(tab), np.arange(16) >= 8)
+    for c in range(16):
+        assert oracle.fp4_code(tab[c:c + 1])[0] == c
+
+
+def test_fp4_round_ties_to_even():
+    # ref/test_kernel.py:18-23 sweep, brute-forced in the fixture
+    x, want = b64(G["fp4_round"]["x"], np.float32), b64(G["fp4_round"]["want"], np.float32)
+    got = oracle.round_fp4(x)
+    assert np.array_equal(got, want)
+
+
+def test_e8m0_decode_matches_torch():
+    got = oracle.e8m0_decode(np.arange(256))
+    want = torch.arange(256, dtype=torch.uint8).view(torch.float8_e8m0fnu).float().numpy()
+    assert np.array_equal(got, want, equal_nan=True)
+
+
+def test_bf16_round_matches_torch():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(100000) * 10.0 ** rng.integers(-30, 30, 100000)).astype(np.float32)
+    x = np.concatenate([x, f32([0.0, -0.0, np.inf, -np.inf, 1 + 2 ** -8, 1 + 3 * 2 ** -8, 3.0e38])])
+    got = oracle.bf16_round(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(got, want)
+
+
+# ---- act_quant / weight quantizers ---------------------------------------------------------------
+
+def test_act_quant_golden():
+    # ref/test_kernel.py:26-35 closed form, act_quant(x, 32, "ue8m0")
+    a = G["act_quant"]
+    x = f32([hexf(v) for v in a["x"]]).reshape(a["rows"], a["n"])
+    codes, scales, deq = oracle.act_quant(x, a["block"], True)
+    assert np.array_equal(scales.ravel(), f32([hexf(v) for v in a["scales"]]))
+    assert codes.ravel().tolist() == a["codes"]
+    assert np.array_equal(deq.ravel(), f32([hexf(v) for v in a["deq"]]))
+
+
+def test_act_quant_block128_non_pow2_matches_torch_casts():
+    # scale_fmt=None path: s = amax * fp32(1/448), y = e4m3(clamp(x / s)); restated with torch casts
+    rng = np.random.default_rng(2)
+    x = torch.from_numpy((rng.standard_normal((4, 512)) * 3).astype(np.float32)).to(torch.bfloat16).float()
+    codes, scales, _ = oracle.act_quant(x.numpy(), 128, False)
+    xf = x.view(4, 4, 128)
+    amax = xf.abs().amax(-1).clamp_min(1e-4)
+    s = amax * torch.tensor(1.0 / 448.0, dtype=torch.float32)
+    y = (xf / s.unsqueeze(-1)).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+    assert np.array_equal(scales, s.numpy())
+    assert np.array_equal(codes, y.view(4, 512).numpy())
+
+
+def test_quant_fp4_golden():
+    q = G["quant_fp4"]
+    w = f32([hexf(v) for v in q["w"]]).reshape(q["rows"], q["k"])
+    codes, scales = oracle.quant_fp4(w)
+    assert codes.ravel().tolist() == q["codes"]
+    assert scales.ravel().tolist() == q["scales"]
+
+
+def test_quant_fp4_roundtrip_bound():
+    # every value lands on the grid point nearest to w/s: |deq - w| <= s * half step
+    w = np.random.default_rng(3).standard_normal((8, 256)).astype(np.float32) * np.float32(0.02)
+    codes, scales = oracle.quant_fp4(w)
+    deq = oracle.dequant_fp4(codes, scales)
+    s = np.repeat(oracle.e8m0_decode(scales), 32, axis=1)
+    half = np.where(np.abs(deq / s) < 2, 0.25, np.where(np.abs(deq / s) < 4, 0.5, 1.0))
+    assert np.all(np.abs(deq - w) <= s * half + 1e-12)
+
+
+def test_quant_fp8_b128_golden():
+    q = G["quant_fp8_b128"]
+    w = b64(q["w"], np.float32).reshape(q["rows"], q["k"])
+    codes, scales = oracle.quant_fp8_b128(w)
+    assert np.array_equal(codes.ravel(), b64(q["codes"], np.uint8))
+    assert np.array_equal(scales.ravel(), b64(q["scales"], np.float32))
+
+
+# ---- dequant / layouts / GEMV ----------------------------------------------------------------------
+
+def _gemv_fp4_case():
+    g = G["gemv_fp4"]
+    n, k, m = g["n"], g["k"], g["m"]
+    codes = np.array(g["codes"], np.uint8).reshape(n, k // 2)
+    scales = np.array(g["scales"], np.uint8).reshape(n, k // 32)
+    x = f32([hexf(v) for v in g["x"]]).reshape(m, k)
+    y = np.array([hexf(v) for v in g["y"]]).reshape(m, n)
+    return codes, scales, x, y
+
+
+def test_gemv_fp4_exact_golden():
+    codes, scales, x, y = _gemv_fp4_case()
+    assert np.array_equal(oracle.gemv_fp4(codes, scales, x), y)  # exact: products and sums fit double
+    deq = oracle.dequant_fp4(codes, scales)
+    assert np.array_equal(oracle.gemm(x, deq), y)
+
+
+def test_gemv_fp4_catches_swapped_nibbles():
+    codes, scales, x, y = _gemv_fp4_case()
+    swapped = ((codes >> 4) | (codes << 4)).astype(np.uint8)
+    assert not np.array_equal(oracle.gemv_fp4(swapped, scales, x), y)
+
+
+def test_gguf17_repack_and_dequant():
+    codes, scales, x, y = _gemv_fp4_case()
+    blocks = oracle.ocp_to_gguf17(codes, scales)
+    assert blocks.ravel().tolist() == G["gguf17"]
+    n, k = codes.shape[0], codes.shape[1] * 2
+    assert np.array_equal(oracle.dequant_gguf17(blocks, n, k), oracle.dequant_fp4(codes, scales))
+
+
+def test_dequant_fp4_matches_torch_formula():
+    # ref/kernel.py:98-101 evaluated with torch: table[nibble] * e8m0 scale, one fp32 product
+    rng = np.random.default_rng(4)
+    codes = rng.integers(0, 256, (16, 64), dtype=np.uint8)
+    scales = rng.integers(100, 140, (16, 4), dtype=np.uint8)
+    scales[0, 0], scales[1, 1] = 0, 254
+    raw = torch.from_numpy(codes)
+    table = torch.tensor(oracle.e2m1_table())
+    vals = torch.stack([table[(raw & 15).long()], table[(raw >> 4).long()]], -1).view(16, 128)
+    sc = torch.from_numpy(scales).view(torch.float8_e8m0fnu).float()
+    want = (vals.view(16, 4, 32) * sc.view(16, 4, 1)).view(16, 128).numpy()
+    assert np.array_equal(oracle.dequant_fp4(codes, scales), want)
+
+
+def test_dequant_fp8_matches_torch_formula():
+    rng = np.random.default_rng(5)
+    codes = rng.integers(0, 256, (130, 260), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0  # no NaN codes (the quantizer never writes them)
+    scales = rng.random((2, 3)).astype(np.float32) * np.float32(0.01)
+    b = torch.from_numpy(codes).view(torch.float8_e4m3fn)
+    sb = torch.from_numpy(scales).repeat_interleave(128, 0)[:130].repeat_interleave(128, 1)[:, :260]
+    want = (b.float() * sb).numpy()  # ref/kernel.py:89-90
+    assert np.array_equal(oracle.dequant_fp8_b128(codes, scales), want)
+    e8 = rng.integers(110, 130, (5, 8), dtype=np.uint8)
+    c2 = codes[:130, :256]
+    s2 = torch.from_numpy(e8).view(torch.float8_e8m0fnu).float().repeat_interleave(32, 0)[:130].repeat_interleave(32, 1)
+    want2 = (torch.from_numpy(np.ascontiguousarray(c2)).view(torch.float8_e4m3fn).float() * s2).numpy()
+    assert np.array_equal(oracle.dequant_fp8_e8m0_b32(c2, e8), want2)
+
+
+def test_gemv_fp8_b128_exact_golden():
+    q = G["quant_fp8_b128"]
+    codes = b64(q["codes"], np.uint8).reshape(q["rows"], q["k"])
+    scales = b64(q["scales"], np.float32).reshape(2, 3)
+    x = b64(G["gemv_fp8_b128"]["x"], np.float32)
+    y = np.array([hexf(v) for v in G["gemv_fp8_b128"]["y"]])
+    got = oracle.gemv_fp8_b128(codes, scales, x)[0]
+    # exact products summed in double: differs from the exact rational sum by double rounding only
+    assert np.max(np.abs(got - y)) <= 1e-12 * np.max(np.abs(y))
+
+
+def test_gemm_matches_numpy():
+    rng = np.random.default_rng(6)
+    a = rng.standard_normal((3, 100)).astype(np.float32)
+    w = rng.standard_normal((7, 100)).astype(np.float32)
+    want = a.astype(np.float64) @ w.astype(np.float64).T
+    assert np.allclose(oracle.gemm(a, w), want, rtol=1e-13, atol=1e-13)
+
+
+def test_fp8_gemm_brute_force():
+    # ref/test_kernel.py:48-57: act_quant(a, 32, ue8m0) then fp8_gemm with 2^-3 weight scales
+    rng = np.random.default_rng(7)
+    a = torch.from_numpy(rng.standard_normal((5, 64)).astype(np.float32)).to(torch.bfloat16).float().numpy()
+    b = rng.standard_normal((40, 64)).astype(np.float32)
+    aq, as_, _ = oracle.act_quant(a, 32, True)
+    bq = oracle.e4m3_encode(np.clip(b * 8, -448, 448))
+    A = (oracle.e4m3_decode(aq).reshape(5, 2, 32) * as_[..., None]).reshape(5, 64)
+    got = oracle.gemm(A, oracle.e4m3_decode(bq) * np.float32(2.0 ** -3))
+    want = A.astype(np.float64) @ (oracle.e4m3_decode(bq).astype(np.float64) * 2.0 ** -3).T
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+# ---- epilogues / router ------------------------------------------------------------------------------
+
+def test_swiglu_golden():
+    for gh, uh, wh, lim, oh in G["swiglu"]:
+        got = oracle.swiglu(f32([hexf(gh)]), f32([hexf(uh)]), hexf(wh), lim)[0]
+        assert got == np.float32(hexf(oh)), (gh, uh)
+
+
+def test_swiglu_matches_torch_silu():
+    # stbl/test_kernels.py:200-207: (w * (silu(clamp(g, max=10)) * clamp(u, +-10))).to(bf16), tol 1e-2
+    rng = np.random.default_rng(8)
+    g = torch.from_numpy((rng.standard_normal(2304) * 4).astype(np.float32)).to(torch.bfloat16).float()
+    u = torch.from_numpy((rng.standard_normal(2304) * 4).astype(np.float32)).to(torch.bfloat16).float()
+    want = (0.37 * (torch.nn.functional.silu(g.clamp(max=10.0)) * u.clamp(-10, 10))).to(torch.bfloat16).float()
+    got = oracle.swiglu(g.numpy(), u.numpy(), 0.37, 10.0)
+    assert np.max(np.abs(got - want.numpy())) <= 1e-2 * np.max(np.abs(want.numpy()))
+
+
+def test_route_golden():
+    r = G["route"]
+    logits = f32([hexf(v) for v in r["logits"]]).reshape(r["t"], r["e"])
+    _, ids, w = oracle.route(logits, r["topk"])
+    assert ids.tolist() == r["ids"]
+    # the fixture's sigmoid used numpy's float32 exp, the oracle libm's expf: both faithful, so the
+    # weights may differ in the last bit or two
+    want = f32([[hexf(v) for v in row] for row in r["weights"]])
+    assert np.allclose(w, want, rtol=4 * 2.0 ** -24, atol=0)
+
+
+def test_route_bias_and_scale():
+    logits = f32([[0.0, 1.0, 2.0, 3.0]])
+    bias = f32([10.0, 0.0, 0.0, 0.0])
+    _, ids, w = oracle.route(logits, 2, bias=bias, route_scale=2.5)
+    assert ids.tolist() == [[0, 3]]  # the bias selects, the unbiased score weighs
+    s = 1 / (1 + np.exp(-np.array([0.0, 3.0], np.float32)))
+    assert np.allclose(w[0], s / s.sum() * 2.5, rtol=1e-6)
+
+
+# ---- expert FFN / MoE composition ----------------------------------------------------------------------
+
+def _fp4_slot(rng, dim, inter):
+    parts = []
+    mats = []
+    for rows, k in ((inter, dim), (inter, dim), (dim, inter)):
+        w = rng.standard_normal((rows, k)).astype(np.float32) * np.float32(0.02)
+        c, s = oracle.quant_fp4(w)
+        parts += [c.ravel(), s.ravel()]
+        mats.append(oracle.dequant_fp4(c, s))
+    return np.concatenate(parts), mats
+
+
+def _ffn_numpy(mats, x, w, official):
+    """stbl/model.cu:536-539 composition with dense float64 products: g, u rounded to bf16, SwiGLU
+    with the route weight, optional act_quant of the input and of the SwiGLU output, bf16 output."""
+    wg, wu, wd = mats
+    if official:
+        x = oracle.act_quant(x[None], 32, True)[2][0]
+    g = oracle.bf16_round((wg.astype(np.float64) @ x.astype(np.float64)).astype(np.float32))
+    u = oracle.bf16_round((wu.astype(np.float64) @ x.astype(np.float64)).astype(np.float32))
+    gt = torch.from_numpy(g)
+    h = ((gt / (1 + torch.exp(-gt))) * torch.from_numpy(u) * w).to(torch.bfloat16).float().numpy()
+    if official:
+        h = oracle.act_quant(h[None], 32, True)[2][0]
+    return oracle.bf16_round((wd.astype(np.float64) @ h.astype(np.float64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("official", [False, True])
+def test_expert_ffn_fp4_composition(official):
+    rng = np.random.default_rng(9)
+    dim, inter = 256, 128
+    slot, mats = _fp4_slot(rng, dim, inter)
+    x = oracle.bf16_round(rng.standard_normal(dim).astype(np.float32))
+    got = oracle.expert_ffn_fp4(slot, dim, inter, x, 0.7, 0.0, official)
+    want = _ffn_numpy(mats, x, 0.7, official)
+    # bf16 outputs of the same exact products: at most one bf16 step apart (summation order only)
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-30)
+    assert np.mean(got == want) > 0.9
+
+
+def test_moe_fp4_sum_order():
+    rng = np.random.default_rng(10)
+    dim, inter, topk = 128, 64, 3
+    slots = [_fp4_slot(rng, dim, inter) for _ in range(4)]
+    x = oracle.bf16_round(rng.standard_normal((2, dim)).astype(np.float32))
+    picks = [[0, 2, 1], [3, 0, 2]]
+    wts = np.array([[0.5, 0.3, 0.2], [0.6, 0.25, 0.15]], np.float32)
+    y = oracle.moe_fp4([[slots[e][0] for e in row] for row in picks], wts, slots[3][0], dim, inter, x)
+    for t in range(2):
+        acc = np.zeros(dim, np.float32)
+        for p, e in enumerate(picks[t]):
+            acc = acc + oracle.expert_ffn_fp4(slots[e][0], dim, inter, x[t], wts[t, p])
+        acc = acc + oracle.expert_ffn_fp4(slots[3][0], dim, inter, x[t], 1.0)
+        assert np.array_equal(y[t], oracle.bf16_round(acc))
+
+
+# ---- expert LRU bookkeeping ------------------------------------------------------------------------------
+
+def test_lru_simulate_hand_case():
+    # 2 slots. step 1: 1, 2 miss into slots 0, 1. step 2: 2 hit; 3 misses and evicts 1 (LRU).
+    # step 3: ids 1, 3: 3 is touched first, so 1's miss evicts 2, not 3.
+    out = oracle.lru_simulate([[1, 2], [2, 3], [1, 3]], 2)
+    assert out[0] == ([False, False], [0, 1], [])
+    assert out[1] == ([True, False], [1, 0], [1])
+    assert out[2] == ([False, True], [1, 0], [2])
+
+
+def test_lru_simulate_brute_force():
+    rng = np.random.default_rng(11)
+    steps = [list(rng.choice(12, size=3, replace=False)) for _ in range(200)]
+    out = oracle.lru_simulate(steps, 5)
+    last_use, cached = {}, set()
+    clock = 0
+    for ids, (hits, _, _) in zip(steps, out):
+        clock += 1
+        for e in ids:
+            if e in cached:
+                last_use[e] = clock  # touched before any miss of this step
+        for e, hit in zip(ids, hits):
+            assert hit == (e in cached)
+            clock += 1
+            if not hit:
+                if len(cached) == 5:
+                    victim = min(cached, key=lambda v: last_use[v])
+                    cached.remove(victim)
+                cached.add(e)
+            last_use[e] = clock

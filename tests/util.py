@@ -1,0 +1,51 @@
+"""Comparison helpers shared by the GPU parity tests."""
+
+import numpy as np
+import torch
+
+import oracle
+
+
+def np_(t):
+    """Device/host tensor -> numpy (bf16 widened to fp32)."""
+    t = t.detach().cpu()
+    if t.dtype == torch.bfloat16:
+        t = t.float()
+    return t.numpy()
+
+
+def bits_equal(got, want):
+    """Bit-identical fp32 arrays (NaNs compared by position only)."""
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    gn, wn = np.isnan(got), np.isnan(want)
+    if not np.array_equal(gn, wn):
+        return False
+    return np.array_equal(got[~gn].view(np.uint32), want[~wn].view(np.uint32))
+
+
+def rel_err(got, want):
+    """max |got - want| / max |want| -- the reference's check() metric (stbl/test_kernels.py:47-52)."""
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want)) / max(float(np.max(np.abs(want))), 1e-30))
+
+
+def bf16_ulps(got_bf16, want_f64):
+    """Per element, how many bf16 steps the bf16 result is from bf16(want) (0 = same rounding)."""
+    want = oracle.f2bf_bits(np.asarray(want_f64, np.float32)).astype(np.int32)
+    got = oracle.f2bf_bits(np.asarray(got_bf16, np.float32)).astype(np.int32)
+
+    def ordered(b):  # sign-magnitude bf16 bits -> monotone integers
+        return np.where(b & 0x8000, -(b & 0x7FFF), b & 0x7FFF)
+
+    return np.abs(ordered(got) - ordered(want))
+
+
+def assert_gemv(got_f32, got_bf16, want, tol=1e-3):
+    """fp32 output within `tol` (normwise), bf16 output at most one bf16 step from bf16(want)."""
+    e = rel_err(got_f32, want)
+    assert e <= tol, f"relative error {e:.3e} > {tol}"
+    if got_bf16 is not None:
+        u = bf16_ulps(got_bf16, want)
+        assert u.max() <= 1, f"bf16 output {u.max()} steps away"
+        assert np.mean(u) < 0.05, f"{np.mean(u):.3f} of bf16 outputs flipped"
+    return e
