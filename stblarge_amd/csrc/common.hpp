@@ -24,11 +24,11 @@ constexpr int kWave = 64;
 
 // ---- bf16 <-> fp32 -------------------------------------------------------------------------------
 
-__host__ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+__host__ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __builtin_bit_cast(float, h << 16); }
 
 // Round to nearest even; a NaN stays a (quiet) NaN.
 __host__ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
     if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
     u += 0x7fffu + ((u >> 16) & 1u);
     return (uint16_t)(u >> 16);
@@ -125,6 +125,21 @@ __device__ __forceinline__ float wave_sum(float v) {
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Sum over the 64 lanes of a wave with DPP data movement only (no LDS crossbar): pairs, quads,
+// half rows, rows, then the row broadcasts. The total is valid in lane 63.
+__device__ __forceinline__ float dpp_sum(float v) {
+#define STBL_DPP_ADD(ctrl, rmask) \
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, rmask, 0xF, false))
+    STBL_DPP_ADD(0xB1, 0xF);   // quad_perm [1,0,3,2]
+    STBL_DPP_ADD(0x4E, 0xF);   // quad_perm [2,3,0,1]
+    STBL_DPP_ADD(0x141, 0xF);  // row_half_mirror
+    STBL_DPP_ADD(0x140, 0xF);  // row_mirror
+    STBL_DPP_ADD(0x142, 0xA);  // row_bcast:15 into rows 1 and 3
+    STBL_DPP_ADD(0x143, 0xC);  // row_bcast:31 into rows 2 and 3
+#undef STBL_DPP_ADD
     return v;
 }
 
