@@ -110,6 +110,80 @@ int stbl_amd_dequant_gguf17(float *out, const void *w, int rows, int k, hipStrea
 int stbl_amd_dequant_fp8(float *out, const void *codes, const void *scales, int rows, int k, int scale_e8m0,
                          hipStream_t st);
 
+/* ---- v2: expert FFN and routed MoE (stbl/model.cu:426-594 composition) ------------------------------ */
+
+/* Weight formats of an expert slot. */
+enum { STBL_AMD_FP4 = 0, STBL_AMD_FP8 = 1 };
+
+/* Byte layout of one expert slot: gate [inter x dim], up [inter x dim], down [dim x inter], each as
+ * codes then scales (FP4: codes [rows][k/2] + E8M0 [rows][k/32]; FP8: codes [rows][k] + fp32
+ * [ceil(rows/128)][ceil(k/128)]), every part 256-byte aligned. Writes the six part offsets (may be
+ * NULL) and returns the slot size. Replaces the gate|up|down slot of stbl/model.cu:374-381. */
+uint64_t stbl_amd_expert_layout(int fmt, int dim, int inter, uint64_t *offsets);
+
+/* One expert FFN on m <= 4 tokens (stbl/model.cu:516-547 for one expert):
+ * y[t] = bf16(down . act(swiglu(bf16(gate . act(x_t)), bf16(up . act(x_t)), weight, limit)))
+ * where act is act_quant(., 32, ue8m0, inplace) when `official`, else the identity, and swiglu is
+ * stbl_swiglu's arithmetic. slot 256-byte aligned in the layout above; x bf16 [m][dim]; y bf16
+ * [m][dim] (fp32 holding the unrounded down product when y_f32); work >= m * inter * 2 bytes of
+ * device scratch. FP4 needs dim, inter % 32 == 0; FP8 % 128; K <= 16384 (FP4) / 8192 (FP8). */
+int stbl_amd_expert_ffn(int fmt, void *y, const void *slot, const void *x, int m, int dim, int inter, float weight,
+                        float limit, int official, int y_f32, void *work, hipStream_t st);
+
+/* A routed MoE layer's expert part over cached slots (stbl/model.cu:505-592): for every token t,
+ * y[t] = bf16(sum_p o(slot[pick[t][p]], weights[t][p]) + o(slot[shared], 1)) with the fp32 sum taken
+ * in top-k order from 0, each o an expert FFN output rounded to bf16 with the route weight applied
+ * inside SwiGLU. slots: HOST array of n_slots device pointers; pick [t][topk] (HOST) indexes it;
+ * weights [t][topk] (HOST); shared = slot index of the always-on expert or -1. t <= 16, topk <= 16.
+ * work: device scratch of stbl_amd_moe_work_bytes() bytes. */
+int stbl_amd_moe_experts(int fmt, void *y, const void *x, int t, int dim, int inter, const void *const *slots,
+                         int n_slots, const int *pick, const float *weights, int topk, int shared, float limit,
+                         int official, int y_f32, void *work, hipStream_t st);
+
+/* Scratch bytes for stbl_amd_moe_experts on t tokens. */
+uint64_t stbl_amd_moe_work_bytes(int t, int topk, int dim, int inter);
+
+/* Router on the device (stbl/model.cu:430-452 with sigmoid scores as the configuration asks):
+ * score = 1 / (1 + exp(-logit)); ids = top-k of score + bias (bias may be NULL), ties to the lower
+ * id, in descending order; weights = score / (sum of the top-k scores in order + 1e-20) *
+ * route_scale. logits fp32 [t][n_exp], ids int32 [t][topk], weights fp32 [t][topk], scores fp32
+ * [t][n_exp] (optional). n_exp <= 1024, topk <= 32. */
+int stbl_amd_route(const float *logits, const float *bias, int t, int n_exp, int topk, float route_scale, int *ids,
+                   float *weights, float *scores, hipStream_t st);
+
+/* ---- v2: HBM expert cache (stbl/model.cu:99-106, 347-422 ExpertCache / expert() / take_slot) -------- */
+
+/* Creates an LRU cache of `slots` expert slots of slot_bytes on the current device (allocates the
+ * slots, a copy stream and events: the only allocating calls of this library). host_pool: pinned
+ * host memory holding n_layers * n_experts experts host_stride bytes apart, alive as long as the
+ * cache. Returns NULL on failure. */
+void *stbl_amd_cache_create(int slots, uint64_t slot_bytes, const void *host_pool, uint64_t host_stride, int n_experts,
+                            int n_layers);
+
+/* Frees the cache after its copies finished. */
+void stbl_amd_cache_destroy(void *cache);
+
+/* Looks up n expert ids (HOST array) of `layer` in order; cached experts of the lookup are touched
+ * first so that a miss never evicts one of them. slot_ptrs (HOST, n) receives each expert's slot,
+ * hit (HOST, optional) 1 for hits. Misses are copied from the host pool on the cache's copy stream
+ * and `compute` is made to wait for them (no host blocking). Returns the number of misses or a
+ * negative hipError_t; a failed refill leaves its slot unmapped. */
+int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **slot_ptrs, int *hit,
+                          hipStream_t compute);
+
+/* Marks the slots of the last lookup as used by the work queued so far on `compute`; a later refill
+ * of one of them waits for that work. */
+int stbl_amd_cache_mark_used(void *cache, hipStream_t compute);
+
+/* out[0..5] = hits, misses, refill bytes, lookups, slots in use, slots (stbl_stats, stbl/stbl.h:20). */
+int stbl_amd_cache_stats(void *cache, uint64_t *out);
+
+/* Slot of a cached expert without touching the LRU order, or NULL. */
+void *stbl_amd_cache_peek(void *cache, int layer, int expert);
+
+/* Test hook: the refill after n more refills fails on the host without copying (n = -1 disables). */
+int stbl_amd_cache_fail_refill_after(void *cache, int n);
+
 /* ---- library ------------------------------------------------------------------------------------------ */
 
 /* The calling thread's last failure: copies its message into buf (len bytes, may be NULL), clears

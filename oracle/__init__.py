@@ -255,21 +255,25 @@ def route(logits, topk=8, bias=None, route_scale=1.0):
     return scores, ids, weights
 
 
-def expert_ffn_fp4(slot, dim, inter, x, w=1.0, limit=0.0, official=False):
+def expert_ffn_fp4(slot, dim, inter, x, w=1.0, limit=0.0, official=False, raw=False):
+    """One FP4 expert on one token (stbl/model.cu:516-547). slot = the six parts packed back to back.
+    Returns o = bf16(down product); with raw=True also the down product before rounding (double)."""
     slot, x = _u8(slot), _f32(x)
     o = np.empty(dim, np.float32)
-    lib().orc_expert_ffn_fp4(_p(slot), I(dim), I(inter), _p(x), F(w), F(limit), I(int(official)), _p(o))
-    return o
+    r = np.empty(dim, np.float64) if raw else None
+    lib().orc_expert_ffn_fp4(_p(slot), I(dim), I(inter), _p(x), F(w), F(limit), I(int(official)), _p(o), _p(r))
+    return (o, r) if raw else o
 
 
-def expert_ffn_fp8(g, u, d, dim, inter, x, w=1.0, limit=0.0, official=False):
+def expert_ffn_fp8(g, u, d, dim, inter, x, w=1.0, limit=0.0, official=False, raw=False):
     """g, u, d = (codes, fp32 scales) of gate [inter][dim], up [inter][dim], down [dim][inter]."""
     (gc, gs), (uc, us), (dc, ds) = [(_u8(c), _f32(s)) for c, s in (g, u, d)]
     x = _f32(x)
     o = np.empty(dim, np.float32)
+    r = np.empty(dim, np.float64) if raw else None
     lib().orc_expert_ffn_fp8(_p(gc), _p(gs), _p(uc), _p(us), _p(dc), _p(ds), I(dim), I(inter), _p(x), F(w), F(limit),
-                             I(int(official)), _p(o))
-    return o
+                             I(int(official)), _p(o), _p(r))
+    return (o, r) if raw else o
 
 
 def moe_fp4(slots, weights, shared, dim, inter, x, limit=0.0, official=False):

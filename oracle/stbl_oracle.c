@@ -339,7 +339,7 @@ void orc_route(const float *logits, const float *bias, int t, int e, int topk, f
  * g = bf16(W1 x), u = bf16(W3 x), h = swiglu(g, u, w), h -> act_quant per 32 (pow2) when `official`,
  * o = bf16(W2 h). If act_in, x is act-quantized first (official linear()). o [dim]. */
 static void ffn_fp4_one(const uint8_t *slot, int dim, int inter, const float *x, float w, float lim, int official,
-                        float *o, float *xbuf, float *h, double *acc) {
+                        float *o, float *xbuf, float *h, double *acc, double *raw) {
     const size_t gc = (size_t)inter * dim / 2, gs = (size_t)inter * dim / 32;
     const uint8_t *gcodes = slot, *gsc = slot + gc, *ucodes = gsc + gs, *usc = ucodes + gc, *dcodes = usc + gs,
                   *dsc = dcodes + gc;
@@ -352,13 +352,15 @@ static void ffn_fp4_one(const uint8_t *slot, int dim, int inter, const float *x,
     if (official) orc_act_quant(h, 1, inter, 32, 1, NULL, NULL, h);
     orc_gemv_fp4(dcodes, dsc, h, 1, dim, inter, acc);
     for (int i = 0; i < dim; i++) o[i] = bf16r((float)acc[i]);
+    if (raw) memcpy(raw, acc, sizeof(double) * dim);
 }
 
+/* raw (may be NULL) receives the down product before its bf16 rounding. */
 void orc_expert_ffn_fp4(const uint8_t *slot, int dim, int inter, const float *x, float w, float lim, int official,
-                        float *o) {
+                        float *o, double *raw) {
     float *xbuf = malloc(sizeof(float) * dim), *h = malloc(sizeof(float) * inter);
     double *acc = malloc(sizeof(double) * (dim > inter ? dim : inter));
-    ffn_fp4_one(slot, dim, inter, x, w, lim, official, o, xbuf, h, acc);
+    ffn_fp4_one(slot, dim, inter, x, w, lim, official, o, xbuf, h, acc, raw);
     free(xbuf), free(h), free(acc);
 }
 
@@ -366,7 +368,7 @@ void orc_expert_ffn_fp4(const uint8_t *slot, int dim, int inter, const float *x,
  * separately per matrix. */
 void orc_expert_ffn_fp8(const uint8_t *gcodes, const float *gsc, const uint8_t *ucodes, const float *usc,
                         const uint8_t *dcodes, const float *dsc, int dim, int inter, const float *x, float w,
-                        float lim, int official, float *o) {
+                        float lim, int official, float *o, double *raw) {
     float *xbuf = malloc(sizeof(float) * dim), *h = malloc(sizeof(float) * inter);
     double *acc = malloc(sizeof(double) * (dim > inter ? dim : inter));
     if (official) orc_act_quant(x, 1, dim, 32, 1, NULL, NULL, xbuf);
@@ -378,6 +380,7 @@ void orc_expert_ffn_fp8(const uint8_t *gcodes, const float *gsc, const uint8_t *
     if (official) orc_act_quant(h, 1, inter, 32, 1, NULL, NULL, h);
     orc_gemv_fp8_b128(dcodes, dsc, h, 1, dim, inter, acc);
     for (int i = 0; i < dim; i++) o[i] = bf16r((float)acc[i]);
+    if (raw) memcpy(raw, acc, sizeof(double) * dim);
     free(xbuf), free(h), free(acc);
 }
 
@@ -396,7 +399,7 @@ void orc_moe_fp4(const uint8_t *const *slots, const float *weights, const uint8_
             const uint8_t *slot = p < topk ? slots[(size_t)i * topk + p] : shared;
             const float w = p < topk ? weights[(size_t)i * topk + p] : 1.f;
             if (!slot) continue;
-            ffn_fp4_one(slot, dim, inter, x + (size_t)i * dim, w, lim, official, o, xbuf, h, acc);
+            ffn_fp4_one(slot, dim, inter, x + (size_t)i * dim, w, lim, official, o, xbuf, h, acc, NULL);
             for (int c = 0; c < dim; c++) sum[c] += 1.f * o[c];
         }
         for (int c = 0; c < dim; c++) y[(size_t)i * dim + c] = bf16r(sum[c]);

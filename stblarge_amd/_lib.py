@@ -15,6 +15,9 @@ I = ctypes.c_int
 F = ctypes.c_float
 PP = ctypes.POINTER(ctypes.c_void_p)
 PF = ctypes.POINTER(ctypes.c_float)
+PI = ctypes.POINTER(ctypes.c_int)
+U64 = ctypes.c_uint64
+PU64 = ctypes.POINTER(ctypes.c_uint64)
 
 # name -> (restype, argtypes). Every function of include/stbl_amd.h appears here.
 SIGNATURES = {
@@ -36,6 +39,18 @@ SIGNATURES = {
     "stbl_amd_dequant_fp4": (I, [P, P, P, I, I, P]),
     "stbl_amd_dequant_gguf17": (I, [P, P, I, I, P]),
     "stbl_amd_dequant_fp8": (I, [P, P, P, I, I, I, P]),
+    "stbl_amd_expert_layout": (U64, [I, I, I, PU64]),
+    "stbl_amd_expert_ffn": (I, [I, P, P, P, I, I, I, F, F, I, I, P, P]),
+    "stbl_amd_moe_experts": (I, [I, P, P, I, I, I, PP, I, PI, PF, I, I, F, I, I, P, P]),
+    "stbl_amd_moe_work_bytes": (U64, [I, I, I, I]),
+    "stbl_amd_route": (I, [P, P, I, I, I, F, P, P, P, P]),
+    "stbl_amd_cache_create": (P, [I, U64, P, U64, I, I]),
+    "stbl_amd_cache_destroy": (None, [P]),
+    "stbl_amd_cache_lookup": (I, [P, PI, I, I, PP, PI, P]),
+    "stbl_amd_cache_mark_used": (I, [P, P]),
+    "stbl_amd_cache_stats": (I, [P, PU64]),
+    "stbl_amd_cache_peek": (P, [P, I, I]),
+    "stbl_amd_cache_fail_refill_after": (I, [P, I]),
     "stbl_amd_last_error": (I, [ctypes.c_char_p, I]),
     "stbl_amd_version": (I, []),
 }
@@ -53,6 +68,10 @@ def load():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise StblError(f"{LIB_PATH} is missing: build it with `python -m stblarge_amd.build`")
+        # torch first: its HIP runtime is then the one the library's HIP symbols bind to, so device
+        # memory, streams and graphs are shared with torch's (one runtime per process)
+        import torch  # noqa: F401
+
         lib = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)

@@ -17,123 +17,9 @@
 //   3. reduces each (token, row) partial over the 64 lanes with DPP moves only, and over the waves
 //      through LDS in wave order, so the result is the same on every run.
 #include "abi_util.hpp"
-#include "common.hpp"
+#include "gemv_core.hpp"
 
 namespace stbl {
-
-constexpr int kMaxWaves = 8;  // K <= 512 chunks: 16384 FP4 / 8192 FP8 elements
-constexpr int kMaxJobs = 16;  // matrices per launch (the reference's kMxBatch, stbl/kernels.h:18)
-
-enum class WFmt { FP4_OCP, FP4_GGUF, FP8_B128, FP8_E8M0 };
-
-template <WFmt F>
-struct WTraits {
-    static constexpr bool fp4 = F == WFmt::FP4_OCP || F == WFmt::FP4_GGUF;
-    static constexpr int CH = fp4 ? 32 : 16;  // elements per lane chunk
-};
-
-// One matrix of a launch: weights, scales, activations, output.
-struct GemvJob {
-    const uint8_t *w;
-    const void *s;
-    const void *x;
-    void *y;
-};
-struct GemvJobs {
-    GemvJob j[kMaxJobs];
-};
-
-enum OutMode { OUT_BF16 = 0, OUT_F32 = 1, OUT_F32_ROUNDED = 2 };
-
-// A GGUF block c of a row sits at byte 17 c, so it is only byte aligned: read the five dwords that
-// cover it from the enclosing 4-byte boundary (each dword starts inside the buffer, and a 4-byte
-// aligned dword never crosses a page) and realign with v_alignbyte.
-__device__ __forceinline__ void load_gguf_block(const uint8_t *blk, uint32_t &scale, u32x4 &codes) {
-    const uintptr_t a = (uintptr_t)blk;
-    const uint32_t *d = (const uint32_t *)(a & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)(a & 3);
-    uint32_t v[5];
-#pragma unroll
-    for (int i = 0; i < 5; i++) v[i] = d[i];
-    scale = (v[0] >> (8 * sh)) & 0xffu;
-    const uint32_t off = sh + 1;  // first code byte, 1..4 bytes past d
-#pragma unroll
-    for (int j = 0; j < 4; j++) codes[j] = off == 4 ? v[j + 1] : __builtin_amdgcn_alignbyte(v[j + 1], v[j], off);
-}
-
-// x chunk of CH elements for M tokens, widened to fp32. x is bf16 or fp32 [M][k].
-template <bool XF32, int M, int CH>
-__device__ __forceinline__ void load_x(float (&xf)[M][CH], const void *x, int k, int k0) {
-#pragma unroll
-    for (int t = 0; t < M; t++) {
-        if constexpr (XF32) {
-            const f32x4 *p = (const f32x4 *)((const float *)x + (size_t)t * k + k0);
-#pragma unroll
-            for (int q = 0; q < CH / 4; q++) {
-                const f32x4 v = p[q];
-                xf[t][4 * q] = v.x, xf[t][4 * q + 1] = v.y, xf[t][4 * q + 2] = v.z, xf[t][4 * q + 3] = v.w;
-            }
-        } else {
-            const u32x4 *p = (const u32x4 *)((const uint16_t *)x + (size_t)t * k + k0);
-#pragma unroll
-            for (int q = 0; q < CH / 8; q++) {
-                const u32x4 v = p[q];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    xf[t][8 * q + 2 * j] = bf16_lo(v[j]);
-                    xf[t][8 * q + 2 * j + 1] = bf16_hi(v[j]);
-                }
-            }
-        }
-    }
-}
-
-// sum over the chunk of x * (unscaled) weight, for each token.
-template <WFmt F, int M, int CH>
-__device__ __forceinline__ void chunk_dot(float (&s)[M], const u32x4 w, const float (&xf)[M][CH]) {
-#pragma unroll
-    for (int t = 0; t < M; t++) s[t] = 0.f;
-#pragma unroll
-    for (int d = 0; d < 4; d++) {
-        if constexpr (WTraits<F>::fp4) {
-            const f32x2 a = e2m1x2<0>(w[d]), b = e2m1x2<1>(w[d]), c = e2m1x2<2>(w[d]), e = e2m1x2<3>(w[d]);
-#pragma unroll
-            for (int t = 0; t < M; t++) {
-                if constexpr (F == WFmt::FP4_OCP) {  // byte b: elements 2b, 2b+1
-                    const float *xv = &xf[t][8 * d];
-                    s[t] = fmaf(xv[0], a.x, s[t]);
-                    s[t] = fmaf(xv[1], a.y, s[t]);
-                    s[t] = fmaf(xv[2], b.x, s[t]);
-                    s[t] = fmaf(xv[3], b.y, s[t]);
-                    s[t] = fmaf(xv[4], c.x, s[t]);
-                    s[t] = fmaf(xv[5], c.y, s[t]);
-                    s[t] = fmaf(xv[6], e.x, s[t]);
-                    s[t] = fmaf(xv[7], e.y, s[t]);
-                } else {  // GGUF byte b: elements b, 16 + b
-                    const float *lo = &xf[t][4 * d], *hi = &xf[t][16 + 4 * d];
-                    s[t] = fmaf(lo[0], a.x, s[t]);
-                    s[t] = fmaf(hi[0], a.y, s[t]);
-                    s[t] = fmaf(lo[1], b.x, s[t]);
-                    s[t] = fmaf(hi[1], b.y, s[t]);
-                    s[t] = fmaf(lo[2], c.x, s[t]);
-                    s[t] = fmaf(hi[2], c.y, s[t]);
-                    s[t] = fmaf(lo[3], e.x, s[t]);
-                    s[t] = fmaf(hi[3], e.y, s[t]);
-                }
-            }
-        } else {
-            const f32x2 a = e4m3x2(w[d], false), b = e4m3x2(w[d], true);
-#pragma unroll
-            for (int t = 0; t < M; t++) {
-                const float *xv = &xf[t][4 * d];
-                s[t] = fmaf(xv[0], a.x, s[t]);
-                s[t] = fmaf(xv[1], a.y, s[t]);
-                s[t] = fmaf(xv[2], b.x, s[t]);
-                s[t] = fmaf(xv[3], b.y, s[t]);
-            }
-        }
-    }
-}
 
 template <WFmt F, bool XF32, int M, int R>
 __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, int out_mode) {

@@ -1,0 +1,151 @@
+// Device building blocks shared by the GEMV, expert-FFN and MoE kernels: weight formats, lane-chunk
+// loads of x and weights, exact chunk dot products, and the on-the-fly activation quantization.
+//
+// Every kernel built from these uses the same work split: lane l of wave w owns one fixed K chunk
+// c = 64 w + l of CH elements (16 bytes of FP4 codes, one 17-byte GGUF block, or 16 bytes of FP8
+// codes), so a wave-wide load of one row reads a contiguous kilobyte, and per-row partial sums are
+// reduced over the lanes with DPP (common.hpp dpp_sum) and over the waves through LDS.
+#pragma once
+
+#include "common.hpp"
+
+namespace stbl {
+
+constexpr int kMaxWaves = 8;  // K <= 512 chunks: 16384 FP4 / 8192 FP8 elements
+constexpr int kMaxJobs = 16;  // matrices per launch (the reference's kMxBatch, stbl/kernels.h:18)
+
+enum class WFmt { FP4_OCP, FP4_GGUF, FP8_B128, FP8_E8M0 };
+
+template <WFmt F>
+struct WTraits {
+    static constexpr bool fp4 = F == WFmt::FP4_OCP || F == WFmt::FP4_GGUF;
+    static constexpr int CH = fp4 ? 32 : 16;  // elements per lane chunk
+};
+
+// One matrix of a launch: weights, scales, activations, output.
+struct GemvJob {
+    const uint8_t *w;
+    const void *s;
+    const void *x;
+    void *y;
+};
+struct GemvJobs {
+    GemvJob j[kMaxJobs];
+};
+
+enum OutMode { OUT_BF16 = 0, OUT_F32 = 1, OUT_F32_ROUNDED = 2 };
+
+// A GGUF block c of a row sits at byte 17 c, so it is only byte aligned: read the five dwords that
+// cover it from the enclosing 4-byte boundary (each dword starts inside the buffer, and a 4-byte
+// aligned dword never crosses a page) and realign with v_alignbyte.
+__device__ __forceinline__ void load_gguf_block(const uint8_t *blk, uint32_t &scale, u32x4 &codes) {
+    const uintptr_t a = (uintptr_t)blk;
+    const uint32_t *d = (const uint32_t *)(a & ~(uintptr_t)3);
+    const uint32_t sh = (uint32_t)(a & 3);
+    uint32_t v[5];
+#pragma unroll
+    for (int i = 0; i < 5; i++) v[i] = d[i];
+    scale = (v[0] >> (8 * sh)) & 0xffu;
+    const uint32_t off = sh + 1;  // first code byte, 1..4 bytes past d
+#pragma unroll
+    for (int j = 0; j < 4; j++) codes[j] = off == 4 ? v[j + 1] : __builtin_amdgcn_alignbyte(v[j + 1], v[j], off);
+}
+
+// x chunk of CH elements for M tokens, widened to fp32. x is bf16 or fp32 [M][k].
+template <bool XF32, int M, int CH>
+__device__ __forceinline__ void load_x(float (&xf)[M][CH], const void *x, int k, int k0) {
+#pragma unroll
+    for (int t = 0; t < M; t++) {
+        if constexpr (XF32) {
+            const f32x4 *p = (const f32x4 *)((const float *)x + (size_t)t * k + k0);
+#pragma unroll
+            for (int q = 0; q < CH / 4; q++) {
+                const f32x4 v = p[q];
+                xf[t][4 * q] = v.x, xf[t][4 * q + 1] = v.y, xf[t][4 * q + 2] = v.z, xf[t][4 * q + 3] = v.w;
+            }
+        } else {
+            const u32x4 *p = (const u32x4 *)((const uint16_t *)x + (size_t)t * k + k0);
+#pragma unroll
+            for (int q = 0; q < CH / 8; q++) {
+                const u32x4 v = p[q];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    xf[t][8 * q + 2 * j] = bf16_lo(v[j]);
+                    xf[t][8 * q + 2 * j + 1] = bf16_hi(v[j]);
+                }
+            }
+        }
+    }
+}
+
+// sum over the chunk of x * (unscaled) weight, for each token.
+template <WFmt F, int M, int CH>
+__device__ __forceinline__ void chunk_dot(float (&s)[M], const u32x4 w, const float (&xf)[M][CH]) {
+#pragma unroll
+    for (int t = 0; t < M; t++) s[t] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        if constexpr (WTraits<F>::fp4) {
+            const f32x2 a = e2m1x2<0>(w[d]), b = e2m1x2<1>(w[d]), c = e2m1x2<2>(w[d]), e = e2m1x2<3>(w[d]);
+#pragma unroll
+            for (int t = 0; t < M; t++) {
+                if constexpr (F == WFmt::FP4_OCP) {  // byte b: elements 2b, 2b+1
+                    const float *xv = &xf[t][8 * d];
+                    s[t] = fmaf(xv[0], a.x, s[t]);
+                    s[t] = fmaf(xv[1], a.y, s[t]);
+                    s[t] = fmaf(xv[2], b.x, s[t]);
+                    s[t] = fmaf(xv[3], b.y, s[t]);
+                    s[t] = fmaf(xv[4], c.x, s[t]);
+                    s[t] = fmaf(xv[5], c.y, s[t]);
+                    s[t] = fmaf(xv[6], e.x, s[t]);
+                    s[t] = fmaf(xv[7], e.y, s[t]);
+                } else {  // GGUF byte b: elements b, 16 + b
+                    const float *lo = &xf[t][4 * d], *hi = &xf[t][16 + 4 * d];
+                    s[t] = fmaf(lo[0], a.x, s[t]);
+                    s[t] = fmaf(hi[0], a.y, s[t]);
+                    s[t] = fmaf(lo[1], b.x, s[t]);
+                    s[t] = fmaf(hi[1], b.y, s[t]);
+                    s[t] = fmaf(lo[2], c.x, s[t]);
+                    s[t] = fmaf(hi[2], c.y, s[t]);
+                    s[t] = fmaf(lo[3], e.x, s[t]);
+                    s[t] = fmaf(hi[3], e.y, s[t]);
+                }
+            }
+        } else {
+            const f32x2 a = e4m3x2(w[d], false), b = e4m3x2(w[d], true);
+#pragma unroll
+            for (int t = 0; t < M; t++) {
+                const float *xv = &xf[t][4 * d];
+                s[t] = fmaf(xv[0], a.x, s[t]);
+                s[t] = fmaf(xv[1], a.y, s[t]);
+                s[t] = fmaf(xv[2], b.x, s[t]);
+                s[t] = fmaf(xv[3], b.y, s[t]);
+            }
+        }
+    }
+}
+
+// In-register act_quant(x, 32, "ue8m0", inplace=True) of the lane's chunk (ref/kernel.py:35-45; the
+// reference engine's stbl_act_quant_fp8, stbl/kernels.cu:54-63): per 32 values s = 2^ceil(log2(
+// max(amax, 1e-4) / 448)), x = bf16(e4m3(clamp(x / s, +-448)) * s). A 16-element chunk shares its
+// 32-block with the neighbouring lane (lanes 2b and 2b+1), whose amax comes over by DPP.
+template <int M, int CH>
+__device__ __forceinline__ void act_quant_chunk(float (&xf)[M][CH]) {
+    static_assert(CH == 32 || CH == 16, "chunk must be one or half an act_quant block");
+#pragma unroll
+    for (int t = 0; t < M; t++) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < CH; i++) a = fmaxf(a, fabsf(xf[t][i]));
+        if constexpr (CH == 16)
+            a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0xB1, 0xF, 0xF, false)));
+        const float s = pow2_ceil(fmaxf(a, 1e-4f) * (1.0f / 448.0f));
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const float q = fminf(fmaxf(xf[t][i] / s, -448.f), 448.f);  // exact: s is a power of two
+            xf[t][i] = bf16_round(e4m3_to_f32(f32_to_e4m3(q)) * s);
+        }
+    }
+}
+
+}  // namespace stbl

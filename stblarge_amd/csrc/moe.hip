@@ -1,0 +1,453 @@
+// Expert FFN and routed-MoE kernels over quantized expert slots (layout: expert_layout.hpp).
+//
+// The reference engine runs one MoE layer as (stbl/model.cu:426-594):
+//   router scores -> host top-k -> for the cached and then the refilled experts:
+//   gemv_mxfp4_batch(gate, up) -> swiglu_batch(route weights) -> act_quant_fp8(mid) ->
+//   gemv_mxfp4_batch(down) -> shared expert -> axpy of every expert output in top-k order, then the
+//   shared one -> round_bf16.
+// Here the same arithmetic runs as three launches over a job table (one job = one expert slot and
+// the <= 4 tokens routed to it, each token with its own route weight):
+//   k_moe_gateup  gate and up rows of a job in the same workgroup; the epilogue rounds both to bf16
+//                 and applies SwiGLU with the token's route weight (stbl/kernels.cu:444-459), so
+//                 the gate/up outputs never leave the chip;
+//   k_moe_down    down rows of a job; output rounded to bf16 as the reference's GEMV does;
+//   k_moe_combine per token, the fp32 sum of its experts' outputs in top-k order plus the shared
+//                 expert's, rounded to bf16 (stbl/model.cu:589-592).
+// In the reference's "official" numerics the expert input and the SwiGLU output are quantized to FP8
+// per 32 first (stbl/model.cu:510, :538); both kernels do that quantization in registers on the
+// lane's own chunk of the activation, so it costs no launch and no memory traffic.
+// The router is k_route: sigmoid scores, top-k by score + bias with ties to the lower id, weights
+// renormalized in top-k order (stbl/model.cu:444-451, :528-530 with sigmoid for sqrt-softplus).
+#include "abi_util.hpp"
+#include "expert_layout.hpp"
+#include "gemv_core.hpp"
+
+namespace stbl {
+
+constexpr int kMoeMaxTok = 4;    // tokens per job
+constexpr int kMoeMaxJobs = 40;  // jobs per launch
+constexpr int kMoeMaxT = 16;     // tokens per MoE call
+constexpr int kMoeMaxPick = 17;  // top-k + shared
+
+struct MoeJob {
+    const uint8_t *slot;
+    int m;                     // tokens of this job, 1..4
+    int tok[kMoeMaxTok];       // token rows of x
+    int pair[kMoeMaxTok];      // rows of the intermediate / output buffers
+    float w[kMoeMaxTok];       // route weight of each token
+};
+struct MoeJobs {
+    MoeJob j[kMoeMaxJobs];
+};
+
+// Weights of matrix `mat` (0 gate, 1 up, 2 down) of a slot.
+template <WFmt F>
+struct SlotMat {
+    const uint8_t *codes;
+    const uint8_t *scales;
+    int rows, k;
+    __device__ SlotMat(const uint8_t *slot, const ExpertLayout &L, int mat, int dim, int inter)
+        : codes(slot + L.off[2 * mat]), scales(slot + L.off[2 * mat + 1]), rows(mat == 2 ? dim : inter),
+          k(mat == 2 ? inter : dim) {}
+    // 16 bytes of codes of row `row`, chunk cc, and the chunk's E8M0 scale byte (FP4 only)
+    __device__ __forceinline__ void load(size_t row, int cc, u32x4 &w, uint32_t &sb) const {
+        if constexpr (WTraits<F>::fp4) {
+            w = *(const u32x4 *)(codes + row * (size_t)(k >> 1) + (size_t)cc * 16);
+            sb = scales[row * (size_t)(k >> 5) + cc];
+        } else {
+            w = *(const u32x4 *)(codes + row * (size_t)k + (size_t)cc * 16);
+            sb = 0;
+        }
+    }
+    // FP8: the lane's block scale for a tile whose rows share row0's 128-row block
+    __device__ __forceinline__ float block_scale(int row0, int cc) const {
+        return ((const float *)scales)[(size_t)(row0 >> 7) * ((k + 127) >> 7) + ((cc * 16) >> 7)];
+    }
+};
+
+template <WFmt F>
+__device__ __forceinline__ float chunk_scale(uint32_t sb, float lscale) {
+    if constexpr (WTraits<F>::fp4) return e8m0_to_f32(sb);
+    else return lscale;
+}
+
+// Sums v (one value per lane, reduced with dpp_sum) over the waves: lane 63 of every wave writes
+// red[wave][i]; after the barrier thread i < n holds the total of value i in *out.
+template <int N>
+__device__ __forceinline__ bool wave_total(float (&tot)[N], float (*red)[N], float *out) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    if (lane == 63) {
+#pragma unroll
+        for (int i = 0; i < N; i++) red[wave][i] = tot[i];
+    }
+    __syncthreads();
+    const int i = threadIdx.x;
+    if (i >= N) return false;
+    float acc = red[0][i];
+    for (int v = 1; v < waves; v++) acc += red[v][i];
+    *out = acc;
+    return true;
+}
+
+// ---- gate/up + SwiGLU ----------------------------------------------------------------------------
+
+// Job blockIdx.y, rows [row0, row0 + R) of gate and of up. x bf16 [T][dim] -> h bf16 [P][inter].
+template <WFmt F, int M, int R>
+__global__ __launch_bounds__(512) void k_moe_gateup(MoeJobs jobs, ExpertLayout L, const uint16_t *__restrict__ x,
+                                                    uint16_t *__restrict__ h, int dim, int inter, float limit,
+                                                    int official) {
+    constexpr int CH = WTraits<F>::CH;
+    const MoeJob &J = jobs.j[blockIdx.y];
+    const SlotMat<F> G(J.slot, L, 0, dim, inter), U(J.slot, L, 1, dim, inter);
+    const int lane = threadIdx.x & 63, c = (threadIdx.x >> 6) * 64 + lane, nch = dim / CH;
+    const bool active = c < nch;
+    const int cc = active ? c : 0;
+    const int row0 = blockIdx.x * R;
+    const int m = J.m;
+
+    float xf[M][CH];
+#pragma unroll
+    for (int t = 0; t < M; t++) {
+        float tmp[1][CH];
+        load_x<false, 1, CH>(tmp, x + (size_t)J.tok[t < m ? t : 0] * dim, dim, cc * CH);
+#pragma unroll
+        for (int i = 0; i < CH; i++) xf[t][i] = tmp[0][i];
+    }
+    u32x4 wg[R], wu[R];
+    uint32_t sg[R], su[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const size_t row = (size_t)min(row0 + r, inter - 1);
+        G.load(row, cc, wg[r], sg[r]);
+        U.load(row, cc, wu[r], su[r]);
+    }
+    float lg = 1.f, lu = 1.f;
+    if constexpr (!WTraits<F>::fp4) lg = G.block_scale(row0, cc), lu = U.block_scale(row0, cc);
+    if (official) act_quant_chunk<M, CH>(xf);
+
+    __shared__ float red[kMaxWaves][2 * M * R];
+    float tot[2 * M * R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float sgv[M], suv[M];
+        chunk_dot<F, M, CH>(sgv, wg[r], xf);
+        chunk_dot<F, M, CH>(suv, wu[r], xf);
+        const float a = chunk_scale<F>(sg[r], lg), b = chunk_scale<F>(su[r], lu);
+#pragma unroll
+        for (int t = 0; t < M; t++) {
+            tot[(t * R + r) * 2] = dpp_sum(active ? sgv[t] * a : 0.f);
+            tot[(t * R + r) * 2 + 1] = dpp_sum(active ? suv[t] * b : 0.f);
+        }
+    }
+    // thread q = (t * R + r) * 2 + {0 gate, 1 up}; the even thread finishes the pair
+    float v = 0.f;
+    const bool mine = wave_total<2 * M * R>(tot, red, &v);
+    const float u = __shfl_down(v, 1, kWave);
+    if (!mine || (threadIdx.x & 1)) return;
+    const int q = threadIdx.x >> 1, t = q / R, r = q % R;
+    if (t >= m || row0 + r >= inter) return;
+    float gv = bf16_round(v), uv = bf16_round(u);
+    if (limit > 0) {
+        uv = fminf(fmaxf(uv, -limit), limit);
+        gv = fminf(gv, limit);
+    }
+    h[(size_t)J.pair[t] * inter + row0 + r] = f32_to_bf16_bits(__fdiv_rn(gv, 1.f + expf(-gv)) * uv * J.w[t]);
+}
+
+// ---- down ------------------------------------------------------------------------------------------
+
+// Job blockIdx.y, rows [row0, row0 + R) of down. h bf16 [P][inter] -> o [P][dim] (bf16, or fp32
+// holding the unrounded sum when out_f32).
+template <WFmt F, int M, int R>
+__global__ __launch_bounds__(512) void k_moe_down(MoeJobs jobs, ExpertLayout L, const uint16_t *__restrict__ h,
+                                                  void *__restrict__ o, int dim, int inter, int official, int out_f32) {
+    constexpr int CH = WTraits<F>::CH;
+    const MoeJob &J = jobs.j[blockIdx.y];
+    const SlotMat<F> D(J.slot, L, 2, dim, inter);
+    const int lane = threadIdx.x & 63, c = (threadIdx.x >> 6) * 64 + lane, nch = inter / CH;
+    const bool active = c < nch;
+    const int cc = active ? c : 0;
+    const int row0 = blockIdx.x * R;
+    const int m = J.m;
+
+    float xf[M][CH];
+#pragma unroll
+    for (int t = 0; t < M; t++) {
+        float tmp[1][CH];
+        load_x<false, 1, CH>(tmp, h + (size_t)J.pair[t < m ? t : 0] * inter, inter, cc * CH);
+#pragma unroll
+        for (int i = 0; i < CH; i++) xf[t][i] = tmp[0][i];
+    }
+    u32x4 wd[R];
+    uint32_t sd[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) D.load((size_t)min(row0 + r, dim - 1), cc, wd[r], sd[r]);
+    float ld = 1.f;
+    if constexpr (!WTraits<F>::fp4) ld = D.block_scale(row0, cc);
+    if (official) act_quant_chunk<M, CH>(xf);
+
+    __shared__ float red[kMaxWaves][M * R];
+    float tot[M * R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float s[M];
+        chunk_dot<F, M, CH>(s, wd[r], xf);
+        const float a = chunk_scale<F>(sd[r], ld);
+#pragma unroll
+        for (int t = 0; t < M; t++) tot[t * R + r] = dpp_sum(active ? s[t] * a : 0.f);
+    }
+    float v = 0.f;
+    if (!wave_total<M * R>(tot, red, &v)) return;
+    const int t = threadIdx.x / R, r = threadIdx.x % R;
+    if (t >= m || row0 + r >= dim) return;
+    const size_t at = (size_t)J.pair[t] * dim + row0 + r;
+    if (out_f32) ((float *)o)[at] = v;
+    else ((uint16_t *)o)[at] = f32_to_bf16_bits(v);
+}
+
+// ---- combine ------------------------------------------------------------------------------------
+
+struct PickTable {
+    int pair[kMoeMaxT][kMoeMaxPick];  // per token: output rows in top-k order, then the shared one
+};
+
+// y[t][r] = bf16(sum over token t's picks in order of o[pair][r]) with the fp32 sum starting at 0
+// (stbl/model.cu:579-592: memset, axpy per expert in top-k order, axpy shared, round_bf16).
+__global__ void k_moe_combine(PickTable picks, int npick, const uint16_t *__restrict__ o, void *__restrict__ y,
+                              int dim, int y_f32) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+    if (r >= dim) return;
+    float acc = 0.f;
+    for (int p = 0; p < npick; p++) acc = fmaf(1.f, bf16_bits_to_f32(o[(size_t)picks.pair[t][p] * dim + r]), acc);
+    if (y_f32) ((float *)y)[(size_t)t * dim + r] = bf16_round(acc);
+    else ((uint16_t *)y)[(size_t)t * dim + r] = f32_to_bf16_bits(acc);
+}
+
+// ---- router -------------------------------------------------------------------------------------
+
+// One workgroup of 256 threads per token. score = 1 / (1 + exp(-logit)); the top-k of score + bias
+// (ties to the lower expert id) by k rounds of a workgroup argmax; weight_i = score_i / (sum of
+// the top-k scores in top-k order + 1e-20) * route_scale.
+__global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits, const float *__restrict__ bias,
+                                               int n_exp, int topk, float route_scale, int *__restrict__ ids,
+                                               float *__restrict__ weights, float *__restrict__ scores) {
+    __shared__ float sc[1024];
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    __shared__ int chosen[32];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    for (int e = tid; e < n_exp; e += 256) {
+        const float s = __fdiv_rn(1.f, 1.f + expf(-logits[(size_t)t * n_exp + e]));
+        sc[e] = s;
+        if (scores) scores[(size_t)t * n_exp + e] = s;
+    }
+    __syncthreads();
+    for (int p = 0; p < topk; p++) {
+        float best = -INFINITY;
+        int besti = 0x7fffffff;
+        for (int e = tid; e < n_exp; e += 256) {
+            bool used = false;
+            for (int q = 0; q < p; q++) used |= chosen[q] == e;
+            if (used) continue;
+            const float v = sc[e] + (bias ? bias[e] : 0.f);
+            if (v > best || (v == best && e < besti)) best = v, besti = e;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(best, off, kWave);
+            const int oi = __shfl_xor(besti, off, kWave);
+            if (ov > best || (ov == best && oi < besti)) best = ov, besti = oi;
+        }
+        if ((tid & 63) == 0) bv[tid >> 6] = best, bi[tid >> 6] = besti;
+        __syncthreads();
+        if (tid == 0) {
+            float b = bv[0];
+            int i = bi[0];
+            for (int w = 1; w < 4; w++)
+                if (bv[w] > b || (bv[w] == b && bi[w] < i)) b = bv[w], i = bi[w];
+            chosen[p] = i;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        float sum = 0.f;
+        for (int p = 0; p < topk; p++) sum += sc[chosen[p]];
+        for (int p = 0; p < topk; p++) {
+            float wt = sc[chosen[p]];
+            wt = __fdiv_rn(wt, sum + 1e-20f);
+            wt *= route_scale;
+            ids[(size_t)t * topk + p] = chosen[p];
+            weights[(size_t)t * topk + p] = wt;
+        }
+    }
+}
+
+// ---- host side -------------------------------------------------------------------------------------
+
+static inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+template <WFmt F, int M>
+static hipError_t launch_gateup(const MoeJobs &jobs, int n, const ExpertLayout &L, const uint16_t *x, uint16_t *h,
+                                int dim, int inter, float limit, int official, hipStream_t st) {
+    constexpr int R = M == 1 ? 4 : 2;
+    const int waves = ceil_div(dim / WTraits<F>::CH, 64);
+    hipLaunchKernelGGL((k_moe_gateup<F, M, R>), dim3(ceil_div(inter, R), n), dim3(64 * waves), 0, st, jobs, L, x, h,
+                       dim, inter, limit, official);
+    return hipGetLastError();
+}
+
+template <WFmt F, int M>
+static hipError_t launch_down(const MoeJobs &jobs, int n, const ExpertLayout &L, const uint16_t *h, void *o, int dim,
+                              int inter, int official, int out_f32, hipStream_t st) {
+    constexpr int R = M == 1 ? 4 : 2;
+    const int waves = ceil_div(inter / WTraits<F>::CH, 64);
+    hipLaunchKernelGGL((k_moe_down<F, M, R>), dim3(ceil_div(dim, R), n), dim3(64 * waves), 0, st, jobs, L, h, o, dim,
+                       inter, official, out_f32);
+    return hipGetLastError();
+}
+
+// Runs the jobs (sorted into launches by token count) through gate/up and down.
+template <WFmt F>
+static hipError_t run_jobs(const MoeJob *all, int njobs, const ExpertLayout &L, const uint16_t *x, uint16_t *h,
+                           void *o, int dim, int inter, float limit, int official, int out_f32, hipStream_t st) {
+    for (int phase = 0; phase < 2; phase++) {
+        for (int mclass = 1; mclass <= 3; mclass++) {  // M = 1, 2, 4 templates
+            MoeJobs batch;
+            int n = 0;
+            auto flush = [&]() -> hipError_t {
+                if (n == 0) return hipSuccess;
+                hipError_t e;
+                if (phase == 0) {
+                    e = mclass == 1 ? launch_gateup<F, 1>(batch, n, L, x, h, dim, inter, limit, official, st)
+                        : mclass == 2 ? launch_gateup<F, 2>(batch, n, L, x, h, dim, inter, limit, official, st)
+                                      : launch_gateup<F, 4>(batch, n, L, x, h, dim, inter, limit, official, st);
+                } else {
+                    e = mclass == 1 ? launch_down<F, 1>(batch, n, L, h, o, dim, inter, official, out_f32, st)
+                        : mclass == 2 ? launch_down<F, 2>(batch, n, L, h, o, dim, inter, official, out_f32, st)
+                                      : launch_down<F, 4>(batch, n, L, h, o, dim, inter, official, out_f32, st);
+                }
+                n = 0;
+                return e;
+            };
+            for (int j = 0; j < njobs; j++) {
+                const int cls = all[j].m == 1 ? 1 : (all[j].m == 2 ? 2 : 3);
+                if (cls != mclass) continue;
+                batch.j[n++] = all[j];
+                if (n == kMoeMaxJobs) {
+                    const hipError_t e = flush();
+                    if (e != hipSuccess) return e;
+                }
+            }
+            const hipError_t e = flush();
+            if (e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
+}
+
+static bool dims_ok(int fmt, int dim, int inter) {
+    const int CH = fmt == EXPERT_FP4 ? 32 : 16;
+    const int align = fmt == EXPERT_FP4 ? 32 : 128;  // FP8: rows of a tile must share a scale block
+    return dim > 0 && inter > 0 && dim % align == 0 && inter % align == 0 && dim / CH <= kMaxWaves * 64 &&
+           inter / CH <= kMaxWaves * 64;
+}
+
+}  // namespace stbl
+
+using namespace stbl;
+
+extern "C" {
+
+uint64_t stbl_amd_expert_layout(int fmt, int dim, int inter, uint64_t *offsets) {
+    const ExpertLayout L = expert_layout(fmt, dim, inter);
+    if (offsets)
+        for (int i = 0; i < 6; i++) offsets[i] = L.off[i];
+    return L.bytes;
+}
+
+int stbl_amd_expert_ffn(int fmt, void *y, const void *slot, const void *x, int m, int dim, int inter, float weight,
+                        float limit, int official, int y_f32, void *work, hipStream_t st) {
+    if (fmt != EXPERT_FP4 && fmt != EXPERT_FP8) return abi_fail(hipErrorInvalidValue, "expert_ffn: unknown format %d", fmt);
+    if (!y || !slot || !x || !work) return abi_fail(hipErrorInvalidValue, "expert_ffn: null pointer");
+    if (!dims_ok(fmt, dim, inter)) return abi_fail(hipErrorInvalidValue, "expert_ffn: unsupported dims %d x %d", dim, inter);
+    if (m < 1 || m > kMoeMaxTok) return abi_fail(hipErrorInvalidValue, "expert_ffn: m must be 1..4 (m=%d)", m);
+    if (!aligned16(slot) || ((uintptr_t)slot & 255) || !aligned16(x) || !aligned16(work))
+        return abi_fail(hipErrorInvalidValue, "expert_ffn: slot must be 256-byte and x/work 16-byte aligned");
+    MoeJob J = {};
+    J.slot = (const uint8_t *)slot;
+    J.m = m;
+    for (int t = 0; t < m; t++) J.tok[t] = t, J.pair[t] = t, J.w[t] = weight;
+    const ExpertLayout L = expert_layout(fmt, dim, inter);
+    const hipError_t e = fmt == EXPERT_FP4
+        ? run_jobs<WFmt::FP4_OCP>(&J, 1, L, (const uint16_t *)x, (uint16_t *)work, y, dim, inter, limit, official, y_f32, st)
+        : run_jobs<WFmt::FP8_B128>(&J, 1, L, (const uint16_t *)x, (uint16_t *)work, y, dim, inter, limit, official, y_f32, st);
+    return abi_status(e, "expert_ffn launch");
+}
+
+// Routed MoE over cached expert slots. slots: HOST array of n_slots device pointers (one per
+// distinct expert used by this call). pick: HOST [t][topk] indices into slots, weights: HOST
+// [t][topk] route weights, shared: index into slots of the always-on expert (weight 1) or -1.
+// work: device scratch of at least stbl_amd_moe_work_bytes(t, topk, dim, inter) bytes.
+int stbl_amd_moe_experts(int fmt, void *y, const void *x, int t, int dim, int inter, const void *const *slots,
+                         int n_slots, const int *pick, const float *weights, int topk, int shared, float limit,
+                         int official, int y_f32, void *work, hipStream_t st) {
+    if (fmt != EXPERT_FP4 && fmt != EXPERT_FP8) return abi_fail(hipErrorInvalidValue, "moe_experts: unknown format %d", fmt);
+    if (!y || !x || !slots || !pick || !weights || !work) return abi_fail(hipErrorInvalidValue, "moe_experts: null pointer");
+    if (!dims_ok(fmt, dim, inter)) return abi_fail(hipErrorInvalidValue, "moe_experts: unsupported dims %d x %d", dim, inter);
+    if (t < 1 || t > kMoeMaxT || topk < 1 || topk + 1 > kMoeMaxPick || n_slots < 1 || shared >= n_slots)
+        return abi_fail(hipErrorInvalidValue, "moe_experts: need 1 <= t <= 16, 1 <= topk <= 16 (t=%d topk=%d)", t, topk);
+    if (!aligned16(x) || !aligned16(work)) return abi_fail(hipErrorInvalidValue, "moe_experts: x and work must be 16-byte aligned");
+    for (int i = 0; i < n_slots; i++)
+        if (!slots[i] || ((uintptr_t)slots[i] & 255)) return abi_fail(hipErrorInvalidValue, "moe_experts: slot %d null or not 256-byte aligned", i);
+    // jobs: one per (slot, group of <= 4 tokens); pair rows numbered in job order
+    static thread_local MoeJob jobs[kMoeMaxT * kMoeMaxPick];
+    PickTable table = {};
+    int njobs = 0, npairs = 0;
+    const int npick = topk + (shared >= 0 ? 1 : 0);
+    for (int s = 0; s < n_slots; s++) {
+        MoeJob *J = nullptr;
+        for (int tt = 0; tt < t; tt++)
+            for (int p = 0; p < npick; p++) {
+                const int sl = p < topk ? pick[tt * topk + p] : shared;
+                if (sl < 0 || sl >= n_slots) return abi_fail(hipErrorInvalidValue, "moe_experts: pick out of range");
+                if (sl != s) continue;
+                if (!J || J->m == kMoeMaxTok) {
+                    J = &jobs[njobs++];
+                    *J = MoeJob{};
+                    J->slot = (const uint8_t *)slots[s];
+                }
+                J->tok[J->m] = tt;
+                J->pair[J->m] = npairs;
+                J->w[J->m] = p < topk ? weights[tt * topk + p] : 1.f;
+                J->m++;
+                table.pair[tt][p] = npairs++;
+            }
+    }
+    const ExpertLayout L = expert_layout(fmt, dim, inter);
+    uint16_t *h = (uint16_t *)work;
+    uint16_t *o = h + (size_t)npairs * inter;
+    hipError_t e = fmt == EXPERT_FP4
+        ? run_jobs<WFmt::FP4_OCP>(jobs, njobs, L, (const uint16_t *)x, h, o, dim, inter, limit, official, 0, st)
+        : run_jobs<WFmt::FP8_B128>(jobs, njobs, L, (const uint16_t *)x, h, o, dim, inter, limit, official, 0, st);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(k_moe_combine, dim3(ceil_div(dim, 256), t), dim3(256), 0, st, table, npick, o, y, dim, y_f32);
+        e = hipGetLastError();
+    }
+    return abi_status(e, "moe_experts launch");
+}
+
+// Scratch bytes stbl_amd_moe_experts needs for t tokens.
+uint64_t stbl_amd_moe_work_bytes(int t, int topk, int dim, int inter) {
+    const uint64_t pairs = (uint64_t)t * (topk + 1);
+    return align256(pairs * inter * 2) + align256(pairs * dim * 2);
+}
+
+int stbl_amd_route(const float *logits, const float *bias, int t, int n_exp, int topk, float route_scale, int *ids,
+                   float *weights, float *scores, hipStream_t st) {
+    if (!logits || !ids || !weights || t < 1 || n_exp < 1 || n_exp > 1024 || topk < 1 || topk > 32 || topk > n_exp)
+        return abi_fail(hipErrorInvalidValue, "route: need 1 <= topk <= min(32, n_exp), n_exp <= 1024");
+    hipLaunchKernelGGL(k_route, dim3(t), dim3(256), 0, st, logits, bias, n_exp, topk, route_scale, ids, weights, scores);
+    return abi_status(hipGetLastError(), "route launch");
+}
+
+}  // extern "C"

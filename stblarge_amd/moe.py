@@ -1,0 +1,122 @@
+"""Host side of the routed MoE layer: the expert cache and the per-step orchestration.
+
+Mirrors the reference engine's moe() (stbl/model.cu:426-594) for one layer:
+  router (device) -> route ids to the host (the reference's to_host sync, :441) -> expert-cache
+  lookups with LRU bookkeeping and refills of misses (:497-507, :383-422) -> the expert kernels
+  (gate/up + SwiGLU, down, ordered combine) -> mark the slots used.
+All device work is in libstbl_amd.so; this module only sequences it and keeps the host-side state.
+"""
+
+import ctypes
+
+import torch
+
+from . import _lib, ops
+
+
+class ExpertCache:
+    """HBM LRU cache of expert slots over a pinned host pool (stbl_amd_cache_*)."""
+
+    def __init__(self, slots, slot_bytes, host_pool, n_experts, n_layers=1, host_stride=None):
+        if not isinstance(host_pool, torch.Tensor) or host_pool.is_cuda or not host_pool.is_pinned():
+            raise ValueError("host_pool must be a pinned host tensor")
+        stride = host_stride if host_stride is not None else slot_bytes
+        if host_pool.numel() * host_pool.element_size() < stride * n_experts * n_layers:
+            raise ValueError("host_pool is smaller than n_layers * n_experts * host_stride bytes")
+        self.pool = host_pool  # keeps the pinned memory alive as long as the cache
+        self.slots, self.slot_bytes, self.n_experts, self.n_layers = slots, slot_bytes, n_experts, n_layers
+        self.handle = _lib.load().stbl_amd_cache_create(slots, slot_bytes, ctypes.c_void_p(host_pool.data_ptr()),
+                                                        stride, n_experts, n_layers)
+        if not self.handle:
+            _lib.check(-1, "cache_create")
+
+    def lookup(self, ids, layer=0, stream=None):
+        """Slots (device addresses) and hit flags of expert ids, in order; returns (ptrs, hits, misses)."""
+        n = len(ids)
+        arr = (ctypes.c_int * n)(*[int(i) for i in ids])
+        ptrs = (ctypes.c_void_p * n)()
+        hit = (ctypes.c_int * n)()
+        s = ops._stream(stream)
+        nmiss = _lib.load().stbl_amd_cache_lookup(self.handle, arr, n, layer, ptrs, hit, s)
+        if nmiss < 0:
+            _lib.check(nmiss, "cache_lookup")
+        return [int(p) for p in ptrs], [bool(h) for h in hit], nmiss
+
+    def mark_used(self, stream=None):
+        _lib.check(_lib.load().stbl_amd_cache_mark_used(self.handle, ops._stream(stream)), "cache_mark_used")
+
+    def stats(self):
+        out = (ctypes.c_uint64 * 6)()
+        _lib.check(_lib.load().stbl_amd_cache_stats(self.handle, out), "cache_stats")
+        keys = ("hits", "misses", "refill_bytes", "lookups", "in_use", "slots")
+        return dict(zip(keys, [int(v) for v in out]))
+
+    def peek(self, expert, layer=0):
+        p = _lib.load().stbl_amd_cache_peek(self.handle, layer, expert)
+        return int(p) if p else None
+
+    def fail_refill_after(self, n):
+        _lib.check(_lib.load().stbl_amd_cache_fail_refill_after(self.handle, n), "cache_fail_refill_after")
+
+    def close(self):
+        if self.handle:
+            _lib.load().stbl_amd_cache_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class MoELayer:
+    """One routed MoE layer: n_experts routed experts in a pinned host pool behind an HBM LRU cache,
+    plus an always-on shared expert resident in HBM.
+
+    forward(x, logits): x bf16 [t, dim] and router logits fp32 [t, n_experts] on the device; returns
+    y bf16 [t, dim]. Routing follows the reference (sigmoid in place of sqrt-softplus, as configured):
+    top-k of score + bias, ties to the lower id, weights renormalized then scaled."""
+
+    def __init__(self, fmt, dim, inter, host_pool, n_experts, topk, cache_slots, shared_slot=None, bias=None,
+                 route_scale=1.0, limit=0.0, official=False, max_tokens=4):
+        self.fmt, self.dim, self.inter, self.topk = fmt, dim, inter, topk
+        self.slot_bytes, _ = ops.expert_layout(fmt, dim, inter)
+        self.cache = ExpertCache(cache_slots, self.slot_bytes, host_pool, n_experts)
+        self.shared = shared_slot
+        self.bias, self.route_scale, self.limit, self.official = bias, route_scale, limit, official
+        dev = torch.device("cuda", torch.cuda.current_device())
+        self.work = torch.empty(ops.moe_work_bytes(max_tokens, topk, dim, inter), dtype=torch.uint8, device=dev)
+        self.max_tokens = max_tokens
+        self.last_route = None  # (ids, weights) of the last step, as lists (stbl_last_route)
+
+    def route(self, logits):
+        ids, w = ops.route(logits, self.topk, self.bias, self.route_scale)
+        return ids.cpu().tolist(), w.cpu().tolist()  # host sync, as the reference's to_host
+
+    def forward(self, x, logits, route=None, stream=None):
+        t = x.shape[0]
+        if t > self.max_tokens:
+            raise ValueError(f"at most {self.max_tokens} tokens per step")
+        ids, w = route if route is not None else self.route(logits)
+        self.last_route = (ids, w)
+        uniq = []
+        for row in ids:
+            for e in row:
+                if e not in uniq:
+                    uniq.append(e)
+        ptrs, _, _ = self.cache.lookup(uniq, stream=stream)
+        slot_of = {e: i for i, e in enumerate(uniq)}
+        slots = list(ptrs)
+        shared = -1
+        if self.shared is not None:
+            shared = len(slots)
+            slots.append(self.shared.data_ptr())
+        pick = [[slot_of[e] for e in row] for row in ids]
+        y = ops.moe_experts(x, slots, pick, w, self.fmt, self.dim, self.inter, shared=shared, limit=self.limit,
+                            official=self.official, work=self.work)
+        self.cache.mark_used(stream)
+        return y
+
+    def close(self):
+        self.cache.close()

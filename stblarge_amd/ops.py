@@ -12,6 +12,7 @@ Names follow the reference:
 """
 
 import ctypes
+import math
 
 import torch
 
@@ -229,3 +230,117 @@ def stbl_axpy(y, x, a, n):
     _lib.load().stbl_axpy(_ptr(y), _ptr(x), float(a), n, _stream())
     _lib.check(None, "stbl_axpy")
     return y
+
+
+# ---- expert FFN / MoE / router (v2) ------------------------------------------------------------------
+
+FP4, FP8 = 0, 1
+
+
+def expert_layout(fmt, dim, inter):
+    """(slot bytes, [offsets of gate codes, gate scales, up codes, up scales, down codes, down scales])."""
+    offs = (ctypes.c_uint64 * 6)()
+    n = _lib.load().stbl_amd_expert_layout(fmt, dim, inter, offs)
+    return int(n), [int(o) for o in offs]
+
+
+def _mat_shapes(fmt, dim, inter):
+    out = []
+    for rows, k in ((inter, dim), (inter, dim), (dim, inter)):
+        if fmt == FP4:
+            out += [((rows, k // 2), torch.uint8), ((rows, k // 32), torch.uint8)]
+        else:
+            out += [((rows, k), torch.uint8), (((rows + 127) // 128, (k + 127) // 128), torch.float32)]
+    return out
+
+
+def slot_views(slot, fmt, dim, inter):
+    """Views of the six parts (codes/scales of gate, up, down) of a uint8 slot tensor."""
+    nbytes, offs = expert_layout(fmt, dim, inter)
+    if slot.dtype != torch.uint8 or slot.numel() < nbytes:
+        raise ValueError(f"slot must be >= {nbytes} uint8 bytes")
+    views = []
+    for off, (shape, dt) in zip(offs, _mat_shapes(fmt, dim, inter)):
+        n = math.prod(shape) * (4 if dt == torch.float32 else 1)
+        views.append(slot[off:off + n].view(dt).view(shape))
+    return views
+
+
+def pack_slot(parts, fmt, dim, inter, out=None):
+    """Writes [gate codes, gate scales, up codes, up scales, down codes, down scales] into a slot."""
+    nbytes, _ = expert_layout(fmt, dim, inter)
+    dev = parts[0].device
+    slot = out if out is not None else torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    for v, p in zip(slot_views(slot, fmt, dim, inter), parts):
+        v.copy_(p)
+    return slot
+
+
+def quant_expert(w_gate, w_up, w_down, fmt, out=None):
+    """Quantize fp32 gate/up [inter, dim] and down [dim, inter] on the device into one slot."""
+    q = quant_fp4 if fmt == FP4 else quant_fp8_b128
+    parts = []
+    for w in (w_gate, w_up, w_down):
+        parts += list(q(w))
+    inter, dim = w_gate.shape
+    return pack_slot(parts, fmt, dim, inter, out)
+
+
+def expert_ffn(slot, x, fmt, dim, inter, weight=1.0, limit=0.0, official=False, out_f32=False):
+    """y [m, dim] = down(swiglu(gate x, up x)) for one expert slot, m <= 4 tokens."""
+    _need(slot, torch.uint8, "slot")
+    _need(x, torch.bfloat16, "x")
+    x2 = _rows2(x)
+    m = x2.shape[0]
+    if x2.shape[1] != dim:
+        raise ValueError("x must be [m, dim]")
+    if slot.numel() < expert_layout(fmt, dim, inter)[0]:
+        raise ValueError("slot too small")
+    y = torch.empty((m, dim), dtype=torch.float32 if out_f32 else torch.bfloat16, device=x.device)
+    work = torch.empty(m * inter, dtype=torch.bfloat16, device=x.device)
+    _lib.check(_lib.load().stbl_amd_expert_ffn(fmt, _ptr(y), _ptr(slot), _ptr(x2), m, dim, inter, float(weight),
+                                               float(limit), int(official), int(out_f32), _ptr(work), _stream()),
+               "expert_ffn")
+    return y
+
+
+def moe_work_bytes(t, topk, dim, inter):
+    return int(_lib.load().stbl_amd_moe_work_bytes(t, topk, dim, inter))
+
+
+def moe_experts(x, slots, pick, weights, fmt, dim, inter, shared=-1, limit=0.0, official=False, out_f32=False,
+                work=None, out=None):
+    """Expert part of a routed MoE layer. slots: list of device uint8 slot tensors (or raw device
+    addresses); pick: [t][topk] indices into slots; weights: [t][topk] floats; shared: slot index of
+    the always-on expert or -1."""
+    _need(x, torch.bfloat16, "x")
+    x2 = _rows2(x)
+    t = x2.shape[0]
+    topk = len(pick[0])
+    addrs = [s if isinstance(s, int) else s.data_ptr() for s in slots]
+    arr = (ctypes.c_void_p * len(addrs))(*addrs)
+    pk = (ctypes.c_int * (t * topk))(*[int(v) for row in pick for v in row])
+    wt = (ctypes.c_float * (t * topk))(*[float(v) for row in weights for v in row])
+    nbytes = moe_work_bytes(t, topk, dim, inter)
+    if work is None or work.numel() < nbytes:
+        work = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    y = out if out is not None else torch.empty((t, dim), dtype=torch.float32 if out_f32 else torch.bfloat16,
+                                                device=x.device)
+    _lib.check(_lib.load().stbl_amd_moe_experts(fmt, _ptr(y), _ptr(x2), t, dim, inter, arr, len(addrs), pk, wt, topk,
+                                                shared, float(limit), int(official), int(out_f32), _ptr(work),
+                                                _stream()), "moe_experts")
+    return y
+
+
+def route(logits, topk, bias=None, route_scale=1.0, want_scores=False):
+    """Device router: (ids int32 [t, topk], weights fp32 [t, topk][, scores fp32 [t, E]])."""
+    _need(logits, torch.float32, "logits", 2)
+    t, e = logits.shape
+    ids = torch.empty((t, topk), dtype=torch.int32, device=logits.device)
+    w = torch.empty((t, topk), dtype=torch.float32, device=logits.device)
+    sc = torch.empty((t, e), dtype=torch.float32, device=logits.device) if want_scores else None
+    if bias is not None:
+        _need(bias, torch.float32, "bias", 1)
+    _lib.check(_lib.load().stbl_amd_route(_ptr(logits), _ptr(bias), t, e, topk, float(route_scale), _ptr(ids), _ptr(w),
+                                          _ptr(sc), _stream()), "route")
+    return (ids, w, sc) if want_scores else (ids, w)

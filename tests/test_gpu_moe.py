@@ -1,0 +1,197 @@
+"""GPU parity of the expert FFN, the routed MoE layer, the router and the expert cache.
+
+Oracle: stbl_oracle.c's expert FFN / MoE composition (stbl/model.cu:505-592), router
+(stbl/model.cu:444-451 with sigmoid) and oracle.lru_simulate (stbl/model.cu:347-422, 497-507).
+Bar: the unrounded down product within 1e-3 normwise of the oracle; bf16 outputs at most one bf16
+step from the oracle's, flips rare (an intermediate bf16 rounding of g or u may flip when the two
+sums differ in their last fp32 bits). Router ids exact; route weights within a few fp32 ulps (the
+sigmoid's exp is a library routine on both sides).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from stblarge_amd import data, ops
+from stblarge_amd.moe import ExpertCache, MoELayer
+from util import assert_gemv, bf16_ulps, np_
+
+pytestmark = pytest.mark.gpu
+
+
+def make_expert(fmt, dim, inter, seed, gpu):
+    """Seeded N(0, 0.02) gate/up/down quantized on the GPU into one slot; also the numpy parts."""
+    ws = [data.weight(inter, dim, seed), data.weight(inter, dim, seed + 1), data.weight(dim, inter, seed + 2)]
+    slot = ops.quant_expert(*[w.to(gpu) for w in ws], fmt)
+    parts = [np_(v) for v in ops.slot_views(slot, fmt, dim, inter)]
+    return slot, parts
+
+
+def oracle_ffn(fmt, parts, dim, inter, x, w, limit, official):
+    if fmt == ops.FP4:
+        packed = np.concatenate([p.ravel() for p in parts])
+        return oracle.expert_ffn_fp4(packed, dim, inter, x, w, limit, official, raw=True)
+    g, u, d = (parts[0], parts[1]), (parts[2], parts[3]), (parts[4], parts[5])
+    return oracle.expert_ffn_fp8(g, u, d, dim, inter, x, w, limit, official, raw=True)
+
+
+@pytest.mark.parametrize("fmt", [ops.FP4, ops.FP8])
+@pytest.mark.parametrize("dim,inter", [(512, 256), (7168, 2048)])
+@pytest.mark.parametrize("official", [False, True])
+def test_expert_ffn(gpu, fmt, dim, inter, official):
+    slot, parts = make_expert(fmt, dim, inter, seed=dim + fmt, gpu=gpu)
+    m = 1 if dim == 7168 else 3
+    x = data.activation(m, dim, seed=7)
+    w, limit = (1.0, 0.0) if dim == 7168 else (0.37, 10.0)
+    y16 = np_(ops.expert_ffn(slot, x.to(gpu), fmt, dim, inter, w, limit, official))
+    y32 = np_(ops.expert_ffn(slot, x.to(gpu), fmt, dim, inter, w, limit, official, out_f32=True))
+    for t in range(m):
+        o, raw = oracle_ffn(fmt, parts, dim, inter, x[t].float().numpy(), w, limit, official)
+        assert np.array_equal(oracle.bf16_round(raw.astype(np.float32)), o)
+        assert_gemv(y32[t], y16[t], raw)
+
+
+def test_expert_ffn_m4_matches_m1(gpu):
+    dim, inter = 1024, 512
+    slot, _ = make_expert(ops.FP4, dim, inter, seed=3, gpu=gpu)
+    x = data.activation(4, dim, seed=4).to(gpu)
+    y4 = ops.expert_ffn(slot, x, ops.FP4, dim, inter, out_f32=True)
+    for t in range(4):
+        y1 = ops.expert_ffn(slot, x[t:t + 1].contiguous(), ops.FP4, dim, inter, out_f32=True)
+        assert torch.equal(y4[t], y1[0])  # same rows, same lanes, same order
+
+
+@pytest.mark.parametrize("t", [1, 4])
+@pytest.mark.parametrize("official", [False, True])
+def test_moe_experts_fp4(gpu, t, official):
+    dim, inter, topk, n = 512, 256, 4, 6
+    experts = [make_expert(ops.FP4, dim, inter, seed=100 + 3 * i, gpu=gpu) for i in range(n)]
+    rng = np.random.default_rng(t)
+    pick = [list(rng.choice(n - 1, size=topk, replace=False)) for _ in range(t)]  # slot n-1 is the shared one
+    w = rng.random((t, topk)).astype(np.float32)
+    x = data.activation(t, dim, seed=9)
+    y = np_(ops.moe_experts(x.to(gpu), [e[0] for e in experts], pick, w.tolist(), ops.FP4, dim, inter, shared=n - 1,
+                            official=official))
+    packed = [np.concatenate([p.ravel() for p in e[1]]) for e in experts]
+    want = oracle.moe_fp4([[packed[i] for i in row] for row in pick], w, packed[n - 1], dim, inter, x.float().numpy(),
+                          official=official)
+    u = bf16_ulps(y, want)
+    assert u.max() <= 1 and u.mean() < 0.02, (u.max(), u.mean())
+
+
+def test_moe_experts_shared_token_groups(gpu):
+    # six tokens all routed to the same two experts: jobs of <= 4 tokens are split (4 + 2)
+    dim, inter, topk = 256, 128, 2
+    experts = [make_expert(ops.FP4, dim, inter, seed=200 + 3 * i, gpu=gpu) for i in range(2)]
+    t = 6
+    pick = [[0, 1] if i % 2 else [1, 0] for i in range(t)]
+    w = np.full((t, topk), 0.5, np.float32)
+    x = data.activation(t, dim, seed=11)
+    y = np_(ops.moe_experts(x.to(gpu), [e[0] for e in experts], pick, w.tolist(), ops.FP4, dim, inter))
+    packed = [np.concatenate([p.ravel() for p in e[1]]) for e in experts]
+    want = oracle.moe_fp4([[packed[i] for i in row] for row in pick], w, None, dim, inter, x.float().numpy())
+    assert bf16_ulps(y, want).max() <= 1
+
+
+def test_route(gpu):
+    t, e, topk = 4, 256, 8
+    logits = data.zipf_logits(t, e, seed=5)
+    bias = data.normal((e,), 0.01, seed=6)
+    ids, w = ops.route(logits.to(gpu), topk, bias.to(gpu), route_scale=2.5)
+    _, oids, ow = oracle.route(logits.numpy(), topk, bias.numpy(), 2.5)
+    assert np_(ids).tolist() == oids.tolist()
+    assert np.allclose(np_(w), ow, rtol=8 * 2.0 ** -24, atol=0)
+    tie = torch.zeros(2, e)
+    ids, w = ops.route(tie.to(gpu), topk)
+    assert np_(ids).tolist() == [list(range(topk))] * 2
+    assert np.allclose(np_(w), 1.0 / topk)
+
+
+# ---- expert cache ------------------------------------------------------------------------------------
+
+def pinned_pool(n_experts, slot_bytes):
+    pool = torch.empty(n_experts * slot_bytes, dtype=torch.uint8, pin_memory=True)
+    view = pool.view(n_experts, slot_bytes)
+    for e in range(n_experts):
+        view[e].fill_(e + 1)
+        view[e, :4] = torch.tensor([e, 255 - e, 7, 9], dtype=torch.uint8)
+    return pool
+
+
+def test_cache_lru_matches_oracle(gpu):
+    n, slots, sb = 40, 6, 4096
+    pool = pinned_pool(n, sb)
+    cache = ExpertCache(slots, sb, pool, n)
+    rng = np.random.default_rng(0)
+    steps = [list(rng.choice(n, size=4, replace=False)) for _ in range(200)]
+    want = oracle.lru_simulate(steps, slots)
+    for ids, (hits, where, _) in zip(steps, want):
+        ptrs, got_hits, nmiss = cache.lookup(ids)
+        assert got_hits == hits
+        assert nmiss == hits.count(False)
+        cache.mark_used()
+        torch.cuda.synchronize()
+        for e, p in zip(ids, ptrs):
+            head = torch.empty(8, dtype=torch.uint8, device=gpu)
+            torch.cuda.current_stream().synchronize()
+            _copy_from_addr(head, p)
+            assert head.cpu().tolist()[:4] == [e, 255 - e, 7, 9]
+    st = cache.stats()
+    assert st["hits"] + st["misses"] == 800 and st["in_use"] == slots
+    assert st["refill_bytes"] == st["misses"] * sb
+    cache.close()
+
+
+def _copy_from_addr(dst, addr):
+    """dst <- bytes at device address addr (a slot handed out by the cache), through the HIP runtime
+    torch already loaded (the same one libstbl_amd.so binds to)."""
+    import ctypes
+    import os
+
+    hip = ctypes.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert hip.hipMemcpy(ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(addr), dst.numel(), 3) == 0
+
+
+def test_cache_refill_failure_leaves_slot_unmapped(gpu):
+    n, slots, sb = 10, 3, 4096
+    cache = ExpertCache(slots, sb, pinned_pool(n, sb), n)
+    cache.lookup([0, 1])
+    cache.fail_refill_after(0)  # the next refill fails on the host
+    with pytest.raises(Exception):
+        cache.lookup([2])
+    assert cache.peek(2) is None
+    ptrs, hits, nmiss = cache.lookup([2])  # retried: misses again, now succeeds
+    assert hits == [False] and nmiss == 1 and cache.peek(2) == ptrs[0]
+    with pytest.raises(Exception):
+        cache.lookup([3, 4, 5, 6])  # more experts than slots in one lookup
+    cache.close()
+
+
+def test_moe_layer_end_to_end(gpu):
+    dim, inter, n, topk, slots = 256, 128, 24, 3, 12  # <= 12 distinct experts per 4-token step
+    fmt = ops.FP4
+    slot_bytes, _ = ops.expert_layout(fmt, dim, inter)
+    pool = torch.empty(n * slot_bytes, dtype=torch.uint8, pin_memory=True)
+    packed = []
+    for e in range(n):
+        s, parts = make_expert(fmt, dim, inter, seed=300 + 3 * e, gpu=gpu)
+        pool[e * slot_bytes:(e + 1) * slot_bytes].copy_(s.cpu())
+        packed.append(np.concatenate([p.ravel() for p in parts]))
+    shared, sparts = make_expert(fmt, dim, inter, seed=999, gpu=gpu)
+    spacked = np.concatenate([p.ravel() for p in sparts])
+    layer = MoELayer(fmt, dim, inter, pool, n, topk, slots, shared_slot=shared)
+    hits_total = 0
+    for step in range(12):
+        t = 1 + step % 4
+        logits = data.zipf_logits(t, n, seed=step)
+        x = data.activation(t, dim, seed=50 + step)
+        y = np_(layer.forward(x.to(gpu), logits.to(gpu)))
+        _, oids, ow = oracle.route(logits.numpy(), topk)
+        assert [list(r) for r in layer.last_route[0]] == oids.tolist()
+        want = oracle.moe_fp4([[packed[i] for i in row] for row in oids], ow, spacked, dim, inter, x.float().numpy())
+        assert bf16_ulps(y, want).max() <= 1
+        hits_total = layer.cache.stats()["hits"]
+    assert hits_total > 0
+    layer.close()
