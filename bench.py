@@ -35,7 +35,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="all", help="fp4 = the headline workload only")
+    ap.add_argument("--only", default="all", help="fp4 (headline only) | gemv | ffn | moe | all")
+    ap.add_argument("--moe-steps", type=int, default=200)
+    ap.add_argument("--moe-warmup", type=int, default=1000)
     ap.add_argument("--eager", action="store_true", help="also time launches issued one by one from Python")
     return ap.parse_args()
 
@@ -111,6 +113,118 @@ def gemv_workload(torch, fmt, rows, k, m, steps, warmup, use_graph=True):
             "graph": use_graph}
 
 
+def ffn_workload(torch, fmt, steps, warmup):
+    """C3: one expert FFN (gate/up + SwiGLU, down) at dim 7168, inter 2048, one token."""
+    from stblarge_amd import data, ops
+
+    dev = torch.device("cuda:0")
+    dim, inter = 7168, 2048
+    slot = ops.quant_expert(data.weight(inter, dim, 11, dev), data.weight(inter, dim, 12, dev),
+                            data.weight(dim, inter, 13, dev), fmt)
+    copies = max(2, math.ceil(ROTATE_BYTES / slot.numel()))
+    slots = [slot.clone() for _ in range(copies)]
+    x = data.activation(1, dim, seed=14, device=dev)
+    y = torch.empty((1, dim), dtype=torch.bfloat16, device=dev)
+    work = torch.empty(inter, dtype=torch.bfloat16, device=dev)
+    from stblarge_amd import _lib
+
+    lib = _lib.load()
+
+    def launch(i):
+        st = ops._stream()
+        _lib.check(lib.stbl_amd_expert_ffn(fmt, ops._ptr(y), ops._ptr(slots[i]), ops._ptr(x), 1, dim, inter, 1.0, 0.0,
+                                           0, 0, ops._ptr(work), st), "expert_ffn")
+
+    ms, n = timed_steps(torch, launch, copies, steps, warmup)
+    nbytes, offs = ops.expert_layout(fmt, dim, inter)
+    wbytes = sum(ops._mat_bytes(fmt, r, k) for r, k in ((inter, dim), (inter, dim), (dim, inter)))
+    alg = wbytes + 2 * dim + 2 * dim
+    gbs = alg / (ms * 1e-3) / 1e9
+    name = "fp4" if fmt == ops.FP4 else "fp8"
+    return {"workload": f"{name}_expert_ffn_7168x2048_m1", "ms_per_step": ms, "steps": n, "alg_bytes": alg,
+            "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS, "slot_copies": copies}
+
+
+def moe_workload(torch, tokens, steps, warmup_steps):
+    """C4: routed MoE layer decode, 256 FP4 experts (pinned host pool) + 1 shared, top-8, sigmoid
+    router on Zipf(1.1) Gumbel-top-k logits, 64-slot HBM LRU refilled over PCIe."""
+    import time as _t
+
+    from stblarge_amd import data, ops
+    from stblarge_amd.moe import MoELayer
+
+    dev = torch.device("cuda:0")
+    dim, inter, n_exp, topk, slots = data.DIM, data.INTER, data.N_EXPERTS, data.TOPK, data.CACHE_SLOTS
+    fmt = ops.FP4
+    sb, _ = ops.expert_layout(fmt, dim, inter)
+    pool = torch.empty(n_exp * sb, dtype=torch.uint8, pin_memory=True)
+    for e in range(n_exp):
+        s = ops.quant_expert(data.weight(inter, dim, 1000 + 3 * e, dev), data.weight(inter, dim, 1001 + 3 * e, dev),
+                             data.weight(dim, inter, 1002 + 3 * e, dev), fmt)
+        pool[e * sb:(e + 1) * sb].copy_(s, non_blocking=False)
+    shared = ops.quant_expert(data.weight(inter, dim, 7, dev), data.weight(inter, dim, 8, dev),
+                              data.weight(dim, inter, 9, dev), fmt)
+    layer = MoELayer(fmt, dim, inter, pool, n_exp, topk, slots, shared_slot=shared, max_tokens=tokens)
+    total = warmup_steps + steps
+    logits = data.zipf_logits(total * tokens, n_exp, seed=77).view(total, tokens, n_exp).to(dev)
+    x = data.activation(tokens, dim, seed=78, device=dev)
+    for i in range(warmup_steps):
+        layer.forward(x, logits[i])
+    torch.cuda.synchronize()
+    st0 = layer.cache.stats()
+    t0 = _t.perf_counter()
+    for i in range(warmup_steps, total):
+        layer.forward(x, logits[i])
+    torch.cuda.synchronize()
+    el = _t.perf_counter() - t0
+    st1 = layer.cache.stats()
+    hits, misses = st1["hits"] - st0["hits"], st1["misses"] - st0["misses"]
+    layer.close()
+    del pool
+    return {"workload": f"moe_layer_t{tokens}_fp4_256x_top8_lru64", "tokens": tokens, "steps": steps,
+            "ms_per_step": el * 1e3 / steps, "tokens_per_s": tokens * steps / el,
+            "hit_rate": hits / max(1, hits + misses), "misses_per_token": misses / (tokens * steps),
+            "refill_GB_s": (st1["refill_bytes"] - st0["refill_bytes"]) / el / 1e9}
+
+
+def moe_allhit_workload(torch, tokens, steps, warmup):
+    """C4's expert kernels alone with every expert resident (the kernel bound of the layer): per
+    step, each token's 8 routed experts are drawn from 64 resident slots (1.5 GB, so weights come
+    from HBM) plus the shared expert; algorithmic bytes = every distinct expert's weights once."""
+    import numpy as np
+
+    from stblarge_amd import data, ops
+
+    dev = torch.device("cuda:0")
+    dim, inter, topk, nres = data.DIM, data.INTER, data.TOPK, data.CACHE_SLOTS
+    fmt = ops.FP4
+    base = ops.quant_expert(data.weight(inter, dim, 21, dev), data.weight(inter, dim, 22, dev),
+                            data.weight(dim, inter, 23, dev), fmt)
+    res = [base.clone() for _ in range(nres + 1)]
+    wbytes = sum(ops._mat_bytes(fmt, r, k) for r, k in ((inter, dim), (inter, dim), (dim, inter)))
+    rng = np.random.default_rng(5)
+    plans = []
+    for _ in range(16):
+        pick = [list(rng.choice(nres, size=topk, replace=False)) for _ in range(tokens)]
+        uniq = sorted({e for row in pick for e in row})
+        slot_of = {e: i for i, e in enumerate(uniq)}
+        plans.append(([res[e] for e in uniq] + [res[nres]], [[slot_of[e] for e in row] for row in pick], len(uniq) + 1))
+    w = [[1.0 / topk] * topk for _ in range(tokens)]
+    x = data.activation(tokens, dim, seed=24, device=dev)
+    y = torch.empty((tokens, dim), dtype=torch.bfloat16, device=dev)
+    work = torch.empty(ops.moe_work_bytes(tokens, topk, dim, inter), dtype=torch.uint8, device=dev)
+
+    def launch(i):
+        sl, pick, _ = plans[i]
+        ops.moe_experts(x, sl, pick, w, fmt, dim, inter, shared=len(sl) - 1, work=work, out=y)
+
+    ms, n = timed_steps(torch, launch, len(plans), steps, warmup)
+    alg = np.mean([p[2] for p in plans]) * wbytes + 4 * dim * tokens
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"workload": f"moe_experts_allhit_t{tokens}_fp4", "ms_per_step": ms, "steps": n, "tokens_per_s":
+            tokens / (ms * 1e-3), "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS}
+
+
 def cpu_baseline(seconds):
     """The oracle's scalar C GEMV (oracle/stbl_oracle.c orc_gemv_fp4) on the headline workload's
     shape, one thread, repeated for about `seconds`."""
@@ -157,13 +271,33 @@ def main():
     print(f"# {head['workload']}: {head['ms_per_step'] * 1e3:.3f} us/step, {head['GB_s']:.0f} GB/s", file=sys.stderr,
           flush=True)
     extra = {}
-    if args.only != "fp4":
+    if args.only in ("all", "gemv"):
         for fmt, rows, k, m in (("fp4", 7168, 2048, 1), ("fp8", 2048, 7168, 1), ("fp8", 7168, 2048, 1),
                                 ("fp4", 2048, 7168, 4), ("fp8", 2048, 7168, 4)):
             r = gemv_workload(torch, fmt, rows, k, m, args.steps, args.warmup)
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
                   flush=True)
+    if args.only in ("all", "ffn"):
+        from stblarge_amd import ops
+
+        for fmt in (ops.FP4, ops.FP8):
+            r = ffn_workload(torch, fmt, max(200, args.steps // 4), args.warmup)
+            extra[r["workload"]] = r
+            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
+                  flush=True)
+    if args.only in ("all", "moe"):
+        for t in (1, 4):
+            r = moe_allhit_workload(torch, t, max(100, args.steps // 10), 32)
+            extra[r["workload"]] = r
+            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s, "
+                  f"{r['GB_s']:.0f} GB/s", file=sys.stderr, flush=True)
+        for t in (1, 4):
+            r = moe_workload(torch, t, args.moe_steps, args.moe_warmup)
+            extra[r["workload"]] = r
+            print(f"# {r['workload']}: {r['ms_per_step']:.3f} ms/step, {r['tokens_per_s']:.0f} tok/s, hit rate "
+                  f"{r['hit_rate']:.3f}, {r['misses_per_token']:.2f} misses/token, refill {r['refill_GB_s']:.1f} GB/s",
+                  file=sys.stderr, flush=True)
     if args.eager:
         r = gemv_workload(torch, "fp4", 2048, 7168, 1, args.steps, args.warmup, use_graph=False)
         extra["fp4_gemv_2048x7168_m1_eager"] = r

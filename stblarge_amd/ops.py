@@ -244,6 +244,13 @@ def expert_layout(fmt, dim, inter):
     return int(n), [int(o) for o in offs]
 
 
+def _mat_bytes(fmt, rows, k):
+    """Codes + scales bytes of one quantized [rows x k] matrix."""
+    if fmt == FP4:
+        return rows * k // 2 + rows * k // 32
+    return rows * k + 4 * ((rows + 127) // 128) * ((k + 127) // 128)
+
+
 def _mat_shapes(fmt, dim, inter):
     out = []
     for rows, k in ((inter, dim), (inter, dim), (dim, inter)):
