@@ -35,7 +35,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="all", help="fp4 (headline only) | gemv | ffn | moe | all")
+    ap.add_argument("--only", default="all", help="fp4 (headline only) | gemv | ffn | gemm | moe | all")
     ap.add_argument("--moe-steps", type=int, default=200)
     ap.add_argument("--moe-warmup", type=int, default=1000)
     ap.add_argument("--eager", action="store_true", help="also time launches issued one by one from Python")
@@ -225,6 +225,37 @@ def moe_allhit_workload(torch, tokens, steps, warmup):
             tokens / (ms * 1e-3), "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS}
 
 
+def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168):
+    """C5: multi-token expert GEMM, M = 64 tokens, W [2048 x 7168] FP4 or FP8 (scaled f8f6f4 MFMA)."""
+    from stblarge_amd import _lib, data, ops
+
+    dev = torch.device("cuda:0")
+    w = data.weight(n, k, seed=31, device=dev)
+    codes, scales = ops.quant_fp4(w) if fmt == ops.FP4 else ops.quant_fp8_b128(w)
+    del w
+    wbytes = ops._mat_bytes(fmt, n, k)
+    copies = max(2, math.ceil(ROTATE_BYTES / wbytes))
+    cs = [codes.clone() for _ in range(copies)]
+    ss = [scales.clone() for _ in range(copies)]
+    x = data.activation(m, k, seed=32, device=dev)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    work = torch.empty(int(_lib.load().stbl_amd_gemm_work_bytes(m, n, k)), dtype=torch.uint8, device=dev)
+    lib = _lib.load()
+
+    def launch(i):
+        _lib.check(lib.stbl_amd_gemm(fmt, ops._ptr(y), ops._ptr(cs[i]), ops._ptr(ss[i]), ops._ptr(x), m, n, k, 128, 0,
+                                     ops._ptr(work), ops._stream()), "gemm")
+
+    ms, nsteps = timed_steps(torch, launch, copies, steps, warmup)
+    alg = wbytes + 2 * m * k + 2 * m * n
+    flops = 2.0 * m * n * k
+    name = "fp4" if fmt == ops.FP4 else "fp8"
+    peak_tf = 5000.0  # e4m3 activations: the MFMA runs at the fp8 rate for both weight formats
+    return {"workload": f"{name}_gemm_m{m}_{n}x{k}", "ms_per_step": ms, "steps": nsteps, "alg_bytes": alg,
+            "GB_s": alg / (ms * 1e-3) / 1e9, "frac_hbm_peak": alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+            "TFLOP_s": flops / (ms * 1e-3) / 1e12, "frac_mfma_peak": flops / (ms * 1e-3) / 1e12 / peak_tf}
+
+
 def cpu_baseline(seconds):
     """The oracle's scalar C GEMV (oracle/stbl_oracle.c orc_gemv_fp4) on the headline workload's
     shape, one thread, repeated for about `seconds`."""
@@ -286,6 +317,14 @@ def main():
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
                   flush=True)
+    if args.only in ("all", "gemm"):
+        from stblarge_amd import ops
+
+        for fmt in (ops.FP4, ops.FP8):
+            r = gemm_workload(torch, fmt, max(200, args.steps // 4), args.warmup)
+            extra[r["workload"]] = r
+            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s, "
+                  f"{r['TFLOP_s']:.0f} TFLOP/s ({100 * r['frac_mfma_peak']:.1f}% MFMA)", file=sys.stderr, flush=True)
     if args.only in ("all", "moe"):
         for t in (1, 4):
             r = moe_allhit_workload(torch, t, max(100, args.steps // 10), 32)

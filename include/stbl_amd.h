@@ -151,6 +151,23 @@ uint64_t stbl_amd_moe_work_bytes(int t, int topk, int dim, int inter);
 int stbl_amd_route(const float *logits, const float *bias, int t, int n_exp, int topk, float route_scale, int *ids,
                    float *weights, float *scores, hipStream_t st);
 
+/* ---- v2: multi-token expert GEMM (ref/kernel.py:85-102 with M > 4, scaled f8f6f4 MFMA) ------------ */
+
+/* Y[m][n] = sum_k Aq[m][k] Wdeq[n][k], m <= 64, where Aq = act_quant(X, act_block, "ue8m0")
+ * (act_block 32 or 128: e4m3 codes with power-of-two scales) and W is FP4 (fmt 0: codes [n][k/2] +
+ * E8M0 [n][k/32]) or FP8 (fmt 1: codes [n][k] + fp32 [ceil(n/128)][k/128]). X bf16 [m][k], Y bf16
+ * [m][n] (fp32 when y_f32). k % 128 == 0. work: device scratch of stbl_amd_gemm_work_bytes() bytes.
+ * Replaces fp8_gemm / fp4_gemm(A = act_quant(X)) of ref/kernel.py:85-102. */
+int stbl_amd_gemm(int fmt, void *y, const void *codes, const void *scales, const void *x, int m, int n, int k,
+                  int act_block, int y_f32, void *work, hipStream_t st);
+
+/* Scratch bytes for stbl_amd_gemm. */
+uint64_t stbl_amd_gemm_work_bytes(int m, int n, int k);
+
+/* act_quant(x, block, "ue8m0") (ref/kernel.py:35-45) as the GEMM consumes it: x bf16 [rows][k] ->
+ * e4m3 codes [rows][k] and E8M0 scale bytes [rows][k/block]; block 32 or 128. */
+int stbl_amd_act_quant_e4m3(const void *x, int rows, int k, int block, void *codes, void *scales, hipStream_t st);
+
 /* ---- v2: HBM expert cache (stbl/model.cu:99-106, 347-422 ExpertCache / expert() / take_slot) -------- */
 
 /* Creates an LRU cache of `slots` expert slots of slot_bytes on the current device (allocates the

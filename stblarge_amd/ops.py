@@ -351,3 +351,41 @@ def route(logits, topk, bias=None, route_scale=1.0, want_scores=False):
     _lib.check(_lib.load().stbl_amd_route(_ptr(logits), _ptr(bias), t, e, topk, float(route_scale), _ptr(ids), _ptr(w),
                                           _ptr(sc), _stream()), "route")
     return (ids, w, sc) if want_scores else (ids, w)
+
+
+# ---- multi-token GEMM (scaled MFMA) ------------------------------------------------------------------
+
+def gemm(codes, scales, x, fmt, act_block=128, out_f32=False, work=None):
+    """Y [M, N] = act_quant(X, act_block) . Wdeq^T for M <= 64 (fp4_gemm / fp8_gemm of ref/kernel.py)."""
+    _need(x, torch.bfloat16, "x", 2)
+    m, k = x.shape
+    if fmt == FP4:
+        _need(codes, torch.uint8, "codes", 2)
+        _need(scales, torch.uint8, "scales", 2)
+        n = codes.shape[0]
+        ok = codes.shape[1] * 2 == k and tuple(scales.shape) == (n, k // 32)
+    else:
+        _need(codes, torch.uint8, "codes", 2)
+        _need(scales, torch.float32, "scales", 2)
+        n = codes.shape[0]
+        ok = codes.shape[1] == k and tuple(scales.shape) == ((n + 127) // 128, (k + 127) // 128)
+    if not ok:
+        raise ValueError(f"shape mismatch: codes {tuple(codes.shape)}, scales {tuple(scales.shape)}, x {tuple(x.shape)}")
+    nbytes = int(_lib.load().stbl_amd_gemm_work_bytes(m, n, k))
+    if work is None or work.numel() < nbytes:
+        work = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=x.device)
+    _lib.check(_lib.load().stbl_amd_gemm(fmt, _ptr(y), _ptr(codes), _ptr(scales), _ptr(x), m, n, k, act_block,
+                                         int(out_f32), _ptr(work), _stream()), "gemm")
+    return y
+
+
+def act_quant_e4m3(x, block=128):
+    """(e4m3 codes uint8 [rows, k], E8M0 scale bytes uint8 [rows, k/block]) of bf16 x."""
+    _need(x, torch.bfloat16, "x", 2)
+    rows, k = x.shape
+    codes = torch.empty((rows, k), dtype=torch.uint8, device=x.device)
+    scales = torch.empty((rows, k // block), dtype=torch.uint8, device=x.device)
+    _lib.check(_lib.load().stbl_amd_act_quant_e4m3(_ptr(x), rows, k, block, _ptr(codes), _ptr(scales), _stream()),
+               "act_quant_e4m3")
+    return codes, scales

@@ -1,0 +1,69 @@
+"""GPU parity of the multi-token GEMM (scaled f8f6f4 MFMA) against the oracle.
+
+Oracle: act_quant(X, block, ue8m0) (ref/kernel.py:35-45) then Aq . Wdeq^T in double (ref/kernel.py:
+85-102). Bar: fp32 output within 1e-3 normwise (the reference's check() metric); the bf16 output is
+exactly our fp32 output rounded, and within 1e-3 + one bf16 half-step normwise. The MFMA's internal
+accumulation is not IEEE fp32 round-per-add (about 1e-4 relative on a 128-term step, measured), so
+outputs near zero can be many bf16 steps from the oracle while the normwise error stays ~1e-4; an
+elementwise ulp bar does not apply here.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from stblarge_amd import data, ops
+from util import bits_equal, np_, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("block", [32, 128])
+def test_act_quant_e4m3_bit_exact(gpu, block):
+    x = (data.normal((64, 7168), 1.0, seed=block) * torch.logspace(-2, 2, 7168)).to(torch.bfloat16)
+    x[3, :block] = 0
+    codes, sc = ops.act_quant_e4m3(x.to(gpu), block)
+    oc, os_, _ = oracle.act_quant(x.float().numpy(), block, True)
+    assert np.array_equal(np_(codes), oc)
+    assert bits_equal((np_(sc).astype(np.uint32) << 23).view(np.float32), os_)
+
+
+def _check(y32, y16, want):
+    e = rel_err(y32, want)
+    print(f"gemm relative error {e:.2e}")
+    assert e <= 1e-3, e
+    assert np.array_equal(y16, oracle.bf16_round(y32))
+    assert rel_err(y16, want) <= 1e-3 + 2.0 ** -8  # bf16 half-step is up to 2^-8 relative
+
+
+def _oracle_gemm(x, w_deq, block):
+    oc, os_, _ = oracle.act_quant(x.float().numpy(), block, True)
+    k = oc.shape[1]
+    a = (oracle.e4m3_decode(oc).reshape(oc.shape[0], k // block, block) * os_[..., None]).reshape(-1, k)
+    return oracle.gemm(a, w_deq)
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 2048, 7168), (64, 7168, 2048), (16, 256, 512), (37, 200, 384)])
+@pytest.mark.parametrize("block", [32, 128])
+def test_gemm_fp4(gpu, m, n, k, block):
+    w = data.weight(n, k, seed=n + k)
+    codes, scales = oracle.quant_fp4(w.numpy())
+    x = data.activation(m, k, seed=m)
+    want = _oracle_gemm(x, oracle.dequant_fp4(codes, scales), block)
+    dc, ds = torch.from_numpy(codes).to(gpu), torch.from_numpy(scales).to(gpu)
+    y32 = np_(ops.gemm(dc, ds, x.to(gpu), ops.FP4, block, out_f32=True))
+    y16 = np_(ops.gemm(dc, ds, x.to(gpu), ops.FP4, block))
+    _check(y32, y16, want)
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 2048, 7168), (64, 7168, 2048), (16, 256, 512), (37, 200, 384)])
+def test_gemm_fp8(gpu, m, n, k):
+    w = data.weight(n, k, seed=3 * n + k)
+    codes, scales = oracle.quant_fp8_b128(w.numpy())
+    x = data.activation(m, k, seed=m + 1)
+    want = _oracle_gemm(x, oracle.dequant_fp8_b128(codes, scales), 128)
+    dc, ds = torch.from_numpy(codes).to(gpu), torch.from_numpy(scales).to(gpu)
+    y32 = np_(ops.gemm(dc, ds, x.to(gpu), ops.FP8, 128, out_f32=True))
+    y16 = np_(ops.gemm(dc, ds, x.to(gpu), ops.FP8, 128))
+    _check(y32, y16, want)
