@@ -39,6 +39,10 @@ def parse():
     ap.add_argument("--moe-steps", type=int, default=200)
     ap.add_argument("--moe-warmup", type=int, default=1000)
     ap.add_argument("--eager", action="store_true", help="also time launches issued one by one from Python")
+    ap.add_argument("--no-graph", action="store_true", help="launch every step from Python (for counter runs)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="after the workloads, copy 64 MiB device to device 5 times (the reference transfer for "
+                         "scaling HBM byte counters)")
     return ap.parse_args()
 
 
@@ -256,6 +260,19 @@ def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168):
             "TFLOP_s": flops / (ms * 1e-3) / 1e12, "frac_mfma_peak": flops / (ms * 1e-3) / 1e12 / peak_tf}
 
 
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3 counter summary
+    (profiles/gemv_fp4_2048x7168_traffic.md, line `traffic_bytes_per_launch: N`), or None."""
+    path = os.path.join(ROOT, "profiles", "gemv_fp4_2048x7168_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(seconds):
     """The oracle's scalar C GEMV (oracle/stbl_oracle.c orc_gemv_fp4) on the headline workload's
     shape, one thread, repeated for about `seconds`."""
@@ -298,7 +315,7 @@ def main():
 
     _lib.load()  # fails loudly when the library was not built
 
-    head = gemv_workload(torch, "fp4", 2048, 7168, 1, args.steps, args.warmup)
+    head = gemv_workload(torch, "fp4", 2048, 7168, 1, args.steps, args.warmup, use_graph=not args.no_graph)
     print(f"# {head['workload']}: {head['ms_per_step'] * 1e3:.3f} us/step, {head['GB_s']:.0f} GB/s", file=sys.stderr,
           flush=True)
     extra = {}
@@ -341,6 +358,12 @@ def main():
         r = gemv_workload(torch, "fp4", 2048, 7168, 1, args.steps, args.warmup, use_graph=False)
         extra["fp4_gemv_2048x7168_m1_eager"] = r
         print(f"# eager launches: {r['ms_per_step'] * 1e3:.3f} us/step", file=sys.stderr, flush=True)
+    if args.copy_calib:
+        a = torch.empty(64 << 20, dtype=torch.uint8, device="cuda:0")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     gbs = head["GB_s"]
     line = {
@@ -359,7 +382,7 @@ def main():
         "config": {"workload": head["workload"], "rows": 2048, "k": 7168, "m": 1,
                    "weight_copies": head["weight_copies"], "rotation_MB": round(head["weight_copies"] * 7.8, 1)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "extra": extra,
     }
