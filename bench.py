@@ -117,6 +117,34 @@ def gemv_workload(torch, fmt, rows, k, m, steps, warmup, use_graph=True):
             "graph": use_graph}
 
 
+def gemv_batch_workload(torch, fmt, rows, k, steps, warmup, nb=16):
+    """Sustained GEMV bandwidth: nb same-shape GEMVs per launch (the reference's kMxBatch batching,
+    stbl/kernels.h:18-20), every launch on nb different weight matrices from a >= 512 MB rotation."""
+    from stblarge_amd import data, ops
+
+    dev = torch.device("cuda:0")
+    w = data.weight(rows, k, seed=1, device=dev)
+    codes, scales = ops.quant_fp4(w) if fmt == "fp4" else ops.quant_fp8_b128(w)
+    del w
+    wbytes = codes.numel() + scales.numel() * scales.element_size()
+    groups = max(2, math.ceil(ROTATE_BYTES / (nb * wbytes)))
+    cs = [[codes.clone() for _ in range(nb)] for _ in range(groups)]
+    ss = [[scales.clone() for _ in range(nb)] for _ in range(groups)]
+    xs = [data.activation(1, k, seed=2, device=dev) for _ in range(nb)]
+    ys = [torch.empty((1, rows), dtype=torch.bfloat16, device=dev) for _ in range(nb)]
+    f = ops.FP4 if fmt == "fp4" else ops.FP8
+
+    def launch(i):
+        ops.gemv_batch(cs[i], ss[i], xs, f, outs=ys)
+
+    ms, n = timed_steps(torch, launch, groups, max(20, steps // nb), max(4, warmup // nb))
+    per = data.algorithmic_bytes_fp4(rows, k, 1) if fmt == "fp4" else data.algorithmic_bytes_fp8(rows, k, 1)
+    alg = nb * per
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"workload": f"{fmt}_gemv_batch{nb}_{rows}x{k}_m1", "ms_per_launch": ms, "gemv_per_launch": nb,
+            "launches": n, "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS}
+
+
 def ffn_workload(torch, fmt, steps, warmup):
     """C3: one expert FFN (gate/up + SwiGLU, down) at dim 7168, inter 2048, one token."""
     from stblarge_amd import data, ops
@@ -326,6 +354,12 @@ def main():
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
                   flush=True)
+    if args.only in ("all", "gemv", "batch"):
+        for fmt, rows, k in (("fp4", 7168, 2048), ("fp4", 2048, 7168), ("fp8", 7168, 2048), ("fp8", 2048, 7168)):
+            r = gemv_batch_workload(torch, fmt, rows, k, args.steps, args.warmup)
+            extra[r["workload"]] = r
+            print(f"# {r['workload']}: {r['ms_per_launch'] * 1e3:.2f} us/launch of 16, {r['GB_s']:.0f} GB/s "
+                  f"({100 * r['frac_hbm_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
     if args.only in ("all", "ffn"):
         from stblarge_amd import ops
 
@@ -342,13 +376,13 @@ def main():
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s, "
                   f"{r['TFLOP_s']:.0f} TFLOP/s ({100 * r['frac_mfma_peak']:.1f}% MFMA)", file=sys.stderr, flush=True)
-    if args.only in ("all", "moe"):
+    if args.only in ("all", "moe", "moeallhit"):
         for t in (1, 4):
             r = moe_allhit_workload(torch, t, max(100, args.steps // 10), 32)
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s, "
                   f"{r['GB_s']:.0f} GB/s", file=sys.stderr, flush=True)
-        for t in (1, 4):
+        for t in ((1, 4) if args.only != "moeallhit" else ()):
             r = moe_workload(torch, t, args.moe_steps, args.moe_warmup)
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step']:.3f} ms/step, {r['tokens_per_s']:.0f} tok/s, hit rate "

@@ -33,6 +33,8 @@ SIGNATURES = {
     # v2
     "stbl_amd_gemv_fp4": (I, [P, P, P, P, I, I, I, I, P]),
     "stbl_amd_gemv_fp8": (I, [P, P, P, P, I, I, I, I, P]),
+    "stbl_amd_gemv_fp4_batch": (I, [PP, PP, PP, PP, I, I, I, I, I, P]),
+    "stbl_amd_gemv_fp8_batch": (I, [PP, PP, PP, PP, I, I, I, I, I, P]),
     "stbl_amd_act_quant": (I, [P, I, I, I, I, P, P, P, P]),
     "stbl_amd_quant_fp4": (I, [P, P, P, I, I, P]),
     "stbl_amd_quant_fp8_b128": (I, [P, P, P, I, I, P]),

@@ -33,9 +33,13 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     const int cc = active ? c : 0;
     const int row0 = blockIdx.x * R;
 
-    // 1. loads: x first (it is needed by every row), then every row of the tile
-    float xf[M][CH];
-    load_x<XF32, M, CH>(xf, J.x, k, cc * CH);
+    // 1. loads: x first (it is needed by every row), then every row of the tile. fp32 activations
+    //    (the reference ABI) are widened once and use exact FMAs; bf16 activations stay packed for
+    //    the dot2 path (gemv_core.hpp).
+    float xf[XF32 ? M : 1][XF32 ? CH : 1];
+    uint32_t xw[XF32 ? 1 : M][XF32 ? 1 : CH / 2];
+    if constexpr (XF32) load_x<true, M, CH>(xf, J.x, k, cc * CH);
+    else load_x_packed<M, CH>(xw, (const uint16_t *)J.x, k, cc * CH);
     u32x4 w[R];
     uint32_t sb[R];
 #pragma unroll
@@ -62,7 +66,8 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
 #pragma unroll
     for (int r = 0; r < R; r++) {
         float s[M];
-        chunk_dot<F, M, CH>(s, w[r], xf);
+        if constexpr (XF32) chunk_dot<F, M, CH>(s, w[r], xf);
+        else chunk_dot_packed<F, M, CH>(s, w[r], xw);
         float scale;
         if constexpr (T::fp4) scale = e8m0_to_f32(sb[r]);
         else if constexpr (F == WFmt::FP8_B128) scale = lscale;
@@ -100,35 +105,53 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
 
 static inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
-template <WFmt F, bool XF32, int M>
-static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int out_mode, hipStream_t st) {
-    constexpr int R = M <= 2 ? 2 : 1;
+template <WFmt F, bool XF32, int M, int R>
+static hipError_t launch_r(const GemvJobs &jobs, int njobs, int rows, int k, int out_mode, hipStream_t st) {
     const int waves = ceil_div(k / WTraits<F>::CH, 64);
     hipLaunchKernelGGL((k_gemv<F, XF32, M, R>), dim3(ceil_div(rows, R), njobs), dim3(64 * waves), 0, st, jobs, rows,
                        k, out_mode);
     return hipGetLastError();
 }
 
-// v2 dispatch over the token count.
+// Rows per workgroup: 2 keeps a single matrix spread over every CU (1024+ workgroups at the
+// configurations' shapes); a launch with much more work (batched matrices) takes 8 rows per
+// workgroup, so the fixed per-workgroup cost (x chunk, prologue, reduction) is spread over 4x the
+// weight bytes while still leaving thousands of workgroups.
+template <WFmt F, bool XF32, int M>
+static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int out_mode, hipStream_t st) {
+    if constexpr (M > 2) return launch_r<F, XF32, M, 1>(jobs, njobs, rows, k, out_mode, st);
+    else {
+        const long wgs8 = (long)ceil_div(rows, 8) * njobs * ceil_div(k / WTraits<F>::CH, 64);
+        if (wgs8 >= 8192) return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
+        return launch_r<F, XF32, M, 2>(jobs, njobs, rows, k, out_mode, st);
+    }
+}
+
+// v2 dispatch over the token count: n <= 16 same-shape matrices (host arrays of device pointers).
 template <WFmt F>
-static int gemv_v2(const char *name, void *y, const void *w, const void *s, const void *x, int m, int rows, int k,
-                   int y_f32, hipStream_t st) {
+static int gemv_v2(const char *name, void *const *y, const void *const *w, const void *const *s,
+                   const void *const *x, int n, int m, int rows, int k, int y_f32, hipStream_t st) {
     constexpr int CH = WTraits<F>::CH;
-    if (!y || !w || !s || !x) return abi_fail(hipErrorInvalidValue, "%s: null pointer", name);
+    if (!y || !w || !s || !x || n < 1 || n > kMaxJobs)
+        return abi_fail(hipErrorInvalidValue, "%s: need 1..%d matrices (n=%d)", name, kMaxJobs, n);
     if (rows <= 0 || k <= 0 || k % CH != 0 || k / CH > kMaxWaves * 64)
         return abi_fail(hipErrorInvalidValue, "%s: need k %% %d == 0 and 0 < k <= %d (k=%d)", name, CH,
                         kMaxWaves * 64 * CH, k);
     if (m < 1 || m > 4) return abi_fail(hipErrorInvalidValue, "%s: m must be 1..4 (m=%d); use the GEMM for more", name, m);
-    if (!aligned16(w) || !aligned16(x)) return abi_fail(hipErrorInvalidValue, "%s: weights and x must be 16-byte aligned", name);
     GemvJobs jobs = {};
-    jobs.j[0] = GemvJob{(const uint8_t *)w, s, x, y};
+    for (int j = 0; j < n; j++) {
+        if (!y[j] || !w[j] || !s[j] || !x[j]) return abi_fail(hipErrorInvalidValue, "%s: matrix %d: null pointer", name, j);
+        if (!aligned16(w[j]) || !aligned16(x[j]))
+            return abi_fail(hipErrorInvalidValue, "%s: matrix %d: weights and x must be 16-byte aligned", name, j);
+        jobs.j[j] = GemvJob{(const uint8_t *)w[j], s[j], x[j], y[j]};
+    }
     const int mode = y_f32 ? OUT_F32 : OUT_BF16;
     hipError_t e;
     switch (m) {
-        case 1: e = launch<F, false, 1>(jobs, 1, rows, k, mode, st); break;
-        case 2: e = launch<F, false, 2>(jobs, 1, rows, k, mode, st); break;
-        case 3: e = launch<F, false, 3>(jobs, 1, rows, k, mode, st); break;
-        default: e = launch<F, false, 4>(jobs, 1, rows, k, mode, st); break;
+        case 1: e = launch<F, false, 1>(jobs, n, rows, k, mode, st); break;
+        case 2: e = launch<F, false, 2>(jobs, n, rows, k, mode, st); break;
+        case 3: e = launch<F, false, 3>(jobs, n, rows, k, mode, st); break;
+        default: e = launch<F, false, 4>(jobs, n, rows, k, mode, st); break;
     }
     return abi_status(e, name);
 }
@@ -141,12 +164,26 @@ extern "C" {
 
 int stbl_amd_gemv_fp4(void *y, const void *codes, const void *scales, const void *x, int m, int rows, int k,
                       int y_f32, hipStream_t st) {
-    return gemv_v2<WFmt::FP4_OCP>("gemv_fp4", y, codes, scales, x, m, rows, k, y_f32, st);
+    const void *sc = scales;
+    return gemv_v2<WFmt::FP4_OCP>("gemv_fp4", &y, &codes, &sc, &x, 1, m, rows, k, y_f32, st);
 }
 
 int stbl_amd_gemv_fp8(void *y, const void *codes, const float *scales, const void *x, int m, int rows, int k,
                       int y_f32, hipStream_t st) {
-    return gemv_v2<WFmt::FP8_B128>("gemv_fp8", y, codes, scales, x, m, rows, k, y_f32, st);
+    const void *sc = scales;
+    return gemv_v2<WFmt::FP8_B128>("gemv_fp8", &y, &codes, &sc, &x, 1, m, rows, k, y_f32, st);
+}
+
+// n <= 16 same-shape GEMVs in one launch (the batching of stbl_gemv_mxfp4_batch, stbl/kernels.h:18-20,
+// in the v2 formats). All pointer arguments are HOST arrays of n device pointers.
+int stbl_amd_gemv_fp4_batch(void *const *y, const void *const *codes, const void *const *scales, const void *const *x,
+                            int n, int m, int rows, int k, int y_f32, hipStream_t st) {
+    return gemv_v2<WFmt::FP4_OCP>("gemv_fp4_batch", y, codes, scales, x, n, m, rows, k, y_f32, st);
+}
+
+int stbl_amd_gemv_fp8_batch(void *const *y, const void *const *codes, const void *const *scales, const void *const *x,
+                            int n, int m, int rows, int k, int y_f32, hipStream_t st) {
+    return gemv_v2<WFmt::FP8_B128>("gemv_fp8_batch", y, codes, scales, x, n, m, rows, k, y_f32, st);
 }
 
 // stbl/kernels.h:14-15. Requires k % 32 == 0 and 16-byte aligned rows, as the reference does.

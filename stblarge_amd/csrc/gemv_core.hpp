@@ -148,4 +148,84 @@ __device__ __forceinline__ void act_quant_chunk(float (&xf)[M][CH]) {
     }
 }
 
+// ---- packed-bf16 path (v2 formats): weights converted to bf16 pairs, v_dot2_f32_bf16 ---------------
+//
+// With bf16 activations the lane keeps its x chunk as packed bf16 words (word i = elements 2i, 2i+1)
+// and each pair of weights is converted straight to a bf16 pair (exactly: e2m1 and e4m3 values are
+// bf16 values) and multiplied into the sum by one v_dot2_f32_bf16: per 32 FP4 elements 16
+// conversions + 16 dot2 instead of 16 conversions + 32 FMAs, which is what keeps a CU ahead of its
+// share of HBM bandwidth. The dot2 products are exact; its internal sum can differ from an IEEE fp32
+// addition in the last bits.
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+template <int M, int CH>
+__device__ __forceinline__ void load_x_packed(uint32_t (&xw)[M][CH / 2], const uint16_t *x, int k, int k0) {
+#pragma unroll
+    for (int t = 0; t < M; t++) {
+        const u32x4 *p = (const u32x4 *)(x + (size_t)t * k + k0);
+#pragma unroll
+        for (int q = 0; q < CH / 8; q++) {
+            const u32x4 v = p[q];
+#pragma unroll
+            for (int j = 0; j < 4; j++) xw[t][4 * q + j] = v[j];
+        }
+    }
+}
+
+// act_quant_chunk on packed words: the quantized values are bf16 values, so they pack back exactly.
+template <int M, int CH>
+__device__ __forceinline__ void act_quant_packed(uint32_t (&xw)[M][CH / 2]) {
+    float xf[M][CH];
+#pragma unroll
+    for (int t = 0; t < M; t++)
+#pragma unroll
+        for (int i = 0; i < CH / 2; i++) xf[t][2 * i] = bf16_lo(xw[t][i]), xf[t][2 * i + 1] = bf16_hi(xw[t][i]);
+    act_quant_chunk<M, CH>(xf);
+#pragma unroll
+    for (int t = 0; t < M; t++)
+#pragma unroll
+        for (int i = 0; i < CH / 2; i++)
+            xw[t][i] = (__float_as_uint(xf[t][2 * i]) >> 16) | (__float_as_uint(xf[t][2 * i + 1]) & 0xffff0000u);
+}
+
+__device__ __forceinline__ float dot2(bf16x2 w, uint32_t x, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(w, __builtin_bit_cast(bf16x2, x), acc, false);
+}
+
+// sum over the chunk of x * (unscaled) weight for each token; OCP FP4 or FP8 weights.
+template <WFmt F, int M, int CH>
+__device__ __forceinline__ void chunk_dot_packed(float (&s)[M], const u32x4 w, const uint32_t (&xw)[M][CH / 2]) {
+    static_assert(F == WFmt::FP4_OCP || F == WFmt::FP8_B128 || F == WFmt::FP8_E8M0, "packed path: OCP FP4 or FP8");
+    float s2[M];
+#pragma unroll
+    for (int t = 0; t < M; t++) s[t] = 0.f, s2[t] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        if constexpr (F == WFmt::FP4_OCP) {  // byte b of dword d: elements 8d + 2b, +1 = x word 4d + b
+            const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 0);
+            const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 1);
+            const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 2);
+            const bf16x2 e = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 3);
+#pragma unroll
+            for (int t = 0; t < M; t++) {
+                s[t] = dot2(a, xw[t][4 * d], s[t]);
+                s2[t] = dot2(b, xw[t][4 * d + 1], s2[t]);
+                s[t] = dot2(c, xw[t][4 * d + 2], s[t]);
+                s2[t] = dot2(e, xw[t][4 * d + 3], s2[t]);
+            }
+        } else {  // bytes 0,1 / 2,3 of dword d: elements 4d, 4d+1 / 4d+2, 4d+3 = x words 2d / 2d+1
+            const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[d], 1.0f, false);
+            const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[d], 1.0f, true);
+#pragma unroll
+            for (int t = 0; t < M; t++) {
+                s[t] = dot2(a, xw[t][2 * d], s[t]);
+                s2[t] = dot2(b, xw[t][2 * d + 1], s2[t]);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < M; t++) s[t] += s2[t];
+}
+
 }  // namespace stbl

@@ -105,13 +105,13 @@ __global__ __launch_bounds__(512) void k_moe_gateup(MoeJobs jobs, ExpertLayout L
     const int row0 = blockIdx.x * R;
     const int m = J.m;
 
-    float xf[M][CH];
+    uint32_t xw[M][CH / 2];
 #pragma unroll
     for (int t = 0; t < M; t++) {
-        float tmp[1][CH];
-        load_x<false, 1, CH>(tmp, x + (size_t)J.tok[t < m ? t : 0] * dim, dim, cc * CH);
+        uint32_t tmp[1][CH / 2];
+        load_x_packed<1, CH>(tmp, x + (size_t)J.tok[t < m ? t : 0] * dim, dim, cc * CH);
 #pragma unroll
-        for (int i = 0; i < CH; i++) xf[t][i] = tmp[0][i];
+        for (int i = 0; i < CH / 2; i++) xw[t][i] = tmp[0][i];
     }
     u32x4 wg[R], wu[R];
     uint32_t sg[R], su[R];
@@ -123,15 +123,15 @@ __global__ __launch_bounds__(512) void k_moe_gateup(MoeJobs jobs, ExpertLayout L
     }
     float lg = 1.f, lu = 1.f;
     if constexpr (!WTraits<F>::fp4) lg = G.block_scale(row0, cc), lu = U.block_scale(row0, cc);
-    if (official) act_quant_chunk<M, CH>(xf);
+    if (official) act_quant_packed<M, CH>(xw);
 
     __shared__ float red[kMaxWaves][2 * M * R];
     float tot[2 * M * R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         float sgv[M], suv[M];
-        chunk_dot<F, M, CH>(sgv, wg[r], xf);
-        chunk_dot<F, M, CH>(suv, wu[r], xf);
+        chunk_dot_packed<F, M, CH>(sgv, wg[r], xw);
+        chunk_dot_packed<F, M, CH>(suv, wu[r], xw);
         const float a = chunk_scale<F>(sg[r], lg), b = chunk_scale<F>(su[r], lu);
 #pragma unroll
         for (int t = 0; t < M; t++) {
@@ -170,13 +170,13 @@ __global__ __launch_bounds__(512) void k_moe_down(MoeJobs jobs, ExpertLayout L, 
     const int row0 = blockIdx.x * R;
     const int m = J.m;
 
-    float xf[M][CH];
+    uint32_t xw[M][CH / 2];
 #pragma unroll
     for (int t = 0; t < M; t++) {
-        float tmp[1][CH];
-        load_x<false, 1, CH>(tmp, h + (size_t)J.pair[t < m ? t : 0] * inter, inter, cc * CH);
+        uint32_t tmp[1][CH / 2];
+        load_x_packed<1, CH>(tmp, h + (size_t)J.pair[t < m ? t : 0] * inter, inter, cc * CH);
 #pragma unroll
-        for (int i = 0; i < CH; i++) xf[t][i] = tmp[0][i];
+        for (int i = 0; i < CH / 2; i++) xw[t][i] = tmp[0][i];
     }
     u32x4 wd[R];
     uint32_t sd[R];
@@ -184,14 +184,14 @@ __global__ __launch_bounds__(512) void k_moe_down(MoeJobs jobs, ExpertLayout L, 
     for (int r = 0; r < R; r++) D.load((size_t)min(row0 + r, dim - 1), cc, wd[r], sd[r]);
     float ld = 1.f;
     if constexpr (!WTraits<F>::fp4) ld = D.block_scale(row0, cc);
-    if (official) act_quant_chunk<M, CH>(xf);
+    if (official) act_quant_packed<M, CH>(xw);
 
     __shared__ float red[kMaxWaves][M * R];
     float tot[M * R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         float s[M];
-        chunk_dot<F, M, CH>(s, wd[r], xf);
+        chunk_dot_packed<F, M, CH>(s, wd[r], xw);
         const float a = chunk_scale<F>(sd[r], ld);
 #pragma unroll
         for (int t = 0; t < M; t++) tot[t * R + r] = dpp_sum(active ? s[t] * a : 0.f);
@@ -299,7 +299,7 @@ static hipError_t launch_gateup(const MoeJobs &jobs, int n, const ExpertLayout &
 template <WFmt F, int M>
 static hipError_t launch_down(const MoeJobs &jobs, int n, const ExpertLayout &L, const uint16_t *h, void *o, int dim,
                               int inter, int official, int out_f32, hipStream_t st) {
-    constexpr int R = M == 1 ? 4 : 2;
+    constexpr int R = M == 1 ? 8 : 2;
     const int waves = ceil_div(inter / WTraits<F>::CH, 64);
     hipLaunchKernelGGL((k_moe_down<F, M, R>), dim3(ceil_div(dim, R), n), dim3(64 * waves), 0, st, jobs, L, h, o, dim,
                        inter, official, out_f32);

@@ -47,6 +47,9 @@ def _rows2(x):
     return x if x.dim() == 2 else x.view(1, -1)
 
 
+FP4, FP8 = 0, 1
+
+
 # ---- quantizers / dequantizers --------------------------------------------------------------------
 
 def quant_fp4(w):
@@ -157,6 +160,31 @@ def gemv_fp8(codes, scales, x, out_f32=False, out=None):
     return y
 
 
+def gemv_batch(codes, scales, xs, fmt, out_f32=False, outs=None):
+    """len(codes) <= 16 same-shape GEMVs in one launch: ys[j] = gemv(codes[j], scales[j], xs[j])."""
+    n = len(codes)
+    if not (len(scales) == n == len(xs)) or n == 0 or n > 16:
+        raise ValueError("gemv_batch: need 1..16 matching codes/scales/x")
+    rows = codes[0].shape[0]
+    k = codes[0].shape[1] * (2 if fmt == FP4 else 1)
+    sdt = torch.uint8 if fmt == FP4 else torch.float32
+    m = _rows2(xs[0]).shape[0]
+    for c, s_, x in zip(codes, scales, xs):
+        _need(c, torch.uint8, "codes", 2)
+        _need(s_, sdt, "scales", 2)
+        _need(x, torch.bfloat16, "x")
+        if tuple(c.shape) != tuple(codes[0].shape) or tuple(_rows2(x).shape) != (m, k):
+            raise ValueError("gemv_batch: all matrices and activations must have one shape")
+    ys = outs if outs is not None else [torch.empty((m, rows), dtype=torch.float32 if out_f32 else torch.bfloat16,
+                                                    device=codes[0].device) for _ in range(n)]
+    arr = ctypes.c_void_p * n
+    fn = _lib.load().stbl_amd_gemv_fp4_batch if fmt == FP4 else _lib.load().stbl_amd_gemv_fp8_batch
+    _lib.check(fn(arr(*[y.data_ptr() for y in ys]), arr(*[c.data_ptr() for c in codes]),
+                  arr(*[s_.data_ptr() for s_ in scales]), arr(*[x.data_ptr() for x in xs]), n, m, rows, k,
+                  int(out_f32), _stream()), "gemv_batch")
+    return ys
+
+
 # ---- the reference engine's operator surface (stbl/kernels.h), fp32 activation buffers ---------------
 
 def stbl_act_quant_fp8(x):
@@ -233,8 +261,6 @@ def stbl_axpy(y, x, a, n):
 
 
 # ---- expert FFN / MoE / router (v2) ------------------------------------------------------------------
-
-FP4, FP8 = 0, 1
 
 
 def expert_layout(fmt, dim, inter):

@@ -133,3 +133,23 @@ def test_stbl_gemv_mxfp4_batch(gpu):
     ops.stbl_gemv_mxfp4_batch(ys, ws, xs, rows, k)
     for y, want in zip(ys, wants):
         assert_gemv(np_(y), np_(y), want, tol=2.0 ** -8)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_gemv_batch(gpu, fmt):
+    # 16 same-shape GEMVs in one launch (stbl_gemv_mxfp4_batch's batching, v2 formats), M = 2
+    rows, k, n, m = 256, 1024, 16, 2
+    q = oracle.quant_fp4 if fmt == 0 else oracle.quant_fp8_b128
+    ref = oracle.gemv_fp4 if fmt == 0 else oracle.gemv_fp8_b128
+    cs, ss, xs, wants = [], [], [], []
+    for j in range(n):
+        c, s = q(data.weight(rows, k, seed=500 + j).numpy())
+        x = data.activation(m, k, seed=600 + j)
+        wants.append(ref(c, s, x.float().numpy()))
+        cs.append(torch.from_numpy(c).to(gpu))
+        ss.append(torch.from_numpy(s).to(gpu))
+        xs.append(x.to(gpu))
+    ys = ops.gemv_batch(cs, ss, xs, fmt, out_f32=True)
+    ys16 = ops.gemv_batch(cs, ss, xs, fmt)
+    for y, y16, want in zip(ys, ys16, wants):
+        assert_gemv(np_(y), np_(y16), want)
