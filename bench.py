@@ -257,8 +257,10 @@ def moe_allhit_workload(torch, tokens, steps, warmup):
             tokens / (ms * 1e-3), "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS}
 
 
-def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168):
-    """C5: multi-token expert GEMM, M = 64 tokens, W [2048 x 7168] FP4 or FP8 (scaled f8f6f4 MFMA)."""
+def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168, prequant=False):
+    """C5: multi-token expert GEMM, M = 64 tokens, W [2048 x 7168] FP4 or FP8 (scaled f8f6f4 MFMA).
+    prequant: the activations are quantized outside the timed region and the GEMM proper is timed
+    (stbl_amd_gemm_q, fp8_gemm(a, a_s, b, b_s)'s form); otherwise act_quant + GEMM (stbl_amd_gemm)."""
     from stblarge_amd import _lib, data, ops
 
     dev = torch.device("cuda:0")
@@ -270,21 +272,26 @@ def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168):
     cs = [codes.clone() for _ in range(copies)]
     ss = [scales.clone() for _ in range(copies)]
     x = data.activation(m, k, seed=32, device=dev)
+    aq, a_s = ops.act_quant_e4m3(x, 128)
     y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-    work = torch.empty(int(_lib.load().stbl_amd_gemm_work_bytes(m, n, k)), dtype=torch.uint8, device=dev)
+    work = ops.gemm_work(m, n, k, dev)
     lib = _lib.load()
 
     def launch(i):
-        _lib.check(lib.stbl_amd_gemm(fmt, ops._ptr(y), ops._ptr(cs[i]), ops._ptr(ss[i]), ops._ptr(x), m, n, k, 128, 0,
-                                     ops._ptr(work), ops._stream()), "gemm")
+        if prequant:
+            _lib.check(lib.stbl_amd_gemm_q(fmt, ops._ptr(y), ops._ptr(cs[i]), ops._ptr(ss[i]), ops._ptr(aq),
+                                           ops._ptr(a_s), m, n, k, 128, 0, ops._ptr(work), ops._stream()), "gemm_q")
+        else:
+            _lib.check(lib.stbl_amd_gemm(fmt, ops._ptr(y), ops._ptr(cs[i]), ops._ptr(ss[i]), ops._ptr(x), m, n, k,
+                                         128, 0, ops._ptr(work), ops._stream()), "gemm")
 
     ms, nsteps = timed_steps(torch, launch, copies, steps, warmup)
-    alg = wbytes + 2 * m * k + 2 * m * n
+    alg = wbytes + (m * k + m * k // 128 if prequant else 2 * m * k) + 2 * m * n
     flops = 2.0 * m * n * k
     name = "fp4" if fmt == ops.FP4 else "fp8"
     peak_tf = 5000.0  # e4m3 activations: the MFMA runs at the fp8 rate for both weight formats
-    return {"workload": f"{name}_gemm_m{m}_{n}x{k}", "ms_per_step": ms, "steps": nsteps, "alg_bytes": alg,
-            "GB_s": alg / (ms * 1e-3) / 1e9, "frac_hbm_peak": alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+    return {"workload": f"{name}_gemm{'_q' if prequant else ''}_m{m}_{n}x{k}", "ms_per_step": ms, "steps": nsteps,
+            "alg_bytes": alg, "GB_s": alg / (ms * 1e-3) / 1e9, "frac_hbm_peak": alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
             "TFLOP_s": flops / (ms * 1e-3) / 1e12, "frac_mfma_peak": flops / (ms * 1e-3) / 1e12 / peak_tf}
 
 
@@ -371,8 +378,9 @@ def main():
     if args.only in ("all", "gemm"):
         from stblarge_amd import ops
 
-        for fmt in (ops.FP4, ops.FP8):
-            r = gemm_workload(torch, fmt, max(200, args.steps // 4), args.warmup)
+        for fmt, pq, n, k in [(ops.FP4, True, 2048, 7168), (ops.FP8, True, 2048, 7168), (ops.FP4, False, 2048, 7168),
+                              (ops.FP8, False, 2048, 7168), (ops.FP4, True, 7168, 2048)]:
+            r = gemm_workload(torch, fmt, max(200, args.steps // 4), args.warmup, n=n, k=k, prequant=pq)
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s, "
                   f"{r['TFLOP_s']:.0f} TFLOP/s ({100 * r['frac_mfma_peak']:.1f}% MFMA)", file=sys.stderr, flush=True)

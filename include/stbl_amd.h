@@ -164,12 +164,21 @@ int stbl_amd_route(const float *logits, const float *bias, int t, int n_exp, int
 /* Y[m][n] = sum_k Aq[m][k] Wdeq[n][k], m <= 64, where Aq = act_quant(X, act_block, "ue8m0")
  * (act_block 32 or 128: e4m3 codes with power-of-two scales) and W is FP4 (fmt 0: codes [n][k/2] +
  * E8M0 [n][k/32]) or FP8 (fmt 1: codes [n][k] + fp32 [ceil(n/128)][k/128]). X bf16 [m][k], Y bf16
- * [m][n] (fp32 when y_f32). k % 128 == 0. work: device scratch of stbl_amd_gemm_work_bytes() bytes.
+ * [m][n] (fp32 when y_f32). k % 128 == 0, n <= 2^20. work: device scratch of
+ * stbl_amd_gemm_work_bytes() bytes (no initial contents needed); calls sharing one work buffer must
+ * not overlap in time.
  * Replaces fp8_gemm / fp4_gemm(A = act_quant(X)) of ref/kernel.py:85-102. */
 int stbl_amd_gemm(int fmt, void *y, const void *codes, const void *scales, const void *x, int m, int n, int k,
                   int act_block, int y_f32, void *work, hipStream_t st);
 
-/* Scratch bytes for stbl_amd_gemm. */
+/* The same GEMM on activations already quantized by stbl_amd_act_quant_e4m3: aq e4m3 codes [m][k]
+ * (16-byte aligned), as E8M0 scale bytes [m][k/act_block]. One launch.
+ * Replaces fp8_gemm(a, a_s, b, b_s) / fp4_gemm(a, a_s, b, b_s) of ref/kernel.py:85-102, which take
+ * the quantized activation and its scales as arguments. */
+int stbl_amd_gemm_q(int fmt, void *y, const void *codes, const void *scales, const void *aq, const void *as, int m,
+                    int n, int k, int act_block, int y_f32, void *work, hipStream_t st);
+
+/* Scratch bytes for stbl_amd_gemm and stbl_amd_gemm_q. */
 uint64_t stbl_amd_gemm_work_bytes(int m, int n, int k);
 
 /* act_quant(x, block, "ue8m0") (ref/kernel.py:35-45) as the GEMM consumes it: x bf16 [rows][k] ->

@@ -4,7 +4,7 @@
 //   A = act_quant(X, block, "ue8m0") (e4m3 codes, power-of-two scales per `block` along K),
 //   FP8 W: e4m3 with fp32 scales per 128x128 block; FP4 W: e2m1 with E8M0 scales per 32 along K;
 //   fp32 accumulation, bf16 output.
-// Three launches:
+// Kernels:
 //   k_act_quant_e4m3  X bf16 -> e4m3 codes + E8M0 scale bytes, one 16-lane group per block of 128
 //                     (or 4 lanes per block of 32); the e4m3 rounding uses v_cvt_pk_fp8_f32, which
 //                     equals the round-to-nearest-even encoder bit for bit on every bf16 input;
@@ -12,12 +12,9 @@
 //                     e2m1 weights. The activation scales (powers of two) and the FP4 weight scales
 //                     (E8M0) are the MFMA's own per-32 scale operands, so the hardware applies them
 //                     exactly; the FP8 weights' fp32 block scale multiplies each 128-K step's product
-//                     in fp32. A workgroup owns 64 output columns (one 16-column MFMA tile per wave)
-//                     and a K slice; its activation slice is staged once in LDS in MFMA operand order
-//                     and shared by the 4 waves; each wave streams its weights straight into
-//                     registers, all of its slice's loads in flight at once;
-//   k_gemm_reduce     sums the K slices' fp32 partials in slice order (deterministic) and rounds to
-//                     bf16.
+//                     in fp32. Split K with the cross-slice sum fused (last workgroup per tile), so
+//                     the GEMM proper is one launch; stbl_amd_gemm_q takes already quantized
+//                     activations, stbl_amd_gemm quantizes X first (two launches).
 // Operand layout of the 16x16x128 f8f6f4 MFMA (probed on gfx950): lane l = r + 16 g holds row r of A
 // (column r of B); e4m3 operands hold K bytes [16g, 16g+16) and [64+16g, 64+16g+16) of the 128-K
 // step, e2m1 operands K elements [32g, 32g+32) (low nibble first); the lane's E8M0 scale covers K
@@ -30,7 +27,10 @@ namespace stbl {
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kGemmMaxM = 64;
-constexpr int kGemmMaxSteps = 8;  // 128-K steps per workgroup slice
+constexpr int kGemmWaveSteps = 2;                  // 128-K steps per wave
+constexpr int kGemmWgSteps = 4 * kGemmWaveSteps;   // per workgroup (one slice of K)
+constexpr int kGemmTileVecs = 16 * 64;  // f32x4 per 64 x 64 tile, in the order k_gemm's threads hold them
+constexpr int kGemmMaxN = 1 << 20;
 
 // ---- activation quantization --------------------------------------------------------------------
 
@@ -69,137 +69,219 @@ __global__ __launch_bounds__(256) void k_act_quant_e4m3(const uint16_t *__restri
 
 // ---- GEMM ---------------------------------------------------------------------------------------
 
-template <bool FP4W>
+// One workgroup owns a 64 x 64 output tile (4 m-tiles x 4 n-tiles of 16 x 16) and a slice of up to
+// 4 SW 128-K steps (SW = kGemmWaveSteps); wave w takes SW consecutive steps of the slice and
+// accumulates all 16 tiles in registers, loading its activations and weights straight from global
+// memory (no operand is shared between waves, so nothing is staged through LDS). All loads of a
+// wave are issued before its first MFMA, from addresses clamped into the buffers; a step past the
+// slice gets zero operands instead of a branch. The 4 waves' tiles are summed through LDS in wave
+// order. With one slice the workgroup writes Y; otherwise it writes its slice's partial tile and
+// k_gemm_reduce adds the slices in order. (Summing the slices in the last workgroup to finish needs
+// an agent-scope release/acquire per workgroup, which writes back and invalidates the XCD's L2 each
+// time: measured at about 4x the whole GEMM, so the kernel boundary is the synchronization point.)
+// Workgroup b takes tile b % ntiles and slice b / ntiles: with ntiles % 8 == 0 every slice of a tile
+// runs on one XCD (workgroups go round-robin over the 8 XCDs), which shares its activation reads.
+// A rows are lda bytes apart.
+template <bool FP4W, int SW>
 __global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ wc, const void *__restrict__ ws,
                                               const uint8_t *__restrict__ aq, const uint8_t *__restrict__ as_,
-                                              float *__restrict__ part, int M, int N, int K, int act_shift,
-                                              int steps_per_slice) {
-    // A operands of the slice, in MFMA order, as two planes of 16 bytes per lane (so that a wave's
-    // ds_read_b128 reads one contiguous kilobyte, free of bank conflicts): plane p holds
-    // [m-tile][step][lane] the lane's bytes [16p, 16p+16); scales [m-tile][step][lane]
-    __shared__ u32x4 lds_a[4 * kGemmMaxSteps * 64 * 2];
-    __shared__ uint32_t lds_s[4 * kGemmMaxSteps * 64];
+                                              f32x4 *__restrict__ part, void *__restrict__ y, int y_f32, int M,
+                                              int N, int K, int lda, int act_shift, int ntiles, int slices,
+                                              int steps_wg) {
+    __shared__ f32x4 red[4 * kGemmTileVecs];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 64, slice = blockIdx.y;
-    const int KS = K >> 7, step0 = slice * steps_per_slice;
-    const int nsteps = min(steps_per_slice, KS - step0);
+    const int tile = blockIdx.x % ntiles, slice = blockIdx.x / ntiles;
+    const int n0 = tile * 64, KS = K >> 7;
+    const int wsteps = (steps_wg + 3) >> 2;
+    const int s0 = slice * steps_wg + wave * wsteps;
+    const int nst = max(0, min(wsteps, min(KS, (slice + 1) * steps_wg) - s0));  // wave-uniform
 
-    // 1. activation slice loads (issued first: they come from L2 and gate the LDS stage)
-    //    unit q = (m-tile, step, lane): 2 x 16 bytes of row 16 mt + r at step k-offsets 16g and 64+16g.
-    //    Every load is unconditional, from an address clamped into the buffers; dead units are
-    //    zeroed afterwards, so no load sits behind a branch and all of them are in flight together.
-    constexpr int kUnits = 4 * kGemmMaxSteps * 64;
-    u32x4 av[kUnits / 256][2];
-    uint32_t sv[kUnits / 256];
-    bool aok[kUnits / 256];
+    // 1. loads: lane (r, g) holds, per step, rows 16 mt + r of A and columns n0 + 16 nt + r of W
+    u32x4 av[SW][4][2];
+    uint32_t asc[SW][4];
+    u32x4 bv[SW][4][FP4W ? 1 : 2];
+    uint32_t bsc[SW][4];
+    float wsc[SW];
 #pragma unroll
-    for (int j = 0; j < kUnits / 256; j++) {
-        const int q = tid + 256 * j, mt = q / (kGemmMaxSteps * 64), st = (q / 64) % kGemmMaxSteps, l = q & 63;
-        const int m = 16 * mt + (l & 15), gg = l >> 4;
-        aok[j] = m < M && st < nsteps;
-        const size_t kb = (size_t)(step0 + (aok[j] ? st : 0)) * 128;
-        const uint8_t *row = aq + (size_t)(aok[j] ? m : 0) * K + kb;
-        av[j][0] = *(const u32x4 *)(row + 16 * gg);
-        av[j][1] = *(const u32x4 *)(row + 64 + 16 * gg);
-        sv[j] = as_[(size_t)(aok[j] ? m : 0) * (K >> act_shift) + ((kb + 32 * gg) >> act_shift)];
-    }
-    // 2. this wave's weights for every step of the slice: column n = n0 + 16 wave + r
-    const int n = min(n0 + 16 * wave + r, N - 1);
-    u32x4 bw[kGemmMaxSteps][2];
-    uint32_t bsc[kGemmMaxSteps];
-    float wsc[kGemmMaxSteps];
-#pragma unroll
-    for (int s = 0; s < kGemmMaxSteps; s++) {
-        const size_t kb = (size_t)(step0 + (s < nsteps ? s : 0)) * 128;
-        if constexpr (FP4W) {
-            bw[s][0] = *(const u32x4 *)(wc + (size_t)n * (K >> 1) + ((kb + 32 * g) >> 1));
-            bsc[s] = ((const uint8_t *)ws)[(size_t)n * (K >> 5) + ((kb + 32 * g) >> 5)];
-        } else {
-            const uint8_t *row = wc + (size_t)n * K + kb;
-            bw[s][0] = *(const u32x4 *)(row + 16 * g);
-            bw[s][1] = *(const u32x4 *)(row + 64 + 16 * g);
-            wsc[s] = ((const float *)ws)[(size_t)(n0 >> 7) * KS + (kb >> 7)];
-        }
-    }
-    // 3. stage the activation operands (dead units as zeros)
-    const u32x4 z4 = {0, 0, 0, 0};
-#pragma unroll
-    for (int j = 0; j < kUnits / 256; j++) {
-        const int q = tid + 256 * j;
-        lds_a[q] = aok[j] ? av[j][0] : z4;
-        lds_a[kUnits + q] = aok[j] ? av[j][1] : z4;
-        lds_s[q] = aok[j] ? sv[j] : 127u;
-    }
-    __syncthreads();
-    // 4. MFMAs: 4 m-tiles x kGemmMaxSteps steps; a step past the slice has zero operands (and a zero
-    //    block scale for FP8), so it adds nothing and needs no branch
-    f32x4 acc[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < kGemmMaxSteps; s++) {
-        const bool live = s < nsteps;
-        const u32x4 b0 = live ? bw[s][0] : z4;
-        i32x8 b;
-        if constexpr (FP4W) {
-            b = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], 0, 0, 0, 0};
-        } else {
-            const u32x4 b1 = live ? bw[s][1] : z4;
-            b = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
-        }
+    for (int s = 0; s < SW; s++) {
+        const size_t kb = (size_t)(s < nst ? s0 + s : 0) * 128;
 #pragma unroll
         for (int mt = 0; mt < 4; mt++) {
-            const int q = (mt * kGemmMaxSteps + s) * 64 + lane;
-            const u32x4 a0 = lds_a[q], a1 = lds_a[kUnits + q];
-            const i32x8 a = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
-            const int sa = (int)lds_s[q];
-            if constexpr (FP4W) {
-                acc[mt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc[mt], 0, 4, 0, sa, 0,
-                                                                           live ? (int)bsc[s] : 127);
-            } else {
-                const f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0,
-                                                                                  0, sa, 0, 127);
-                const float sw = live ? wsc[s] : 0.f;
+            const int m = min(16 * mt + r, M - 1);
+            const uint8_t *row = aq + (size_t)m * lda + kb;
+            av[s][mt][0] = *(const u32x4 *)(row + 16 * g);
+            av[s][mt][1] = *(const u32x4 *)(row + 64 + 16 * g);
+            asc[s][mt] = as_[(size_t)m * (K >> act_shift) + ((kb + 32 * g) >> act_shift)];
+        }
 #pragma unroll
-                for (int e = 0; e < 4; e++) acc[mt][e] = fmaf(sw, d[e], acc[mt][e]);
+        for (int nt = 0; nt < 4; nt++) {
+            const int n = min(n0 + 16 * nt + r, N - 1);
+            if constexpr (FP4W) {
+                bv[s][nt][0] = *(const u32x4 *)(wc + (size_t)n * (K >> 1) + (kb >> 1) + 16 * g);
+                bsc[s][nt] = ((const uint8_t *)ws)[(size_t)n * (K >> 5) + (kb >> 5) + g];
+            } else {
+                const uint8_t *row = wc + (size_t)n * K + kb;
+                bv[s][nt][0] = *(const u32x4 *)(row + 16 * g);
+                bv[s][nt][1] = *(const u32x4 *)(row + 64 + 16 * g);
             }
         }
+        if constexpr (!FP4W) wsc[s] = ((const float *)ws)[(size_t)(n0 >> 7) * KS + (kb >> 7)];
     }
-    // 5. partials [slice][m][n]
-    const int ncol = n0 + 16 * wave + r;
-    if (ncol >= N) return;
+    // 2. MFMAs, 16 independent accumulators per step
+    f32x4 acc[4][4];
 #pragma unroll
     for (int mt = 0; mt < 4; mt++)
 #pragma unroll
+        for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const u32x4 z4 = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < SW; s++) {
+        const bool live = s < nst;
+        i32x8 b[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) {
+            const u32x4 b0 = live ? bv[s][nt][0] : z4;
+            if constexpr (FP4W) {
+                b[nt] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], 0, 0, 0, 0};
+            } else {
+                const u32x4 b1 = live ? bv[s][nt][1] : z4;
+                b[nt] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) {
+            const u32x4 a0 = live ? av[s][mt][0] : z4, a1 = live ? av[s][mt][1] : z4;
+            const i32x8 a = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++) {
+                if constexpr (FP4W) {
+                    acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b[nt], acc[mt][nt], 0, 4, 0,
+                                                                                   (int)asc[s][mt], 0, (int)bsc[s][nt]);
+                } else {
+                    const f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b[nt], f32x4{0.f, 0.f, 0.f, 0.f},
+                                                                                      0, 0, 0, (int)asc[s][mt], 0, 127);
+                    const float sw = live ? wsc[s] : 0.f;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[mt][nt][e] = fmaf(sw, d[e], acc[mt][nt][e]);
+                }
+            }
+        }
+    }
+    // 3. the workgroup's sum, in wave order; thread (wave, lane) keeps m-tile j, n-tile `wave`
+#pragma unroll
+    for (int t = 0; t < 16; t++) red[(wave * 16 + t) * 64 + lane] = acc[t >> 2][t & 3];
+    __syncthreads();
+    f32x4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int q = tid + 256 * j;
+        v[j] = ((red[q] + red[kGemmTileVecs + q]) + red[2 * kGemmTileVecs + q]) + red[3 * kGemmTileVecs + q];
+    }
+    if (slices > 1) {
+        f32x4 *tp = part + ((size_t)tile * slices + slice) * kGemmTileVecs;
+#pragma unroll
+        for (int j = 0; j < 4; j++) tp[tid + 256 * j] = v[j];
+        return;
+    }
+    // Y: element e of v[j] is row 16 j + 4 g + e, column n0 + 16 wave + r
+    const int n = n0 + 16 * wave + r;
+    if (n >= N) return;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int m = 16 * mt + 4 * g + e;
-            if (m < M) part[((size_t)slice * M + m) * N + ncol] = acc[mt][e];
+            const int m = 16 * j + 4 * g + e;
+            if (m >= M) continue;
+            if (y_f32) ((float *)y)[(size_t)m * N + n] = v[j][e];
+            else ((uint16_t *)y)[(size_t)m * N + n] = f32_to_bf16_bits(v[j][e]);
         }
 }
 
-// y[m][n] = bf16(sum over slices in order of part[slice][m][n]) (or the fp32 sum when y_f32).
-__global__ void k_gemm_reduce(const float *__restrict__ part, int slices, int mn, void *__restrict__ y, int y_f32) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= mn) return;
-    float s = part[i];
-    for (int sl = 1; sl < slices; sl++) s += part[(size_t)sl * mn + i];
-    if (y_f32) ((float *)y)[i] = s;
-    else ((uint16_t *)y)[i] = f32_to_bf16_bits(s);
+// Y = the slices' partial tiles added in slice order; thread i takes f32x4 i of every tile (the
+// layout k_gemm's threads stored them in), so partial reads are contiguous per slice.
+__global__ __launch_bounds__(256) void k_gemm_reduce(const f32x4 *__restrict__ part, int slices, int ntiles,
+                                                     void *__restrict__ y, int y_f32, int M, int N) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= ntiles * kGemmTileVecs) return;
+    const int tile = i / kGemmTileVecs, q = i % kGemmTileVecs;
+    const f32x4 *tp = part + (size_t)tile * slices * kGemmTileVecs + q;
+    f32x4 s = tp[0];
+    for (int sl = 1; sl < slices; sl++) s += tp[(size_t)sl * kGemmTileVecs];
+    // q = tid + 256 j of the producing workgroup: m-tile j, n-tile tid / 64, lane tid % 64
+    const int j = q >> 8, t = q & 255, r = t & 15, g = (t >> 4) & 3, w = t >> 6;
+    const int n = tile * 64 + 16 * w + r;
+    if (n >= N) return;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int m = 16 * j + 4 * g + e;
+        if (m >= M) continue;
+        if (y_f32) ((float *)y)[(size_t)m * N + n] = s[e];
+        else ((uint16_t *)y)[(size_t)m * N + n] = f32_to_bf16_bits(s[e]);
+    }
 }
 
-// Slicing of K: about 2 workgroups per CU in total, each slice at most kGemmMaxSteps 128-K steps.
-static void gemm_plan(int n, int k, int *slices, int *steps) {
-    const int ntiles = (n + 63) / 64, ks = k / 128;
-    int want = 256 / ntiles;
-    if (want < 1) want = 1;
-    int st = (ks + want - 1) / want;
-    if (st > kGemmMaxSteps) st = kGemmMaxSteps;
-    if (st < 1) st = 1;
-    *steps = st;
-    *slices = (ks + st - 1) / st;
+// Split of K: slices of 8 steps (2 per wave), fewer steps per slice when that leaves under 192
+// workgroups. (Unsplit tiles with 4 steps per wave, which need no partials, measured slower at
+// 7168 x 2048: 112 workgroups leave half the CUs idle.)
+struct GemmPlan {
+    int ntiles, slices, steps;
+};
+
+static GemmPlan gemm_plan(int n, int k) {
+    GemmPlan p;
+    p.ntiles = (n + 63) / 64;
+    const int ks = k / 128;
+    int st = kGemmWgSteps;
+    while (st > 1 && p.ntiles * ((ks + st - 1) / st) < 192) st--;
+    p.steps = st, p.slices = (ks + st - 1) / st;
+    return p;
 }
 
 static uint64_t a256(uint64_t v) { return (v + 255) & ~(uint64_t)255; }
+
+static uint64_t part_bytes(const GemmPlan &p) {
+    return p.slices > 1 ? (uint64_t)p.ntiles * p.slices * kGemmTileVecs * 16 : 0;
+}
+
+// Requires p.steps <= kGemmWgSteps and p.slices * p.steps covering k / 128; A rows lda bytes apart.
+static hipError_t launch_gemm_plan(const GemmPlan &p, int fmt, void *y, const void *codes, const void *scales,
+                                   const uint8_t *aq, int lda, const uint8_t *as_, int m, int n, int k, int act_block,
+                                   int y_f32, void *work, hipStream_t st) {
+    f32x4 *part = (f32x4 *)work;
+    const int shift = act_block == 32 ? 5 : 7;
+    const dim3 grid(p.ntiles * p.slices);
+    if (fmt == 0)
+        hipLaunchKernelGGL((k_gemm<true, kGemmWaveSteps>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales, aq,
+                           as_, part, y, y_f32, m, n, k, lda, shift, p.ntiles, p.slices, p.steps);
+    else
+        hipLaunchKernelGGL((k_gemm<false, kGemmWaveSteps>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales, aq,
+                           as_, part, y, y_f32, m, n, k, lda, shift, p.ntiles, p.slices, p.steps);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && p.slices > 1) {
+        hipLaunchKernelGGL(k_gemm_reduce, dim3(p.ntiles * kGemmTileVecs / 256), dim3(256), 0, st, part, p.slices,
+                           p.ntiles, y, y_f32, m, n);
+        e = hipGetLastError();
+    }
+    return e;
+}
+
+static hipError_t launch_gemm(int fmt, void *y, const void *codes, const void *scales, const uint8_t *aq,
+                              const uint8_t *as_, int m, int n, int k, int act_block, int y_f32, void *work,
+                              hipStream_t st) {
+    return launch_gemm_plan(gemm_plan(n, k), fmt, y, codes, scales, aq, k, as_, m, n, k, act_block, y_f32, work, st);
+}
+
+static int check_gemm(const char *name, int fmt, const void *y, const void *codes, const void *scales, int m, int n,
+                      int k, int act_block, const void *work) {
+    if (fmt != 0 && fmt != 1) return abi_fail(hipErrorInvalidValue, "%s: unknown format %d", name, fmt);
+    if (!y || !codes || !scales || !work) return abi_fail(hipErrorInvalidValue, "%s: null pointer", name);
+    if (m < 1 || m > kGemmMaxM || n < 1 || n > kGemmMaxN || k < 128 || k % 128 || (act_block != 32 && act_block != 128))
+        return abi_fail(hipErrorInvalidValue,
+                        "%s: need 1 <= m <= 64, n <= %d, k %% 128 == 0, act_block 32 or 128 (m=%d n=%d k=%d)", name,
+                        kGemmMaxN, m, n, k);
+    if (!aligned16(codes) || !aligned16(work)) return abi_fail(hipErrorInvalidValue, "%s: codes and work must be 16-byte aligned", name);
+    return 0;
+}
 
 }  // namespace stbl
 
@@ -208,40 +290,29 @@ using namespace stbl;
 extern "C" {
 
 uint64_t stbl_amd_gemm_work_bytes(int m, int n, int k) {
-    int slices, steps;
-    gemm_plan(n, k, &slices, &steps);
-    return a256((uint64_t)m * k) + a256((uint64_t)m * (k / 32)) + a256((uint64_t)slices * m * n * 4);
+    if (m < 1 || n < 1 || k < 128) return 256;
+    return a256(part_bytes(gemm_plan(n, k))) + a256((uint64_t)m * k) + a256((uint64_t)m * (k / 32)) + 256;
+}
+
+int stbl_amd_gemm_q(int fmt, void *y, const void *codes, const void *scales, const void *aq, const void *as, int m,
+                    int n, int k, int act_block, int y_f32, void *work, hipStream_t st) {
+    if (int e = check_gemm("gemm_q", fmt, y, codes, scales, m, n, k, act_block, work)) return e;
+    if (!aq || !as || !aligned16(aq)) return abi_fail(hipErrorInvalidValue, "gemm_q: aq (16-byte aligned) and as needed");
+    return abi_status(launch_gemm(fmt, y, codes, scales, (const uint8_t *)aq, (const uint8_t *)as, m, n, k, act_block,
+                                  y_f32, work, st),
+                      "gemm_q launch");
 }
 
 int stbl_amd_gemm(int fmt, void *y, const void *codes, const void *scales, const void *x, int m, int n, int k,
                   int act_block, int y_f32, void *work, hipStream_t st) {
-    if (fmt != 0 && fmt != 1) return abi_fail(hipErrorInvalidValue, "gemm: unknown format %d", fmt);
-    if (!y || !codes || !scales || !x || !work) return abi_fail(hipErrorInvalidValue, "gemm: null pointer");
-    if (m < 1 || m > kGemmMaxM || n < 1 || k < 128 || k % 128 || (act_block != 32 && act_block != 128))
-        return abi_fail(hipErrorInvalidValue, "gemm: need 1 <= m <= 64, k %% 128 == 0, act_block 32 or 128 (m=%d k=%d)", m, k);
-    if (!aligned16(codes) || !aligned16(x) || !aligned16(work)) return abi_fail(hipErrorInvalidValue, "gemm: codes, x, work must be 16-byte aligned");
-    int slices, steps;
-    gemm_plan(n, k, &slices, &steps);
-    uint8_t *aq = (uint8_t *)work;
+    if (int e = check_gemm("gemm", fmt, y, codes, scales, m, n, k, act_block, work)) return e;
+    if (!x || !aligned16(x)) return abi_fail(hipErrorInvalidValue, "gemm: x must be 16-byte aligned");
+    uint8_t *aq = (uint8_t *)work + a256(part_bytes(gemm_plan(n, k)));
     uint8_t *as_ = aq + a256((uint64_t)m * k);
-    float *part = (float *)(as_ + a256((uint64_t)m * (k / 32)));
     const int n8 = m * k / 8;
     hipLaunchKernelGGL(k_act_quant_e4m3, dim3((n8 + 255) / 256), dim3(256), 0, st, (const uint16_t *)x, n8, act_block, aq, as_);
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess) {
-        const dim3 grid((n + 63) / 64, slices);
-        if (fmt == 0)
-            hipLaunchKernelGGL(k_gemm<true>, grid, dim3(256), 0, st, (const uint8_t *)codes, scales, aq, as_, part, m, n, k,
-                               act_block == 32 ? 5 : 7, steps);
-        else
-            hipLaunchKernelGGL(k_gemm<false>, grid, dim3(256), 0, st, (const uint8_t *)codes, scales, aq, as_, part, m, n,
-                               k, act_block == 32 ? 5 : 7, steps);
-        e = hipGetLastError();
-    }
-    if (e == hipSuccess) {
-        hipLaunchKernelGGL(k_gemm_reduce, dim3((m * n + 255) / 256), dim3(256), 0, st, part, slices, m * n, y, y_f32);
-        e = hipGetLastError();
-    }
+    if (e == hipSuccess) e = launch_gemm(fmt, y, codes, scales, aq, as_, m, n, k, act_block, y_f32, work, st);
     return abi_status(e, "gemm launch");
 }
 

@@ -381,28 +381,57 @@ def route(logits, topk, bias=None, route_scale=1.0, want_scores=False):
 
 # ---- multi-token GEMM (scaled MFMA) ------------------------------------------------------------------
 
-def gemm(codes, scales, x, fmt, act_block=128, out_f32=False, work=None):
-    """Y [M, N] = act_quant(X, act_block) . Wdeq^T for M <= 64 (fp4_gemm / fp8_gemm of ref/kernel.py)."""
-    _need(x, torch.bfloat16, "x", 2)
-    m, k = x.shape
+def _gemm_shapes(codes, scales, fmt, k):
+    _need(codes, torch.uint8, "codes", 2)
+    _need(scales, torch.uint8 if fmt == FP4 else torch.float32, "scales", 2)
+    n = codes.shape[0]
     if fmt == FP4:
-        _need(codes, torch.uint8, "codes", 2)
-        _need(scales, torch.uint8, "scales", 2)
-        n = codes.shape[0]
         ok = codes.shape[1] * 2 == k and tuple(scales.shape) == (n, k // 32)
     else:
-        _need(codes, torch.uint8, "codes", 2)
-        _need(scales, torch.float32, "scales", 2)
-        n = codes.shape[0]
         ok = codes.shape[1] == k and tuple(scales.shape) == ((n + 127) // 128, (k + 127) // 128)
     if not ok:
-        raise ValueError(f"shape mismatch: codes {tuple(codes.shape)}, scales {tuple(scales.shape)}, x {tuple(x.shape)}")
-    nbytes = int(_lib.load().stbl_amd_gemm_work_bytes(m, n, k))
-    if work is None or work.numel() < nbytes:
-        work = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        raise ValueError(f"shape mismatch: codes {tuple(codes.shape)}, scales {tuple(scales.shape)}, k {k}")
+    return n
+
+
+def gemm_work(m, n, k, device):
+    """Scratch for gemm / gemm_q (split-K partial tiles and the quantized activations)."""
+    return torch.empty(int(_lib.load().stbl_amd_gemm_work_bytes(m, n, k)), dtype=torch.uint8, device=device)
+
+
+def _work_for(work, m, n, k, device):
+    if work is None or work.numel() < int(_lib.load().stbl_amd_gemm_work_bytes(m, n, k)):
+        return gemm_work(m, n, k, device)
+    return work
+
+
+def gemm(codes, scales, x, fmt, act_block=128, out_f32=False, work=None):
+    """Y [M, N] = act_quant(X, act_block) . Wdeq^T for M <= 64 (fp4_gemm / fp8_gemm of ref/kernel.py).
+    `work` (from gemm_work) may be passed to reuse the scratch across calls on one stream."""
+    _need(x, torch.bfloat16, "x", 2)
+    m, k = x.shape
+    n = _gemm_shapes(codes, scales, fmt, k)
+    work = _work_for(work, m, n, k, x.device)
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=x.device)
     _lib.check(_lib.load().stbl_amd_gemm(fmt, _ptr(y), _ptr(codes), _ptr(scales), _ptr(x), m, n, k, act_block,
                                          int(out_f32), _ptr(work), _stream()), "gemm")
+    return y
+
+
+def gemm_q(codes, scales, aq, a_s, fmt, act_block=128, out_f32=False, work=None):
+    """Y [M, N] = (Aq * a_s) . Wdeq^T with the activations already quantized: aq e4m3 codes uint8 [M, K],
+    a_s E8M0 scale bytes uint8 [M, K / act_block] (act_quant_e4m3's output), as ref/kernel.py's
+    fp8_gemm(a, a_s, b, b_s) takes them."""
+    _need(aq, torch.uint8, "aq", 2)
+    _need(a_s, torch.uint8, "a_s", 2)
+    m, k = aq.shape
+    if tuple(a_s.shape) != (m, k // act_block):
+        raise ValueError(f"a_s {tuple(a_s.shape)} does not match aq {tuple(aq.shape)} at block {act_block}")
+    n = _gemm_shapes(codes, scales, fmt, k)
+    work = _work_for(work, m, n, k, aq.device)
+    y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=aq.device)
+    _lib.check(_lib.load().stbl_amd_gemm_q(fmt, _ptr(y), _ptr(codes), _ptr(scales), _ptr(aq), _ptr(a_s), m, n, k,
+                                           act_block, int(out_f32), _ptr(work), _stream()), "gemm_q")
     return y
 
 

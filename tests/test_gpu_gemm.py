@@ -67,3 +67,43 @@ def test_gemm_fp8(gpu, m, n, k):
     y32 = np_(ops.gemm(dc, ds, x.to(gpu), ops.FP8, 128, out_f32=True))
     y16 = np_(ops.gemm(dc, ds, x.to(gpu), ops.FP8, 128))
     _check(y32, y16, want)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("block", [32, 128])
+def test_gemm_q_matches_gemm_and_oracle(gpu, fmt, block):
+    # fp8_gemm(a, a_s, b, b_s) form: the activation quantized by a separate call (ref/kernel.py:85-102)
+    if fmt == 1 and block == 32:
+        pytest.skip("FP8 weights pair with act_block 128 in the reference configuration")
+    m, n, k = 64, 2048, 7168
+    w = data.weight(n, k, seed=77 + fmt)
+    q = oracle.quant_fp4 if fmt == 0 else oracle.quant_fp8_b128
+    codes, scales = q(w.numpy())
+    deq = oracle.dequant_fp4(codes, scales) if fmt == 0 else oracle.dequant_fp8_b128(codes, scales)
+    x = data.activation(m, k, seed=78)
+    want = _oracle_gemm(x, deq, block)
+    dc, ds = torch.from_numpy(codes).to(gpu), torch.from_numpy(scales).to(gpu)
+    aq, a_s = ops.act_quant_e4m3(x.to(gpu), block)
+    y32 = np_(ops.gemm_q(dc, ds, aq, a_s, fmt, block, out_f32=True))
+    y16 = np_(ops.gemm_q(dc, ds, aq, a_s, fmt, block))
+    _check(y32, y16, want)
+    assert bits_equal(y32, np_(ops.gemm(dc, ds, x.to(gpu), fmt, block, out_f32=True)))
+
+
+def test_gemm_deterministic_and_work_reuse(gpu):
+    # split-K partials are added in slice order, so repeated calls agree bit for bit; one work buffer
+    # (sized for the largest shape) serves every shape
+    shapes = [(64, 2048, 7168), (64, 7168, 2048), (16, 256, 512), (64, 2048, 7168)]
+    work = ops.gemm_work(64, 7168, 7168, gpu)
+    first = {}
+    for i, (m, n, k) in enumerate(shapes * 2):
+        w = data.weight(n, k, seed=n + 2 * k)
+        codes, scales = oracle.quant_fp4(w.numpy())
+        x = data.activation(m, k, seed=k)
+        dc, ds = torch.from_numpy(codes).to(gpu), torch.from_numpy(scales).to(gpu)
+        y = np_(ops.gemm(dc, ds, x.to(gpu), ops.FP4, 128, out_f32=True, work=work))
+        if (m, n, k) in first:
+            assert bits_equal(y, first[(m, n, k)]), (m, n, k)
+        else:
+            first[(m, n, k)] = y
+            assert rel_err(y, _oracle_gemm(x, oracle.dequant_fp4(codes, scales), 128)) <= 1e-3
