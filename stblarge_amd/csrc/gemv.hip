@@ -33,6 +33,25 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     const int cc = active ? c : 0;
     const int row0 = blockIdx.x * R;
 
+    // 0. OCP FP4 scales: the tile's rows hold one contiguous block of R * nch scale bytes, fetched
+    //    with one 16-byte load per thread (from the block's 16-byte units; such a load never crosses
+    //    a page, so the bytes around the block are safe to read) and handed out through LDS, instead
+    //    of one byte load per row per lane. Issued first, so waiting for it does not wait for W.
+    constexpr bool kStageScales = F == WFmt::FP4_OCP;
+    static_assert(!kStageScales || R <= 8, "the staged scale block holds at most 8 rows");
+    __shared__ u32x4 lds_sc[kStageScales ? kMaxScaleUnits : 1];
+    u32x4 scv = {0, 0, 0, 0};
+    uintptr_t sc_a0 = 0;
+    size_t sc_len = 0;
+    int sc_units = 0;
+    if constexpr (kStageScales) {
+        const uint8_t *blk = (const uint8_t *)J.s + (size_t)row0 * nch;
+        sc_len = (size_t)(min(row0 + R, rows) - row0) * nch;
+        sc_a0 = (uintptr_t)blk & ~(uintptr_t)15;
+        const uintptr_t a1 = ((uintptr_t)blk + sc_len - 1) & ~(uintptr_t)15;
+        sc_units = (int)((a1 - sc_a0) >> 4) + 1;
+        scv = ld_stream((const void *)min(sc_a0 + 16 * (uintptr_t)threadIdx.x, a1));
+    }
     // 1. loads: x first (it is needed by every row), then every row of the tile. fp32 activations
     //    (the reference ABI) are widened once and use exact FMAs; bf16 activations stay packed for
     //    the dot2 path (gemv_core.hpp).
@@ -46,12 +65,11 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     for (int r = 0; r < R; r++) {
         const size_t row = (size_t)min(row0 + r, rows - 1);
         if constexpr (F == WFmt::FP4_OCP) {
-            w[r] = *(const u32x4 *)(J.w + row * (k >> 1) + (size_t)cc * 16);
-            sb[r] = ((const uint8_t *)J.s)[row * nch + cc];
+            w[r] = ld_stream(J.w + row * (k >> 1) + (size_t)cc * 16);
         } else if constexpr (F == WFmt::FP4_GGUF) {
             load_gguf_block(J.w + (row * nch + cc) * 17, sb[r], w[r]);
         } else {
-            w[r] = *(const u32x4 *)(J.w + row * k + (size_t)cc * 16);
+            w[r] = ld_stream(J.w + row * k + (size_t)cc * 16);
         }
     }
     float lscale = 1.f;  // FP8: one block scale per lane for the whole tile
@@ -59,6 +77,13 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
         lscale = ((const float *)J.s)[(size_t)(row0 >> 7) * ((k + 127) >> 7) + ((cc * 16) >> 7)];
     uint32_t lsb = 0;
     if constexpr (F == WFmt::FP8_E8M0) lsb = ((const uint8_t *)J.s)[(size_t)(row0 >> 5) * (k >> 5) + ((cc * 16) >> 5)];
+    if constexpr (kStageScales) {
+        if ((int)threadIdx.x < sc_units) lds_sc[threadIdx.x] = scv;
+        __syncthreads();
+        const uint8_t *sl = (const uint8_t *)lds_sc + (((uintptr_t)J.s + (size_t)row0 * nch) & 15);
+#pragma unroll
+        for (int r = 0; r < R; r++) sb[r] = sl[min((size_t)r * nch + cc, sc_len - 1)];
+    }
 
     // 2. products, scales, masking; 3. lane reduction
     __shared__ float red[kMaxWaves][M * R];

@@ -52,10 +52,10 @@ struct SlotMat {
     // 16 bytes of codes of row `row`, chunk cc, and the chunk's E8M0 scale byte (FP4 only)
     __device__ __forceinline__ void load(size_t row, int cc, u32x4 &w, uint32_t &sb) const {
         if constexpr (WTraits<F>::fp4) {
-            w = *(const u32x4 *)(codes + row * (size_t)(k >> 1) + (size_t)cc * 16);
-            sb = scales[row * (size_t)(k >> 5) + cc];
+            w = ld_stream(codes + row * (size_t)(k >> 1) + (size_t)cc * 16);
+            sb = ld_stream_u8(scales + row * (size_t)(k >> 5) + cc);
         } else {
-            w = *(const u32x4 *)(codes + row * (size_t)k + (size_t)cc * 16);
+            w = ld_stream(codes + row * (size_t)k + (size_t)cc * 16);
             sb = 0;
         }
     }
