@@ -38,9 +38,10 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     //    a page, so the bytes around the block are safe to read) and handed out through LDS, instead
     //    of one byte load per row per lane. Issued first, so waiting for it does not wait for W.
     constexpr bool kStageScales = F == WFmt::FP4_OCP;
-    static_assert(!kStageScales || R <= 8, "the staged scale block holds at most 8 rows");
+    static_assert(!kStageScales || R <= kMaxStageRows, "the staged scale block holds at most kMaxStageRows rows");
+    constexpr int kScaleLoads = R > 8 ? 2 : 1;  // units <= R nch / 16 + 2 <= kScaleLoads * threads
     __shared__ u32x4 lds_sc[kStageScales ? kMaxScaleUnits : 1];
-    u32x4 scv = {0, 0, 0, 0};
+    u32x4 scv[kScaleLoads] = {};
     uintptr_t sc_a0 = 0;
     size_t sc_len = 0;
     int sc_units = 0;
@@ -50,7 +51,9 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
         sc_a0 = (uintptr_t)blk & ~(uintptr_t)15;
         const uintptr_t a1 = ((uintptr_t)blk + sc_len - 1) & ~(uintptr_t)15;
         sc_units = (int)((a1 - sc_a0) >> 4) + 1;
-        scv = ld_stream((const void *)min(sc_a0 + 16 * (uintptr_t)threadIdx.x, a1));
+#pragma unroll
+        for (int i = 0; i < kScaleLoads; i++)
+            scv[i] = ld_stream((const void *)min(sc_a0 + 16 * (uintptr_t)(threadIdx.x + i * blockDim.x), a1));
     }
     // 1. loads: x first (it is needed by every row), then every row of the tile. fp32 activations
     //    (the reference ABI) are widened once and use exact FMAs; bf16 activations stay packed for
@@ -78,7 +81,11 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     uint32_t lsb = 0;
     if constexpr (F == WFmt::FP8_E8M0) lsb = ((const uint8_t *)J.s)[(size_t)(row0 >> 5) * (k >> 5) + ((cc * 16) >> 5)];
     if constexpr (kStageScales) {
-        if ((int)threadIdx.x < sc_units) lds_sc[threadIdx.x] = scv;
+#pragma unroll
+        for (int i = 0; i < kScaleLoads; i++) {
+            const int u = threadIdx.x + i * blockDim.x;
+            if (u < sc_units) lds_sc[u] = scv[i];
+        }
         __syncthreads();
         const uint8_t *sl = (const uint8_t *)lds_sc + (((uintptr_t)J.s + (size_t)row0 * nch) & 15);
 #pragma unroll

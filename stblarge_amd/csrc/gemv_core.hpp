@@ -12,9 +12,10 @@
 namespace stbl {
 
 constexpr int kMaxWaves = 8;  // K <= 512 chunks: 16384 FP4 / 8192 FP8 elements
-// 16-byte units of a tile's OCP FP4 scale block (R <= 8 rows of at most kMaxWaves * 64 bytes),
-// plus one for a block that starts mid-unit and one for its end.
-constexpr int kMaxScaleUnits = 8 * kMaxWaves * 64 / 16 + 2;
+// 16-byte units of a tile's OCP FP4 scale block (R <= kMaxStageRows rows of at most kMaxWaves * 64
+// bytes), plus one for a block that starts mid-unit and one for its end.
+constexpr int kMaxStageRows = 8;
+constexpr int kMaxScaleUnits = kMaxStageRows * kMaxWaves * 64 / 16 + 2;
 constexpr int kMaxJobs = 16;  // matrices per launch (the reference's kMxBatch, stbl/kernels.h:18)
 
 enum class WFmt { FP4_OCP, FP4_GGUF, FP8_B128, FP8_E8M0 };

@@ -213,12 +213,19 @@ struct PickTable {
 
 // y[t][r] = bf16(sum over token t's picks in order of o[pair][r]) with the fp32 sum starting at 0
 // (stbl/model.cu:579-592: memset, axpy per expert in top-k order, axpy shared, round_bf16).
+// Every pick's load is issued before the sum (a fixed trip count; unused picks read pick 0's row),
+// so the thread waits for one memory latency, not one per pick.
 __global__ void k_moe_combine(PickTable picks, int npick, const uint16_t *__restrict__ o, void *__restrict__ y,
                               int dim, int y_f32) {
     const int r = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
     if (r >= dim) return;
+    uint32_t v[kMoeMaxPick];
+#pragma unroll
+    for (int p = 0; p < kMoeMaxPick; p++) v[p] = o[(size_t)picks.pair[t][p < npick ? p : 0] * dim + r];
     float acc = 0.f;
-    for (int p = 0; p < npick; p++) acc = fmaf(1.f, bf16_bits_to_f32(o[(size_t)picks.pair[t][p] * dim + r]), acc);
+#pragma unroll
+    for (int p = 0; p < kMoeMaxPick; p++)
+        if (p < npick) acc = fmaf(1.f, bf16_bits_to_f32(v[p]), acc);
     if (y_f32) ((float *)y)[(size_t)t * dim + r] = bf16_round(acc);
     else ((uint16_t *)y)[(size_t)t * dim + r] = f32_to_bf16_bits(acc);
 }
