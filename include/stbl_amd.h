@@ -46,6 +46,10 @@ void stbl_gemv_fp8(float *y, const void *w, const void *scale, const float *x, i
  * 16+i high nibble]); y = bf16(W x) stored as fp32. k % 256 == 0, k <= 16384, w 8-byte aligned. */
 void stbl_gemv_mxfp4(float *y, const void *w, const float *x, int rows, int k, hipStream_t st);
 
+/* y[r] = sum_k x[k] * w[r][k] in fp32 (bf16-rounded when round_out), fp32 weights [rows][k]: the
+ * router's logits. Replaces stbl_gemv_f32 (stbl/kernels.h:23, stbl/kernels.cu:206-214). */
+void stbl_gemv_f32(float *y, const float *w, const float *x, int rows, int k, int round_out, hipStream_t st);
+
 /* stbl/kernels.h:18-20 -- n <= 16 same-shape stbl_gemv_mxfp4 products in one launch. y, w and x are
  * HOST arrays of n device pointers. */
 enum { kMxBatch = 16 };
@@ -107,6 +111,13 @@ int stbl_amd_quant_fp4(void *codes, void *scales, const float *w, int rows, int 
  * quantizes 128x128 weights; this follows the configs' definition with act_quant's clamp. */
 int stbl_amd_quant_fp8_b128(void *codes, float *scales, const float *w, int rows, int k, hipStream_t st);
 
+/* FP8 weight quantization in the reference engine's layout, one E8M0 scale byte per 32x32 block
+ * (stbl/kernels.cu:98-103; the reference's own weights arrive quantized, tools/convert_official.py:
+ * 53-54): s = pow2_ceil(max(amax, 1e-4) * (1/448)) as act_quant's power-of-two rule
+ * (ref/kernel.py:38-40), codes = e4m3_rne(clamp(w/s, +-448)). scales [ceil(rows/32)][k/32] bytes;
+ * k % 32 == 0. */
+int stbl_amd_quant_fp8_e8m0(void *codes, void *scales, const float *w, int rows, int k, hipStream_t st);
+
 /* out fp32 [rows][k] = e2m1(code) * 2^(s-127), one fp32 product per element (ref/kernel.py:98-101). */
 int stbl_amd_dequant_fp4(float *out, const void *codes, const void *scales, int rows, int k, hipStream_t st);
 
@@ -121,11 +132,12 @@ int stbl_amd_dequant_fp8(float *out, const void *codes, const void *scales, int 
 /* ---- v2: expert FFN and routed MoE (stbl/model.cu:426-594 composition) ------------------------------ */
 
 /* Weight formats of an expert slot. */
-enum { STBL_AMD_FP4 = 0, STBL_AMD_FP8 = 1 };
+enum { STBL_AMD_FP4 = 0, STBL_AMD_FP8 = 1, STBL_AMD_FP8_E8M0 = 2 };
 
 /* Byte layout of one expert slot: gate [inter x dim], up [inter x dim], down [dim x inter], each as
  * codes then scales (FP4: codes [rows][k/2] + E8M0 [rows][k/32]; FP8: codes [rows][k] + fp32
- * [ceil(rows/128)][ceil(k/128)]), every part 256-byte aligned. Writes the six part offsets (may be
+ * [ceil(rows/128)][ceil(k/128)]; FP8_E8M0: codes [rows][k] + E8M0 [ceil(rows/32)][k/32]), every
+ * part 256-byte aligned. Writes the six part offsets (may be
  * NULL) and returns the slot size. Replaces the gate|up|down slot of stbl/model.cu:374-381. */
 uint64_t stbl_amd_expert_layout(int fmt, int dim, int inter, uint64_t *offsets);
 
@@ -134,7 +146,8 @@ uint64_t stbl_amd_expert_layout(int fmt, int dim, int inter, uint64_t *offsets);
  * where act is act_quant(., 32, ue8m0, inplace) when `official`, else the identity, and swiglu is
  * stbl_swiglu's arithmetic. slot 256-byte aligned in the layout above; x bf16 [m][dim]; y bf16
  * [m][dim] (fp32 holding the unrounded down product when y_f32); work >= m * inter * 2 bytes of
- * device scratch. FP4 needs dim, inter % 32 == 0; FP8 % 128; K <= 16384 (FP4) / 8192 (FP8). */
+ * device scratch. FP4 and FP8_E8M0 need dim, inter % 32 == 0; FP8 % 128; K <= 16384 (FP4) / 8192
+ * (FP8). */
 int stbl_amd_expert_ffn(int fmt, void *y, const void *slot, const void *x, int m, int dim, int inter, float weight,
                         float limit, int official, int y_f32, void *work, hipStream_t st);
 
@@ -142,22 +155,26 @@ int stbl_amd_expert_ffn(int fmt, void *y, const void *slot, const void *x, int m
  * y[t] = bf16(sum_p o(slot[pick[t][p]], weights[t][p]) + o(slot[shared], 1)) with the fp32 sum taken
  * in top-k order from 0, each o an expert FFN output rounded to bf16 with the route weight applied
  * inside SwiGLU. slots: HOST array of n_slots device pointers; pick [t][topk] (HOST) indexes it;
- * weights [t][topk] (HOST); shared = slot index of the always-on expert or -1. t <= 16, topk <= 16.
- * work: device scratch of stbl_amd_moe_work_bytes() bytes. */
+ * weights [t][topk] (HOST); shared = slot index of the always-on expert or -1; shared_fmt = that
+ * slot's format, or -1 for fmt (the reference pairs FP4 routed experts with an FP8 E8M0 shared
+ * expert, stbl/model.cu:544-547). t <= 16, topk <= 16. work: device scratch of
+ * stbl_amd_moe_work_bytes() bytes. */
 int stbl_amd_moe_experts(int fmt, void *y, const void *x, int t, int dim, int inter, const void *const *slots,
-                         int n_slots, const int *pick, const float *weights, int topk, int shared, float limit,
-                         int official, int y_f32, void *work, hipStream_t st);
+                         int n_slots, const int *pick, const float *weights, int topk, int shared, int shared_fmt,
+                         float limit, int official, int y_f32, void *work, hipStream_t st);
 
 /* Scratch bytes for stbl_amd_moe_experts on t tokens. */
 uint64_t stbl_amd_moe_work_bytes(int t, int topk, int dim, int inter);
 
-/* Router on the device (stbl/model.cu:430-452 with sigmoid scores as the configuration asks):
- * score = 1 / (1 + exp(-logit)); ids = top-k of score + bias (bias may be NULL), ties to the lower
- * id, in descending order; weights = score / (sum of the top-k scores in order + 1e-20) *
- * route_scale. logits fp32 [t][n_exp], ids int32 [t][topk], weights fp32 [t][topk], scores fp32
- * [t][n_exp] (optional). n_exp <= 1024, topk <= 32. */
-int stbl_amd_route(const float *logits, const float *bias, int t, int n_exp, int topk, float route_scale, int *ids,
-                   float *weights, float *scores, hipStream_t st);
+/* Router on the device (stbl/model.cu:430-452): score_fn 0: score = 1 / (1 + exp(-logit)) (the
+ * configuration's sigmoid router); score_fn 1: score = sqrt(softplus(logit)), softplus(l) = l above
+ * 20 else log1p(exp(l)) (the reference engine's, stbl/kernels.cu:436-442). ids = top-k of score +
+ * bias (bias may be NULL), ties to the lower id, in descending order; weights = score / (sum of the
+ * top-k scores in order + 1e-20) * route_scale. logits fp32 [t][n_exp], ids int32 [t][topk],
+ * weights fp32 [t][topk], scores fp32 [t][n_exp] (optional). n_exp <= 1024, topk <= 32.
+ * Replaces stbl_sqrt_softplus + the host partial_sort of stbl/model.cu:431-451. */
+int stbl_amd_route(const float *logits, const float *bias, int t, int n_exp, int topk, float route_scale, int score_fn,
+                   int *ids, float *weights, float *scores, hipStream_t st);
 
 /* ---- v2: multi-token expert GEMM (ref/kernel.py:85-102 with M > 4, scaled f8f6f4 MFMA) ------------ */
 

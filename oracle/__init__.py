@@ -55,10 +55,13 @@ def lib():
         L.orc_f2bf.argtypes = [F]
         L.orc_swiglu1.restype = F
         L.orc_swiglu1.argtypes = [F, F, F, F]
+        L.orc_route_score.restype = F
+        L.orc_route_score.argtypes = [F, I]
         for name in ("orc_act_quant", "orc_quant_fp4", "orc_quant_fp8_b128", "orc_dequant_fp8_b128",
                      "orc_dequant_fp8_e8m0_b32", "orc_dequant_fp4", "orc_dequant_gguf17", "orc_ocp_to_gguf17",
                      "orc_gemm", "orc_gemv_fp4", "orc_gemv_fp8_b128", "orc_swiglu", "orc_round_bf16",
-                     "orc_route", "orc_e4m3_encode_n", "orc_expert_ffn_fp4", "orc_expert_ffn_fp8", "orc_moe_fp4"):
+                     "orc_route", "orc_e4m3_encode_n", "orc_expert_ffn_fp4", "orc_expert_ffn_fp8", "orc_moe_fp4",
+                     "orc_quant_fp8_e8m0_b32", "orc_expert_ffn_deq", "orc_moe_deq"):
             getattr(L, name).restype = None
         _lib = L
     return _lib
@@ -165,6 +168,17 @@ def quant_fp8_b128(w):
     return codes, scales
 
 
+def quant_fp8_e8m0_b32(w):
+    """Weight [rows][k] -> (e4m3 codes u8 [rows][k], E8M0 scale bytes u8 [ceil(rows/32)][k/32]): per
+    32x32 block s = pow2_ceil(max(amax, 1e-4) / 448), the reference engine's FP8 layout."""
+    w = _f32(w)
+    rows, k = w.shape
+    codes = np.empty((rows, k), np.uint8)
+    scales = np.empty(((rows + 31) // 32, k // 32), np.uint8)
+    lib().orc_quant_fp8_e8m0_b32(_p(w), I(rows), I(k), _p(codes), _p(scales))
+    return codes, scales
+
+
 def dequant_fp8_b128(codes, scales):
     codes, scales = _u8(codes), _f32(scales)
     rows, k = codes.shape
@@ -243,15 +257,25 @@ def swiglu(g, u, w=1.0, limit=0.0):
     return out
 
 
-def route(logits, topk=8, bias=None, route_scale=1.0):
-    """Sigmoid scores, top-k (ties to the lower id), renormalised weights. Returns (scores, ids, weights)."""
+SCORE_SIGMOID, SCORE_SQRT_SOFTPLUS = 0, 1
+
+
+def route_score(l, score_fn=SCORE_SIGMOID):
+    """One router score: sigmoid (0) or sqrt(softplus) with threshold 20 (1, stbl/kernels.cu:436-442)."""
+    return lib().orc_route_score(F(l), I(score_fn))
+
+
+def route(logits, topk=8, bias=None, route_scale=1.0, score_fn=SCORE_SIGMOID):
+    """Router scores (sigmoid, or sqrt(softplus) as the reference engine), top-k by score + bias
+    (ties to the lower id), renormalised weights. Returns (scores, ids, weights)."""
     logits = _f32(logits)
     t, e = logits.shape
     scores = np.empty((t, e), np.float32)
     ids = np.empty((t, topk), np.int32)
     weights = np.empty((t, topk), np.float32)
     b = _f32(bias) if bias is not None else None
-    lib().orc_route(_p(logits), _p(b), I(t), I(e), I(topk), F(route_scale), _p(scores), _p(ids), _p(weights))
+    lib().orc_route(_p(logits), _p(b), I(t), I(e), I(topk), F(route_scale), I(score_fn), _p(scores), _p(ids),
+                    _p(weights))
     return scores, ids, weights
 
 
@@ -287,6 +311,36 @@ def moe_fp4(slots, weights, shared, dim, inter, x, limit=0.0, official=False):
     sh = _u8(shared) if shared is not None else None
     y = np.empty((t, dim), np.float32)
     lib().orc_moe_fp4(arr, _p(w), _p(sh), I(t), I(topk), I(dim), I(inter), _p(x), F(limit), I(int(official)), _p(y))
+    return y
+
+
+def expert_ffn_deq(gw, uw, dw, x, w=1.0, limit=0.0, official=False, raw=False):
+    """One expert from dequantized fp32 matrices gate/up [inter][dim], down [dim][inter] (any weight
+    format dequantizes exactly); the composition of expert_ffn_fp4."""
+    gw, uw, dw, x = _f32(gw), _f32(uw), _f32(dw), _f32(x)
+    inter, dim = gw.shape
+    o = np.empty(dim, np.float32)
+    r = np.empty(dim, np.float64) if raw else None
+    lib().orc_expert_ffn_deq(_p(gw), _p(uw), _p(dw), I(dim), I(inter), _p(x), F(w), F(limit), I(int(official)),
+                             _p(o), _p(r))
+    return (o, r) if raw else o
+
+
+def moe_deq(experts, weights, shared, x, limit=0.0, official=False):
+    """experts: per token, a list (top-k order) of (gate, up, down) dequantized fp32 matrices;
+    shared: (gate, up, down) or None; weights [t][topk]. The composition of moe_fp4."""
+    x = _f32(x)
+    dim = x.shape[-1]
+    x = x.reshape(-1, dim)
+    t, topk = x.shape[0], len(experts[0])
+    keep = [_f32(m) for row in experts for e in row for m in e]
+    inter = keep[0].shape[0]
+    arr = (ctypes.c_void_p * len(keep))(*[k.ctypes.data for k in keep])
+    sh_keep = [_f32(m) for m in shared] if shared is not None else None
+    sh = (ctypes.c_void_p * 3)(*[k.ctypes.data for k in sh_keep]) if sh_keep else None
+    w = _f32(weights)
+    y = np.empty((t, dim), np.float32)
+    lib().orc_moe_deq(arr, _p(w), sh, I(t), I(topk), I(dim), I(inter), _p(x), F(limit), I(int(official)), _p(y))
     return y
 
 

@@ -7,7 +7,8 @@
  *   - ref/kernel.py:12-102      codecs, act_quant, fp4 quantization, fp8_gemm / fp4_gemm dequant;
  *   - tools/convert_official.py:40-48   e4m3 closed form; :187-201 GGUF MXFP4 17-byte blocks;
  *   - stbl/kernels.cu:54-63,86-89,134-191,444-464   engine act_quant / round / GEMV / SwiGLU / axpy;
- *   - stbl/model.cu:426-594     MoE composition (router weights, order of the expert sums).
+ *   - stbl/model.cu:426-594     MoE composition (router weights, order of the expert sums);
+ *   - stbl/kernels.cu:436-442   router score sqrt(softplus) (threshold 20).
  * Matrix products accumulate in double: the reference's own GEMMs only fix the products, not the
  * summation order (ref/kernel.py:6-7), so a more accurate sum is the right yardstick.
  */
@@ -171,6 +172,30 @@ void orc_quant_fp8_b128(const float *w, int rows, int k, uint8_t *codes, float *
         }
 }
 
+/* FP8 e4m3 with one E8M0 scale byte per 32x32 block, the reference engine's FP8 layout
+ * (stbl/kernels.cu:98-103; its weights arrive quantized, tools/convert_official.py:53-54). Synthetic
+ * weights use act_quant's power-of-two rule (ref/kernel.py:38-40) per block:
+ * s = pow2_ceil(max(amax, 1e-4) * fp32(1/448)), q = e4m3(clamp(w / s, +-448)).
+ * scales [(rows+31)/32][k/32]; k % 32 == 0; the last row block may be partial. */
+void orc_quant_fp8_e8m0_b32(const float *w, int rows, int k, uint8_t *codes, uint8_t *scales) {
+    const float inv = (float)(1.0 / 448.0);
+    const int nb = (rows + 31) / 32, kb = k / 32;
+    for (int bi = 0; bi < nb; bi++)
+        for (int bj = 0; bj < kb; bj++) {
+            const int r0 = bi * 32, r1 = r0 + 32 < rows ? r0 + 32 : rows, c0 = bj * 32;
+            float amax = 0.f;
+            for (int r = r0; r < r1; r++)
+                for (int c = c0; c < c0 + 32; c++) amax = fmaxf(amax, fabsf(w[(size_t)r * k + c]));
+            const float sc = orc_pow2_ceil(fmaxf(amax, 1e-4f) * inv);
+            scales[(size_t)bi * kb + bj] = (uint8_t)((f2u(sc) >> 23) & 0xff);
+            for (int r = r0; r < r1; r++)
+                for (int c = c0; c < c0 + 32; c++) {
+                    const float v = fminf(fmaxf(w[(size_t)r * k + c] / sc, -448.f), 448.f);
+                    codes[(size_t)r * k + c] = orc_e4m3_encode(v);
+                }
+        }
+}
+
 /* ---- dequantization (ref/kernel.py:89-90, :98-101): one fp32 product per element ---------------- */
 
 void orc_dequant_fp8_b128(const uint8_t *codes, const float *scales, int rows, int k, float *out) {
@@ -298,16 +323,24 @@ void orc_round_bf16(float *x, int n) {
     for (int i = 0; i < n; i++) x[i] = bf16r(x[i]);
 }
 
-/* ---- router (sigmoid scores, top-k, renormalised weights) ------------------------------------- */
+/* ---- router (scores, top-k, renormalised weights) ------------------------------------------------ */
 
-/* logits [t][e]. score = 1/(1+exp(-l)); top-k by score + bias (bias may be NULL), ties to the lower
- * id; weight_i = score_i / (sum of the top-k scores in top-k order + 1e-20) * route_scale
- * (stbl/model.cu:444-451, 528-530, with sigmoid in place of sqrt-softplus). */
-void orc_route(const float *logits, const float *bias, int t, int e, int topk, float route_scale, float *scores,
-               int *ids, float *weights) {
+/* Router score of one logit: score_fn 0 = sigmoid 1/(1+exp(-l)) (the configuration's router);
+ * 1 = sqrt(softplus(l)) with softplus(l) = l above 20, else log1p(exp(l)) (stbl/kernels.cu:436-442,
+ * torch's threshold). */
+float orc_route_score(float l, int score_fn) {
+    if (score_fn == 1) return sqrtf(l > 20.f ? l : log1pf(expf(l)));
+    return 1.f / (1.f + expf(-l));
+}
+
+/* logits [t][e]. score = orc_route_score(l); top-k by score + bias (bias may be NULL), ties to the
+ * lower id; weight_i = score_i / (sum of the top-k scores in top-k order + 1e-20) * route_scale
+ * (stbl/model.cu:444-451, 528-530). */
+void orc_route(const float *logits, const float *bias, int t, int e, int topk, float route_scale, int score_fn,
+               float *scores, int *ids, float *weights) {
     for (int i = 0; i < t; i++) {
         float *sc = scores + (size_t)i * e;
-        for (int j = 0; j < e; j++) sc[j] = 1.f / (1.f + expf(-logits[(size_t)i * e + j]));
+        for (int j = 0; j < e; j++) sc[j] = orc_route_score(logits[(size_t)i * e + j], score_fn);
         int *id = ids + (size_t)i * topk;
         for (int p = 0; p < topk; p++) {
             int best = -1;
@@ -405,4 +438,44 @@ void orc_moe_fp4(const uint8_t *const *slots, const float *weights, const uint8_
         for (int c = 0; c < dim; c++) y[(size_t)i * dim + c] = bf16r(sum[c]);
     }
     free(xbuf), free(h), free(o), free(sum), free(acc);
+}
+
+/* ---- expert FFN / MoE on dequantized weights (any weight format) -------------------------------- */
+
+/* One expert with dequantized fp32 matrices gw, uw [inter][dim], dw [dim][inter]: the composition of
+ * ffn_fp4_one (every format dequantizes exactly, so the products are the same). raw may be NULL. */
+void orc_expert_ffn_deq(const float *gw, const float *uw, const float *dw, int dim, int inter, const float *x,
+                        float w, float lim, int official, float *o, double *raw) {
+    float *xbuf = malloc(sizeof(float) * dim), *h = malloc(sizeof(float) * inter);
+    double *acc = malloc(sizeof(double) * (dim > inter ? dim : inter));
+    if (official) orc_act_quant(x, 1, dim, 32, 1, NULL, NULL, xbuf);
+    else memcpy(xbuf, x, sizeof(float) * dim);
+    orc_gemm(xbuf, gw, 1, inter, dim, acc);
+    for (int i = 0; i < inter; i++) h[i] = bf16r((float)acc[i]);
+    orc_gemm(xbuf, uw, 1, inter, dim, acc);
+    for (int i = 0; i < inter; i++) h[i] = orc_swiglu1(h[i], bf16r((float)acc[i]), w, lim);
+    if (official) orc_act_quant(h, 1, inter, 32, 1, NULL, NULL, h);
+    orc_gemm(h, dw, 1, dim, inter, acc);
+    for (int i = 0; i < dim; i++) o[i] = bf16r((float)acc[i]);
+    if (raw) memcpy(raw, acc, sizeof(double) * dim);
+    free(xbuf), free(h), free(acc);
+}
+
+/* The MoE of orc_moe_fp4 on dequantized experts: mats[(i*topk + p)*3 + {0,1,2}] are token i's p-th
+ * pick's gate, up and down; shared[0..2] the shared expert's (or NULL). y [t][dim]. */
+void orc_moe_deq(const float *const *mats, const float *weights, const float *const *shared, int t, int topk,
+                 int dim, int inter, const float *x, float lim, int official, float *y) {
+    float *o = malloc(sizeof(float) * dim), *sum = malloc(sizeof(float) * dim);
+    for (int i = 0; i < t; i++) {
+        for (int c = 0; c < dim; c++) sum[c] = 0.f;
+        for (int p = 0; p <= topk; p++) {
+            const float *const *m = p < topk ? mats + ((size_t)i * topk + p) * 3 : shared;
+            if (!m) continue;
+            const float w = p < topk ? weights[(size_t)i * topk + p] : 1.f;
+            orc_expert_ffn_deq(m[0], m[1], m[2], dim, inter, x + (size_t)i * dim, w, lim, official, o, NULL);
+            for (int c = 0; c < dim; c++) sum[c] += 1.f * o[c];
+        }
+        for (int c = 0; c < dim; c++) y[(size_t)i * dim + c] = bf16r(sum[c]);
+    }
+    free(o), free(sum);
 }

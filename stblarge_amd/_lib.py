@@ -27,6 +27,7 @@ SIGNATURES = {
     "stbl_gemv_fp8": (None, [P, P, P, P, I, I, I, P]),
     "stbl_gemv_mxfp4": (None, [P, P, P, I, I, P]),
     "stbl_gemv_mxfp4_batch": (None, [PP, PP, PP, I, I, I, P]),
+    "stbl_gemv_f32": (None, [P, P, P, I, I, I, P]),
     "stbl_swiglu": (None, [P, P, P, F, F, I, P]),
     "stbl_swiglu_batch": (None, [P, P, P, PF, I, F, I, P]),
     "stbl_axpy": (None, [P, P, F, I, P]),
@@ -38,14 +39,15 @@ SIGNATURES = {
     "stbl_amd_act_quant": (I, [P, I, I, I, I, P, P, P, P]),
     "stbl_amd_quant_fp4": (I, [P, P, P, I, I, P]),
     "stbl_amd_quant_fp8_b128": (I, [P, P, P, I, I, P]),
+    "stbl_amd_quant_fp8_e8m0": (I, [P, P, P, I, I, P]),
     "stbl_amd_dequant_fp4": (I, [P, P, P, I, I, P]),
     "stbl_amd_dequant_gguf17": (I, [P, P, I, I, P]),
     "stbl_amd_dequant_fp8": (I, [P, P, P, I, I, I, P]),
     "stbl_amd_expert_layout": (U64, [I, I, I, PU64]),
     "stbl_amd_expert_ffn": (I, [I, P, P, P, I, I, I, F, F, I, I, P, P]),
-    "stbl_amd_moe_experts": (I, [I, P, P, I, I, I, PP, I, PI, PF, I, I, F, I, I, P, P]),
+    "stbl_amd_moe_experts": (I, [I, P, P, I, I, I, PP, I, PI, PF, I, I, I, F, I, I, P, P]),
     "stbl_amd_moe_work_bytes": (U64, [I, I, I, I]),
-    "stbl_amd_route": (I, [P, P, I, I, I, F, P, P, P, P]),
+    "stbl_amd_route": (I, [P, P, I, I, I, F, I, P, P, P, P]),
     "stbl_amd_gemm": (I, [I, P, P, P, P, I, I, I, I, I, P, P]),
     "stbl_amd_gemm_q": (I, [I, P, P, P, P, P, I, I, I, I, I, P, P]),
     "stbl_amd_gemm_work_bytes": (U64, [I, I, I]),

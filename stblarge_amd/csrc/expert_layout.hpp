@@ -3,6 +3,8 @@
 //
 //   FP4 (OCP e2m1 + E8M0 per 32 along K): codes [rows][k/2], scales [rows][k/32] bytes.
 //   FP8 (e4m3 + fp32 per 128x128 block):  codes [rows][k],   scales [ceil(rows/128)][ceil(k/128)] fp32.
+//   FP8_E8M0 (e4m3 + E8M0 per 32x32, the reference engine's FP8 layout, stbl/kernels.cu:98-103):
+//                                          codes [rows][k],   scales [ceil(rows/32)][k/32] bytes.
 //
 // Every part starts on a 256-byte boundary, so 128-bit loads of codes are aligned and the fp32
 // scales are naturally aligned. The reference keeps gate | up | down contiguous in its slot the same
@@ -13,7 +15,7 @@
 
 namespace stbl {
 
-enum ExpertFmt { EXPERT_FP4 = 0, EXPERT_FP8 = 1 };
+enum ExpertFmt { EXPERT_FP4 = 0, EXPERT_FP8 = 1, EXPERT_FP8_E8M0 = 2 };
 
 struct ExpertLayout {
     uint64_t off[6];  // gate codes, gate scales, up codes, up scales, down codes, down scales
@@ -27,7 +29,9 @@ __host__ __device__ inline uint64_t codes_bytes(int fmt, int rows, int k) {
 }
 
 __host__ __device__ inline uint64_t scales_bytes(int fmt, int rows, int k) {
-    return fmt == EXPERT_FP4 ? (uint64_t)rows * (k / 32) : (uint64_t)((rows + 127) / 128) * ((k + 127) / 128) * 4;
+    if (fmt == EXPERT_FP4) return (uint64_t)rows * (k / 32);
+    if (fmt == EXPERT_FP8_E8M0) return (uint64_t)((rows + 31) / 32) * (k / 32);
+    return (uint64_t)((rows + 127) / 128) * ((k + 127) / 128) * 4;
 }
 
 __host__ __device__ inline ExpertLayout expert_layout(int fmt, int dim, int inter) {

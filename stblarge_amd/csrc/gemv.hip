@@ -135,6 +135,45 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     }
 }
 
+// fp32 GEMV (the router's logits, stbl/kernels.cu:206-214): y[r] = sum_k x[k] w[r][k], optionally
+// rounded to bf16. One 256-thread workgroup per row; with VEC (k % 4 == 0, 16-byte aligned w and x)
+// every thread issues up to 8 16-byte loads of the row at once, else it strides the row one float at
+// a time. Lanes reduce with DPP and the 4 waves through LDS in wave order.
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_gemv_f32(float *__restrict__ y, const float *__restrict__ w,
+                                                  const float *__restrict__ x, int k, int round_out) {
+    __shared__ float red[4];
+    const float *wr = w + (size_t)blockIdx.x * k;
+    float acc = 0.f;
+    if constexpr (VEC) {
+        const int n4 = k >> 2;
+        for (int base = threadIdx.x; base < n4; base += 256 * 8) {
+            f32x4 wv[8], xv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = base + 256 * u, ic = i < n4 ? i : 0;
+                wv[u] = __builtin_bit_cast(f32x4, ld_stream(wr + 4 * (size_t)ic));
+                xv[u] = *(const f32x4 *)(x + 4 * (size_t)ic);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (base + 256 * u >= n4) continue;
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc = fmaf(xv[u][e], wv[u][e], acc);
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < k; i += 256) acc = fmaf(x[i], wr[i], acc);
+    }
+    acc = dpp_sum(acc);
+    if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float v = ((red[0] + red[1]) + red[2]) + red[3];
+        y[blockIdx.x] = round_out ? bf16_round(v) : v;
+    }
+}
+
 static inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 template <WFmt F, bool XF32, int M, int R>
@@ -254,6 +293,20 @@ void stbl_gemv_mxfp4_batch(float *const *y, const void *const *w, const float *c
 // stbl/kernels.h:16.
 void stbl_gemv_mxfp4(float *y, const void *w, const float *x, int rows, int k, hipStream_t st) {
     stbl_gemv_mxfp4_batch(&y, &w, &x, 1, rows, k, st);
+}
+
+// stbl/kernels.h:23 (the router's logits, stbl/model.cu:430). Any k; the 16-byte path when k % 4 == 0
+// and w, x are 16-byte aligned.
+void stbl_gemv_f32(float *y, const float *w, const float *x, int rows, int k, int round_out, hipStream_t st) {
+    if (!y || !w || !x || rows <= 0 || k <= 0) {
+        abi_fail(hipErrorInvalidValue, "stbl_gemv_f32: bad arguments (rows=%d k=%d)", rows, k);
+        return;
+    }
+    if (k % 4 == 0 && aligned16(w) && aligned16(x))
+        hipLaunchKernelGGL(k_gemv_f32<true>, dim3(rows), dim3(256), 0, st, y, w, x, k, round_out);
+    else
+        hipLaunchKernelGGL(k_gemv_f32<false>, dim3(rows), dim3(256), 0, st, y, w, x, k, round_out);
+    abi_status(hipGetLastError(), "stbl_gemv_f32 launch");
 }
 
 }  // extern "C"

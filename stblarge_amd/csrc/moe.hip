@@ -59,9 +59,12 @@ struct SlotMat {
             sb = 0;
         }
     }
-    // FP8: the lane's block scale for a tile whose rows share row0's 128-row block
+    // FP8: the lane's block scale for a tile whose rows share row0's 128-row (fp32 scales) or
+    // 32-row (E8M0 scales) block
     __device__ __forceinline__ float block_scale(int row0, int cc) const {
-        return ((const float *)scales)[(size_t)(row0 >> 7) * ((k + 127) >> 7) + ((cc * 16) >> 7)];
+        if constexpr (F == WFmt::FP8_E8M0)
+            return e8m0_to_f32(scales[(size_t)(row0 >> 5) * (k >> 5) + ((cc * 16) >> 5)]);
+        else return ((const float *)scales)[(size_t)(row0 >> 7) * ((k + 127) >> 7) + ((cc * 16) >> 7)];
     }
 };
 
@@ -232,19 +235,23 @@ __global__ void k_moe_combine(PickTable picks, int npick, const uint16_t *__rest
 
 // ---- router -------------------------------------------------------------------------------------
 
-// One workgroup of 256 threads per token. score = 1 / (1 + exp(-logit)); the top-k of score + bias
-// (ties to the lower expert id) by k rounds of a workgroup argmax; weight_i = score_i / (sum of
-// the top-k scores in top-k order + 1e-20) * route_scale.
+// One workgroup of 256 threads per token. score = 1 / (1 + exp(-logit)) (score_fn 0, the
+// configuration's router) or sqrt(softplus(logit)) with softplus(l) = l above 20, else
+// log1p(exp(l)) (score_fn 1, stbl/kernels.cu:436-442); the top-k of score + bias (ties to the lower
+// expert id) by k rounds of a workgroup argmax; weight_i = score_i / (sum of the top-k scores in
+// top-k order + 1e-20) * route_scale.
 __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits, const float *__restrict__ bias,
-                                               int n_exp, int topk, float route_scale, int *__restrict__ ids,
-                                               float *__restrict__ weights, float *__restrict__ scores) {
+                                               int n_exp, int topk, float route_scale, int score_fn,
+                                               int *__restrict__ ids, float *__restrict__ weights,
+                                               float *__restrict__ scores) {
     __shared__ float sc[1024];
     __shared__ float bv[4];
     __shared__ int bi[4];
     __shared__ int chosen[32];
     const int t = blockIdx.x, tid = threadIdx.x;
     for (int e = tid; e < n_exp; e += 256) {
-        const float s = __fdiv_rn(1.f, 1.f + expf(-logits[(size_t)t * n_exp + e]));
+        const float l = logits[(size_t)t * n_exp + e];
+        const float s = score_fn == 1 ? sqrtf(l > 20.f ? l : log1pf(expf(l))) : __fdiv_rn(1.f, 1.f + expf(-l));
         sc[e] = s;
         if (scores) scores[(size_t)t * n_exp + e] = s;
     }
@@ -352,9 +359,23 @@ static hipError_t run_jobs(const MoeJob *all, int njobs, const ExpertLayout &L, 
     return hipSuccess;
 }
 
+// Runs jobs whose slots hold format fmt.
+static hipError_t run_fmt(int fmt, const MoeJob *all, int njobs, int dim, int inter, const uint16_t *x, uint16_t *h,
+                          void *o, float limit, int official, int out_f32, hipStream_t st) {
+    const ExpertLayout L = expert_layout(fmt, dim, inter);
+    if (fmt == EXPERT_FP4)
+        return run_jobs<WFmt::FP4_OCP>(all, njobs, L, x, h, o, dim, inter, limit, official, out_f32, st);
+    if (fmt == EXPERT_FP8)
+        return run_jobs<WFmt::FP8_B128>(all, njobs, L, x, h, o, dim, inter, limit, official, out_f32, st);
+    return run_jobs<WFmt::FP8_E8M0>(all, njobs, L, x, h, o, dim, inter, limit, official, out_f32, st);
+}
+
+static bool fmt_ok(int fmt) { return fmt == EXPERT_FP4 || fmt == EXPERT_FP8 || fmt == EXPERT_FP8_E8M0; }
+
 static bool dims_ok(int fmt, int dim, int inter) {
     const int CH = fmt == EXPERT_FP4 ? 32 : 16;
-    const int align = fmt == EXPERT_FP4 ? 32 : 128;  // FP8: rows of a tile must share a scale block
+    // FP8: the rows of a tile must share a scale block (128 rows for fp32 scales, 32 for E8M0)
+    const int align = fmt == EXPERT_FP8 ? 128 : 32;
     return dim > 0 && inter > 0 && dim % align == 0 && inter % align == 0 && dim / CH <= kMaxWaves * 64 &&
            inter / CH <= kMaxWaves * 64;
 }
@@ -374,7 +395,7 @@ uint64_t stbl_amd_expert_layout(int fmt, int dim, int inter, uint64_t *offsets) 
 
 int stbl_amd_expert_ffn(int fmt, void *y, const void *slot, const void *x, int m, int dim, int inter, float weight,
                         float limit, int official, int y_f32, void *work, hipStream_t st) {
-    if (fmt != EXPERT_FP4 && fmt != EXPERT_FP8) return abi_fail(hipErrorInvalidValue, "expert_ffn: unknown format %d", fmt);
+    if (!fmt_ok(fmt)) return abi_fail(hipErrorInvalidValue, "expert_ffn: unknown format %d", fmt);
     if (!y || !slot || !x || !work) return abi_fail(hipErrorInvalidValue, "expert_ffn: null pointer");
     if (!dims_ok(fmt, dim, inter)) return abi_fail(hipErrorInvalidValue, "expert_ffn: unsupported dims %d x %d", dim, inter);
     if (m < 1 || m > kMoeMaxTok) return abi_fail(hipErrorInvalidValue, "expert_ffn: m must be 1..4 (m=%d)", m);
@@ -384,32 +405,36 @@ int stbl_amd_expert_ffn(int fmt, void *y, const void *slot, const void *x, int m
     J.slot = (const uint8_t *)slot;
     J.m = m;
     for (int t = 0; t < m; t++) J.tok[t] = t, J.pair[t] = t, J.w[t] = weight;
-    const ExpertLayout L = expert_layout(fmt, dim, inter);
-    const hipError_t e = fmt == EXPERT_FP4
-        ? run_jobs<WFmt::FP4_OCP>(&J, 1, L, (const uint16_t *)x, (uint16_t *)work, y, dim, inter, limit, official, y_f32, st)
-        : run_jobs<WFmt::FP8_B128>(&J, 1, L, (const uint16_t *)x, (uint16_t *)work, y, dim, inter, limit, official, y_f32, st);
+    const hipError_t e = run_fmt(fmt, &J, 1, dim, inter, (const uint16_t *)x, (uint16_t *)work, y, limit, official,
+                                 y_f32, st);
     return abi_status(e, "expert_ffn launch");
 }
 
 // Routed MoE over cached expert slots. slots: HOST array of n_slots device pointers (one per
 // distinct expert used by this call). pick: HOST [t][topk] indices into slots, weights: HOST
-// [t][topk] route weights, shared: index into slots of the always-on expert (weight 1) or -1.
+// [t][topk] route weights, shared: index into slots of the always-on expert (weight 1) or -1, whose
+// slot holds format shared_fmt (-1: the routed experts' format; the reference's shared expert is
+// FP8 with E8M0 32x32 scales, stbl/model.cu:544-547, next to FP4 routed experts).
 // work: device scratch of at least stbl_amd_moe_work_bytes(t, topk, dim, inter) bytes.
 int stbl_amd_moe_experts(int fmt, void *y, const void *x, int t, int dim, int inter, const void *const *slots,
-                         int n_slots, const int *pick, const float *weights, int topk, int shared, float limit,
-                         int official, int y_f32, void *work, hipStream_t st) {
-    if (fmt != EXPERT_FP4 && fmt != EXPERT_FP8) return abi_fail(hipErrorInvalidValue, "moe_experts: unknown format %d", fmt);
+                         int n_slots, const int *pick, const float *weights, int topk, int shared, int shared_fmt,
+                         float limit, int official, int y_f32, void *work, hipStream_t st) {
+    if (shared_fmt < 0) shared_fmt = fmt;
+    if (!fmt_ok(fmt) || !fmt_ok(shared_fmt))
+        return abi_fail(hipErrorInvalidValue, "moe_experts: unknown format %d / %d", fmt, shared_fmt);
     if (!y || !x || !slots || !pick || !weights || !work) return abi_fail(hipErrorInvalidValue, "moe_experts: null pointer");
-    if (!dims_ok(fmt, dim, inter)) return abi_fail(hipErrorInvalidValue, "moe_experts: unsupported dims %d x %d", dim, inter);
+    if (!dims_ok(fmt, dim, inter) || !dims_ok(shared_fmt, dim, inter))
+        return abi_fail(hipErrorInvalidValue, "moe_experts: unsupported dims %d x %d", dim, inter);
     if (t < 1 || t > kMoeMaxT || topk < 1 || topk + 1 > kMoeMaxPick || n_slots < 1 || shared >= n_slots)
         return abi_fail(hipErrorInvalidValue, "moe_experts: need 1 <= t <= 16, 1 <= topk <= 16 (t=%d topk=%d)", t, topk);
     if (!aligned16(x) || !aligned16(work)) return abi_fail(hipErrorInvalidValue, "moe_experts: x and work must be 16-byte aligned");
     for (int i = 0; i < n_slots; i++)
         if (!slots[i] || ((uintptr_t)slots[i] & 255)) return abi_fail(hipErrorInvalidValue, "moe_experts: slot %d null or not 256-byte aligned", i);
-    // jobs: one per (slot, group of <= 4 tokens); pair rows numbered in job order
-    static thread_local MoeJob jobs[kMoeMaxT * kMoeMaxPick];
+    // jobs: one per (slot, group of <= 4 tokens); pair rows numbered in job order. A shared expert of
+    // another format runs in launches of its own (sjobs).
+    static thread_local MoeJob jobs[kMoeMaxT * kMoeMaxPick], sjobs[kMoeMaxT];
     PickTable table = {};
-    int njobs = 0, npairs = 0;
+    int njobs = 0, nsjobs = 0, npairs = 0;
     const int npick = topk + (shared >= 0 ? 1 : 0);
     for (int s = 0; s < n_slots; s++) {
         MoeJob *J = nullptr;
@@ -419,7 +444,7 @@ int stbl_amd_moe_experts(int fmt, void *y, const void *x, int t, int dim, int in
                 if (sl < 0 || sl >= n_slots) return abi_fail(hipErrorInvalidValue, "moe_experts: pick out of range");
                 if (sl != s) continue;
                 if (!J || J->m == kMoeMaxTok) {
-                    J = &jobs[njobs++];
+                    J = s == shared && shared_fmt != fmt ? &sjobs[nsjobs++] : &jobs[njobs++];
                     *J = MoeJob{};
                     J->slot = (const uint8_t *)slots[s];
                 }
@@ -430,12 +455,11 @@ int stbl_amd_moe_experts(int fmt, void *y, const void *x, int t, int dim, int in
                 table.pair[tt][p] = npairs++;
             }
     }
-    const ExpertLayout L = expert_layout(fmt, dim, inter);
     uint16_t *h = (uint16_t *)work;
     uint16_t *o = h + (size_t)npairs * inter;
-    hipError_t e = fmt == EXPERT_FP4
-        ? run_jobs<WFmt::FP4_OCP>(jobs, njobs, L, (const uint16_t *)x, h, o, dim, inter, limit, official, 0, st)
-        : run_jobs<WFmt::FP8_B128>(jobs, njobs, L, (const uint16_t *)x, h, o, dim, inter, limit, official, 0, st);
+    hipError_t e = run_fmt(fmt, jobs, njobs, dim, inter, (const uint16_t *)x, h, o, limit, official, 0, st);
+    if (e == hipSuccess && nsjobs > 0)
+        e = run_fmt(shared_fmt, sjobs, nsjobs, dim, inter, (const uint16_t *)x, h, o, limit, official, 0, st);
     if (e == hipSuccess) {
         hipLaunchKernelGGL(k_moe_combine, dim3(ceil_div(dim, 256), t), dim3(256), 0, st, table, npick, o, y, dim, y_f32);
         e = hipGetLastError();
@@ -449,11 +473,13 @@ uint64_t stbl_amd_moe_work_bytes(int t, int topk, int dim, int inter) {
     return align256(pairs * inter * 2) + align256(pairs * dim * 2);
 }
 
-int stbl_amd_route(const float *logits, const float *bias, int t, int n_exp, int topk, float route_scale, int *ids,
-                   float *weights, float *scores, hipStream_t st) {
+int stbl_amd_route(const float *logits, const float *bias, int t, int n_exp, int topk, float route_scale, int score_fn,
+                   int *ids, float *weights, float *scores, hipStream_t st) {
     if (!logits || !ids || !weights || t < 1 || n_exp < 1 || n_exp > 1024 || topk < 1 || topk > 32 || topk > n_exp)
         return abi_fail(hipErrorInvalidValue, "route: need 1 <= topk <= min(32, n_exp), n_exp <= 1024");
-    hipLaunchKernelGGL(k_route, dim3(t), dim3(256), 0, st, logits, bias, n_exp, topk, route_scale, ids, weights, scores);
+    if (score_fn != 0 && score_fn != 1) return abi_fail(hipErrorInvalidValue, "route: score_fn must be 0 (sigmoid) or 1 (sqrt-softplus)");
+    hipLaunchKernelGGL(k_route, dim3(t), dim3(256), 0, st, logits, bias, n_exp, topk, route_scale, score_fn, ids,
+                       weights, scores);
     return abi_status(hipGetLastError(), "route launch");
 }
 

@@ -108,6 +108,29 @@ __global__ __launch_bounds__(256) void k_quant_fp8_b128(const float *w, int rows
     }
 }
 
+// FP8 e4m3 with one E8M0 scale per 32x32 block (the reference engine's FP8 layout, stbl/kernels.cu:
+// 98-103): s = pow2_ceil(max(amax, 1e-4) * fp32(1/448)) as act_quant's power-of-two rule
+// (ref/kernel.py:38-40), q = e4m3_rne(clamp(w / s, +-448)) (w / s is exact). One 256-thread
+// workgroup per block; scales [(rows+31)/32][k/32] bytes.
+__global__ __launch_bounds__(256) void k_quant_fp8_e8m0(const float *w, int rows, int k, uint8_t *codes,
+                                                        uint8_t *scales) {
+    __shared__ float red[4];
+    const int bi = blockIdx.y, bj = blockIdx.x, kb = gridDim.x;
+    const int r0 = bi * 32, c0 = bj * 32, nr = min(32, rows - r0);
+    float amax = 0.f;
+    for (int i = threadIdx.x; i < nr * 32; i += 256) amax = fmaxf(amax, fabsf(w[(size_t)(r0 + i / 32) * k + c0 + i % 32]));
+    amax = wave_max(amax);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float s = pow2_ceil(fmaxf(amax, 1e-4f) * (1.0f / 448.0f));
+    if (threadIdx.x == 0) scales[(size_t)bi * kb + bj] = (uint8_t)((__float_as_uint(s) >> 23) & 0xffu);
+    for (int i = threadIdx.x; i < nr * 32; i += 256) {
+        const size_t at = (size_t)(r0 + i / 32) * k + c0 + i % 32;
+        codes[at] = (uint8_t)f32_to_e4m3(fminf(fmaxf(__fdiv_rn(w[at], s), -448.f), 448.f));
+    }
+}
+
 // ---- dequantizers (the bit-exactness check of the decoders the GEMVs use) ------------------------
 
 // FP4 OCP: out[r][c] = e2m1(code) * 2^(s-127), one fp32 product. One thread per 32-group.
@@ -270,6 +293,15 @@ int stbl_amd_quant_fp8_b128(void *codes, float *scales, const float *w, int rows
     hipLaunchKernelGGL(k_quant_fp8_b128, dim3((k + 127) / 128, (rows + 127) / 128), dim3(256), 0, st, w, rows, k,
                        (uint8_t *)codes, scales);
     return abi_status(hipGetLastError(), "quant_fp8_b128 launch");
+}
+
+// FP8 e4m3 with E8M0 scales per 32x32 block: codes [rows][k], scales [(rows+31)/32][k/32]. k % 32 == 0.
+int stbl_amd_quant_fp8_e8m0(void *codes, void *scales, const float *w, int rows, int k, hipStream_t st) {
+    if (!codes || !scales || !w || rows <= 0 || k <= 0 || k % 32)
+        return abi_fail(hipErrorInvalidValue, "quant_fp8_e8m0: need k %% 32 == 0");
+    hipLaunchKernelGGL(k_quant_fp8_e8m0, dim3(k / 32, (rows + 31) / 32), dim3(256), 0, st, w, rows, k, (uint8_t *)codes,
+                       (uint8_t *)scales);
+    return abi_status(hipGetLastError(), "quant_fp8_e8m0 launch");
 }
 
 int stbl_amd_dequant_fp4(float *out, const void *codes, const void *scales, int rows, int k, hipStream_t st) {

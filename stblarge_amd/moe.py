@@ -75,12 +75,17 @@ class MoELayer:
     plus an always-on shared expert resident in HBM.
 
     forward(x, logits): x bf16 [t, dim] and router logits fp32 [t, n_experts] on the device; returns
-    y bf16 [t, dim]. Routing follows the reference (sigmoid in place of sqrt-softplus, as configured):
-    top-k of score + bias, ties to the lower id, weights renormalized then scaled."""
+    y bf16 [t, dim]. Routing follows the reference: top-k of score + bias, ties to the lower id,
+    weights renormalized then scaled, with score_fn sigmoid (the configuration's) or sqrt-softplus
+    (the reference engine's). shared_fmt: the shared expert's format (the reference engine pairs FP4
+    routed experts with an FP8 E8M0 shared one), default the routed experts' format."""
 
     def __init__(self, fmt, dim, inter, host_pool, n_experts, topk, cache_slots, shared_slot=None, bias=None,
-                 route_scale=1.0, limit=0.0, official=False, max_tokens=4):
+                 route_scale=1.0, limit=0.0, official=False, max_tokens=4, score_fn=ops.SCORE_SIGMOID,
+                 shared_fmt=None):
         self.fmt, self.dim, self.inter, self.topk = fmt, dim, inter, topk
+        self.score_fn = score_fn
+        self.shared_fmt = fmt if shared_fmt is None else shared_fmt
         self.slot_bytes, _ = ops.expert_layout(fmt, dim, inter)
         self.cache = ExpertCache(cache_slots, self.slot_bytes, host_pool, n_experts)
         self.shared = shared_slot
@@ -91,7 +96,7 @@ class MoELayer:
         self.last_route = None  # (ids, weights) of the last step, as lists (stbl_last_route)
 
     def route(self, logits):
-        ids, w = ops.route(logits, self.topk, self.bias, self.route_scale)
+        ids, w = ops.route(logits, self.topk, self.bias, self.route_scale, score_fn=self.score_fn)
         return ids.cpu().tolist(), w.cpu().tolist()  # host sync, as the reference's to_host
 
     def forward(self, x, logits, route=None, stream=None):
@@ -114,7 +119,7 @@ class MoELayer:
             slots.append(self.shared.data_ptr())
         pick = [[slot_of[e] for e in row] for row in ids]
         y = ops.moe_experts(x, slots, pick, w, self.fmt, self.dim, self.inter, shared=shared, limit=self.limit,
-                            official=self.official, work=self.work)
+                            official=self.official, work=self.work, shared_fmt=self.shared_fmt)
         self.cache.mark_used(stream)
         return y
 

@@ -47,7 +47,7 @@ def _rows2(x):
     return x if x.dim() == 2 else x.view(1, -1)
 
 
-FP4, FP8 = 0, 1
+FP4, FP8, FP8_E8M0 = 0, 1, 2  # expert formats: OCP FP4; FP8 + fp32 128x128 scales; FP8 + E8M0 32x32
 
 
 # ---- quantizers / dequantizers --------------------------------------------------------------------
@@ -70,6 +70,18 @@ def quant_fp8_b128(w):
     scales = torch.empty(((n + 127) // 128, (k + 127) // 128), dtype=torch.float32, device=w.device)
     _lib.check(_lib.load().stbl_amd_quant_fp8_b128(_ptr(codes), _ptr(scales), _ptr(w), n, k, _stream()),
                "quant_fp8_b128")
+    return codes, scales
+
+
+def quant_fp8_e8m0(w):
+    """fp32 [N, K] -> (e4m3 codes uint8 [N, K], E8M0 scale bytes uint8 [ceil(N/32), K/32]), the
+    reference engine's FP8 layout (per 32x32 block, power-of-two scales)."""
+    _need(w, torch.float32, "w", 2)
+    n, k = w.shape
+    codes = torch.empty((n, k), dtype=torch.uint8, device=w.device)
+    scales = torch.empty(((n + 31) // 32, k // 32), dtype=torch.uint8, device=w.device)
+    _lib.check(_lib.load().stbl_amd_quant_fp8_e8m0(_ptr(codes), _ptr(scales), _ptr(w), n, k, _stream()),
+               "quant_fp8_e8m0")
     return codes, scales
 
 
@@ -234,6 +246,18 @@ def stbl_gemv_mxfp4_batch(ys, ws, xs, rows, k):
     return ys
 
 
+def stbl_gemv_f32(y, w, x, rows, k, round_out=0):
+    """fp32 GEMV of the reference ABI (the router's logits): y [rows] = w [rows, k] . x [k]."""
+    _need(y, torch.float32, "y")
+    _need(w, torch.float32, "w")
+    _need(x, torch.float32, "x")
+    if y.numel() < rows or w.numel() < rows * k or x.numel() < k:
+        raise ValueError("stbl_gemv_f32: buffer sizes do not match rows/k")
+    _lib.load().stbl_gemv_f32(_ptr(y), _ptr(w), _ptr(x), rows, k, int(round_out), _stream())
+    _lib.check(None, "stbl_gemv_f32")
+    return y
+
+
 def stbl_swiglu(out, g, u, weight, limit, n):
     return stbl_swiglu_batch(out, g, u, [weight], limit, n)
 
@@ -274,6 +298,8 @@ def _mat_bytes(fmt, rows, k):
     """Codes + scales bytes of one quantized [rows x k] matrix."""
     if fmt == FP4:
         return rows * k // 2 + rows * k // 32
+    if fmt == FP8_E8M0:
+        return rows * k + ((rows + 31) // 32) * (k // 32)
     return rows * k + 4 * ((rows + 127) // 128) * ((k + 127) // 128)
 
 
@@ -282,6 +308,8 @@ def _mat_shapes(fmt, dim, inter):
     for rows, k in ((inter, dim), (inter, dim), (dim, inter)):
         if fmt == FP4:
             out += [((rows, k // 2), torch.uint8), ((rows, k // 32), torch.uint8)]
+        elif fmt == FP8_E8M0:
+            out += [((rows, k), torch.uint8), (((rows + 31) // 32, k // 32), torch.uint8)]
         else:
             out += [((rows, k), torch.uint8), (((rows + 127) // 128, (k + 127) // 128), torch.float32)]
     return out
@@ -311,7 +339,7 @@ def pack_slot(parts, fmt, dim, inter, out=None):
 
 def quant_expert(w_gate, w_up, w_down, fmt, out=None):
     """Quantize fp32 gate/up [inter, dim] and down [dim, inter] on the device into one slot."""
-    q = quant_fp4 if fmt == FP4 else quant_fp8_b128
+    q = {FP4: quant_fp4, FP8: quant_fp8_b128, FP8_E8M0: quant_fp8_e8m0}[fmt]
     parts = []
     for w in (w_gate, w_up, w_down):
         parts += list(q(w))
@@ -342,10 +370,10 @@ def moe_work_bytes(t, topk, dim, inter):
 
 
 def moe_experts(x, slots, pick, weights, fmt, dim, inter, shared=-1, limit=0.0, official=False, out_f32=False,
-                work=None, out=None):
+                work=None, out=None, shared_fmt=-1):
     """Expert part of a routed MoE layer. slots: list of device uint8 slot tensors (or raw device
     addresses); pick: [t][topk] indices into slots; weights: [t][topk] floats; shared: slot index of
-    the always-on expert or -1."""
+    the always-on expert or -1; shared_fmt: its format when it differs from the routed experts'."""
     _need(x, torch.bfloat16, "x")
     x2 = _rows2(x)
     t = x2.shape[0]
@@ -360,13 +388,17 @@ def moe_experts(x, slots, pick, weights, fmt, dim, inter, shared=-1, limit=0.0, 
     y = out if out is not None else torch.empty((t, dim), dtype=torch.float32 if out_f32 else torch.bfloat16,
                                                 device=x.device)
     _lib.check(_lib.load().stbl_amd_moe_experts(fmt, _ptr(y), _ptr(x2), t, dim, inter, arr, len(addrs), pk, wt, topk,
-                                                shared, float(limit), int(official), int(out_f32), _ptr(work),
-                                                _stream()), "moe_experts")
+                                                shared, int(shared_fmt), float(limit), int(official), int(out_f32),
+                                                _ptr(work), _stream()), "moe_experts")
     return y
 
 
-def route(logits, topk, bias=None, route_scale=1.0, want_scores=False):
-    """Device router: (ids int32 [t, topk], weights fp32 [t, topk][, scores fp32 [t, E]])."""
+SCORE_SIGMOID, SCORE_SQRT_SOFTPLUS = 0, 1
+
+
+def route(logits, topk, bias=None, route_scale=1.0, want_scores=False, score_fn=SCORE_SIGMOID):
+    """Device router: (ids int32 [t, topk], weights fp32 [t, topk][, scores fp32 [t, E]]). score_fn:
+    SCORE_SIGMOID (the configuration's) or SCORE_SQRT_SOFTPLUS (the reference engine's)."""
     _need(logits, torch.float32, "logits", 2)
     t, e = logits.shape
     ids = torch.empty((t, topk), dtype=torch.int32, device=logits.device)
@@ -374,8 +406,8 @@ def route(logits, topk, bias=None, route_scale=1.0, want_scores=False):
     sc = torch.empty((t, e), dtype=torch.float32, device=logits.device) if want_scores else None
     if bias is not None:
         _need(bias, torch.float32, "bias", 1)
-    _lib.check(_lib.load().stbl_amd_route(_ptr(logits), _ptr(bias), t, e, topk, float(route_scale), _ptr(ids), _ptr(w),
-                                          _ptr(sc), _stream()), "route")
+    _lib.check(_lib.load().stbl_amd_route(_ptr(logits), _ptr(bias), t, e, topk, float(route_scale), int(score_fn),
+                                          _ptr(ids), _ptr(w), _ptr(sc), _stream()), "route")
     return (ids, w, sc) if want_scores else (ids, w)
 
 

@@ -153,3 +153,20 @@ def test_gemv_batch(gpu, fmt):
     ys16 = ops.gemv_batch(cs, ss, xs, fmt)
     for y, y16, want in zip(ys, ys16, wants):
         assert_gemv(np_(y), np_(y16), want)
+
+
+@pytest.mark.parametrize("rows,k,round_out", [(256, 7168, 0), (256, 5120, 0), (100, 1001, 0), (64, 2048, 1)])
+def test_stbl_gemv_f32(gpu, rows, k, round_out):
+    # the router's fp32 logits GEMV (stbl/kernels.cu:206-214); the reference's own check uses 1e-5
+    # (stbl/test_kernels.py:126-130). k = 1001 takes the unaligned one-float-at-a-time path.
+    w = data.normal((rows, k), 0.02, seed=rows + k)
+    x = data.normal((k,), 1.0, seed=k)
+    want = oracle.gemm(x.numpy()[None], w.numpy())[0]
+    y = torch.empty(rows, device=gpu)
+    ops.stbl_gemv_f32(y, w.to(gpu), x.to(gpu), rows, k, round_out)
+    got = np_(y)
+    if round_out:
+        assert np.array_equal(got, oracle.bf16_round(got))
+        assert np.max(np.abs(got - want)) <= np.max(np.abs(want)) * (1e-5 + 2.0 ** -8)
+    else:
+        assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))

@@ -1,7 +1,8 @@
 """GPU parity of the expert FFN, the routed MoE layer, the router and the expert cache.
 
 Oracle: stbl_oracle.c's expert FFN / MoE composition (stbl/model.cu:505-592), router
-(stbl/model.cu:444-451 with sigmoid) and oracle.lru_simulate (stbl/model.cu:347-422, 497-507).
+(stbl/model.cu:444-451, sigmoid or the engine's sqrt-softplus) and oracle.lru_simulate
+(stbl/model.cu:347-422, 497-507).
 Bar: the unrounded down product within 1e-3 normwise of the oracle; bf16 outputs at most one bf16
 step from the oracle's, flips rare (an intermediate bf16 rounding of g or u may flip when the two
 sums differ in their last fp32 bits). Router ids exact; route weights within a few fp32 ulps (the
@@ -92,6 +93,73 @@ def test_moe_experts_shared_token_groups(gpu):
     packed = [np.concatenate([p.ravel() for p in e[1]]) for e in experts]
     want = oracle.moe_fp4([[packed[i] for i in row] for row in pick], w, None, dim, inter, x.float().numpy())
     assert bf16_ulps(y, want).max() <= 1
+
+
+def deq_parts(fmt, parts):
+    """(gate, up, down) dequantized fp32 from a slot's six parts."""
+    out = []
+    for c, sc in zip(parts[0::2], parts[1::2]):
+        if fmt == ops.FP4:
+            out.append(oracle.dequant_fp4(c, sc))
+        elif fmt == ops.FP8:
+            out.append(oracle.dequant_fp8_b128(c, sc))
+        else:
+            out.append(oracle.dequant_fp8_e8m0_b32(c, sc))
+    return out
+
+
+@pytest.mark.parametrize("dim,inter", [(512, 256), (5120, 2304)])
+@pytest.mark.parametrize("official", [False, True])
+def test_expert_ffn_fp8_e8m0(gpu, dim, inter, official):
+    # the reference engine's FP8 layout (E8M0 per 32x32, stbl/kernels.cu:98-103) as an expert slot
+    slot, parts = make_expert(ops.FP8_E8M0, dim, inter, seed=dim + 40, gpu=gpu)
+    x = data.activation(2, dim, seed=41)
+    y16 = np_(ops.expert_ffn(slot, x.to(gpu), ops.FP8_E8M0, dim, inter, 0.6, 10.0, official))
+    y32 = np_(ops.expert_ffn(slot, x.to(gpu), ops.FP8_E8M0, dim, inter, 0.6, 10.0, official, out_f32=True))
+    mats = deq_parts(ops.FP8_E8M0, parts)
+    for t in range(2):
+        o, raw = oracle.expert_ffn_deq(*mats, x[t].float().numpy(), 0.6, 10.0, official, raw=True)
+        assert_gemv(y32[t], y16[t], raw)
+
+
+@pytest.mark.parametrize("t", [1, 4])
+def test_moe_v41_semantics(gpu, t):
+    # the reference engine's MoE at V4.1 shapes (stbl/bench_gemv.py:15): dim 5120, inter 2304, top-6,
+    # FP4 routed experts + an FP8 E8M0 shared expert, official numerics (act_quant of x and of the
+    # SwiGLU output, stbl/model.cu:510,538), sqrt-softplus router with bias, SwiGLU limit 10
+    dim, inter, topk, n = 5120, 2304, 6, 8
+    experts = [make_expert(ops.FP4, dim, inter, seed=400 + 3 * i, gpu=gpu) for i in range(n)]
+    shared = make_expert(ops.FP8_E8M0, dim, inter, seed=490, gpu=gpu)
+    logits = data.zipf_logits(t, n, seed=43) * 2
+    bias = data.normal((n,), 0.05, seed=44)
+    ids, w = ops.route(logits.to(gpu), topk, bias.to(gpu), route_scale=2.5, score_fn=ops.SCORE_SQRT_SOFTPLUS)
+    _, oids, ow = oracle.route(logits.numpy(), topk, bias.numpy(), 2.5, score_fn=oracle.SCORE_SQRT_SOFTPLUS)
+    assert np_(ids).tolist() == oids.tolist()
+    assert np.allclose(np_(w), ow, rtol=8 * 2.0 ** -24, atol=0)
+    x = data.activation(t, dim, seed=45)
+    slots = [e[0] for e in experts] + [shared[0]]
+    y = np_(ops.moe_experts(x.to(gpu), slots, oids.tolist(), ow.tolist(), ops.FP4, dim, inter, shared=n, limit=10.0,
+                            official=True, shared_fmt=ops.FP8_E8M0))
+    mats = [deq_parts(ops.FP4, e[1]) for e in experts]
+    want = oracle.moe_deq([[mats[i] for i in row] for row in oids], ow, deq_parts(ops.FP8_E8M0, shared[1]),
+                          x.float().numpy(), limit=10.0, official=True)
+    u = bf16_ulps(y, want)
+    assert u.max() <= 1 and u.mean() < 0.02, (u.max(), u.mean())
+
+
+def test_route_sqrt_softplus(gpu):
+    t, e, topk = 4, 256, 6
+    logits = data.zipf_logits(t, e, seed=15) * 4  # spans both sides of the softplus threshold (20)
+    bias = data.normal((e,), 0.01, seed=16)
+    ids, w, sc = ops.route(logits.to(gpu), topk, bias.to(gpu), route_scale=2.5, want_scores=True,
+                           score_fn=ops.SCORE_SQRT_SOFTPLUS)
+    osc, oids, ow = oracle.route(logits.numpy(), topk, bias.numpy(), 2.5, score_fn=oracle.SCORE_SQRT_SOFTPLUS)
+    assert np_(ids).tolist() == oids.tolist()
+    # scores at the reference's own bar for this kernel, max |d| <= 1e-6 max |score|
+    # (stbl/test_kernels.py:208-211, the check metric of :47-52): for logits near -30 the device's
+    # expf differs from the host's by ~10 ulp of a value ~1e-13, invisible next to the selected scores
+    assert np.max(np.abs(np_(sc) - osc)) <= 1e-6 * np.max(np.abs(osc))
+    assert np.allclose(np_(w), ow, rtol=8 * 2.0 ** -24, atol=0)
 
 
 def test_route(gpu):
@@ -194,4 +262,31 @@ def test_moe_layer_end_to_end(gpu):
         assert bf16_ulps(y, want).max() <= 1
         hits_total = layer.cache.stats()["hits"]
     assert hits_total > 0
+    layer.close()
+
+
+def test_moe_layer_reference_engine_semantics(gpu):
+    # sqrt-softplus router, FP8 E8M0 shared expert next to FP4 routed experts, official numerics
+    dim, inter, n, topk, slots = 256, 128, 16, 3, 12
+    slot_bytes, _ = ops.expert_layout(ops.FP4, dim, inter)
+    pool = torch.empty(n * slot_bytes, dtype=torch.uint8, pin_memory=True)
+    mats = []
+    for e in range(n):
+        s, parts = make_expert(ops.FP4, dim, inter, seed=600 + 3 * e, gpu=gpu)
+        pool[e * slot_bytes:(e + 1) * slot_bytes].copy_(s.cpu())
+        mats.append(deq_parts(ops.FP4, parts))
+    shared, sparts = make_expert(ops.FP8_E8M0, dim, inter, seed=699, gpu=gpu)
+    bias = data.normal((n,), 0.05, seed=17)
+    layer = MoELayer(ops.FP4, dim, inter, pool, n, topk, slots, shared_slot=shared, bias=bias.to(gpu), route_scale=2.5,
+                     limit=10.0, official=True, score_fn=ops.SCORE_SQRT_SOFTPLUS, shared_fmt=ops.FP8_E8M0)
+    for step in range(6):
+        t = 1 + step % 4
+        logits = data.zipf_logits(t, n, seed=70 + step) * 2
+        x = data.activation(t, dim, seed=80 + step)
+        y = np_(layer.forward(x.to(gpu), logits.to(gpu)))
+        _, oids, ow = oracle.route(logits.numpy(), topk, bias.numpy(), 2.5, score_fn=oracle.SCORE_SQRT_SOFTPLUS)
+        assert [list(r) for r in layer.last_route[0]] == oids.tolist()
+        want = oracle.moe_deq([[mats[i] for i in row] for row in oids], ow, deq_parts(ops.FP8_E8M0, sparts),
+                              x.float().numpy(), limit=10.0, official=True)
+        assert bf16_ulps(y, want).max() <= 1
     layer.close()

@@ -73,6 +73,17 @@ def test_quant_fp8_b128_matches_oracle(gpu, rows, k):
     assert np.array_equal(np_(scales), os_)
     assert np.array_equal(np_(codes), oc)
 
+@pytest.mark.parametrize("rows,k", [(70, 96), (33, 32), (2304, 5120), (5120, 2304)])
+def test_quant_fp8_e8m0_matches_oracle(gpu, rows, k):
+    w = data.weight(rows, k, seed=rows + k)
+    w[0, :32] = 0  # a block row with a zero part
+    codes, scales = ops.quant_fp8_e8m0(w.to(gpu))
+    oc, os_ = oracle.quant_fp8_e8m0_b32(w.numpy())
+    assert np.array_equal(np_(codes), oc) and np.array_equal(np_(scales), os_)
+    deq = ops.dequant_fp8(codes, scales, e8m0=True)
+    assert bits_equal(np_(deq), oracle.dequant_fp8_e8m0_b32(oc, os_))
+
+
 
 @pytest.mark.parametrize("block,pow2", [(32, True), (128, True), (128, False)])
 def test_act_quant_matches_oracle(gpu, block, pow2):

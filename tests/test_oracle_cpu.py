@@ -283,6 +283,63 @@ def test_route_bias_and_scale():
     assert np.allclose(w[0], s / s.sum() * 2.5, rtol=1e-6)
 
 
+def test_route_score_sqrt_softplus():
+    # stbl/kernels.cu:436-442: sqrt(x > 20 ? x : log1p(exp(x))), fp32; checked against float64 within
+    # 2 ulp over [-30, 40], and the threshold itself: 20 takes log1p(exp), above 20 the identity
+    xs = np.concatenate([np.linspace(-30, 40, 7001), [20.0, np.nextafter(np.float32(20), 30), 19.99]]).astype(np.float32)
+    got = np.array([oracle.route_score(float(v), 1) for v in xs], np.float32)
+    x64 = xs.astype(np.float64)
+    want = np.sqrt(np.where(x64 > 20, x64, np.log1p(np.exp(x64))))
+    ulp = np.spacing(want.astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 2 * ulp)
+    assert oracle.route_score(20.0, 1) == np.float32(np.sqrt(np.log1p(np.exp(20.0))))
+    above = np.nextafter(np.float32(20), np.float32(30))
+    assert oracle.route_score(float(above), 1) == np.sqrt(above)
+    assert oracle.route_score(0.0, 0) == 0.5
+
+
+def test_route_sqrt_softplus_brute_force():
+    rng = np.random.default_rng(21)
+    t, e, k = 3, 64, 6
+    logits = (rng.standard_normal((t, e)) * 3).astype(np.float32)
+    logits[1, 5] = logits[1, 9]  # an exact tie: the lower id first
+    bias = (rng.standard_normal(e) * 0.1).astype(np.float32)
+    sc, ids, w = oracle.route(logits, k, bias=bias, route_scale=2.5, score_fn=oracle.SCORE_SQRT_SOFTPLUS)
+    for i in range(t):
+        want_sc = np.array([oracle.route_score(float(v), 1) for v in logits[i]], np.float32)
+        assert np.array_equal(sc[i], want_sc)
+        key = want_sc + bias
+        order = sorted(range(e), key=lambda j: (-key[j], j))[:k]
+        assert ids[i].tolist() == order
+        tot = np.float32(0)
+        for j in order:
+            tot = np.float32(tot + want_sc[j])
+        ww = (want_sc[order] / np.float32(tot + np.float32(1e-20))) * np.float32(2.5)
+        assert np.array_equal(w[i], ww.astype(np.float32))
+
+
+def test_quant_fp8_e8m0_b32_properties():
+    rng = np.random.default_rng(22)
+    rows, k = 70, 96  # a partial last row block
+    w = (rng.standard_normal((rows, k)) * 0.02).astype(np.float32)
+    w[0:32, 0:32] = 0  # an all-zero block takes the 1e-4 floor
+    w[32:64, 32:64] *= 1e4
+    codes, sc = oracle.quant_fp8_e8m0_b32(w)
+    assert sc.shape == (3, 3)
+    for bi in range(3):
+        for bj in range(3):
+            blk = w[32 * bi:32 * bi + 32, 32 * bj:32 * bj + 32]
+            t = np.float32(max(np.abs(blk).max(), np.float32(1e-4)) * np.float32(1 / 448))
+            s = 2.0 ** np.ceil(np.log2(np.float64(t)))  # pow2_ceil by log2 of the fp32 value
+            assert sc[bi, bj] == 127 + int(np.log2(s))
+            q = np.clip(blk / np.float32(s), -448, 448).astype(np.float32)
+            assert np.array_equal(codes[32 * bi:32 * bi + 32, 32 * bj:32 * bj + 32], oracle.e4m3_encode(q))
+    # round trip: half an e4m3 step (2^-4 relative), or half the subnormal step 2^-9 * s
+    deq = oracle.dequant_fp8_e8m0_b32(codes, sc)
+    s_el = np.repeat(np.repeat(2.0 ** (sc.astype(np.int32) - 127), 32, 0)[:rows], 32, 1)
+    assert np.all(np.abs(deq - w) <= np.abs(w) * 2.0 ** -4 + 2.0 ** -10 * s_el)
+
+
 # ---- expert FFN / MoE composition ----------------------------------------------------------------------
 
 def _fp4_slot(rng, dim, inter):
@@ -338,6 +395,32 @@ def test_moe_fp4_sum_order():
             acc = acc + oracle.expert_ffn_fp4(slots[e][0], dim, inter, x[t], wts[t, p])
         acc = acc + oracle.expert_ffn_fp4(slots[3][0], dim, inter, x[t], 1.0)
         assert np.array_equal(y[t], oracle.bf16_round(acc))
+
+
+@pytest.mark.parametrize("official", [False, True])
+def test_expert_ffn_deq_equals_fp4_path(official):
+    # the format-independent composition on dequantized matrices against the pinned FP4 one
+    rng = np.random.default_rng(23)
+    dim, inter = 256, 128
+    slot, mats = _fp4_slot(rng, dim, inter)
+    x = oracle.bf16_round(rng.standard_normal(dim).astype(np.float32))
+    a = oracle.expert_ffn_fp4(slot, dim, inter, x, 0.7, 3.0, official)
+    b = oracle.expert_ffn_deq(*mats, x, 0.7, 3.0, official)
+    assert np.all(np.abs(a - b) <= np.abs(a) * 2.0 ** -7 + 1e-30)
+    assert np.mean(a == b) > 0.99
+
+
+def test_moe_deq_equals_fp4_path():
+    rng = np.random.default_rng(24)
+    dim, inter = 128, 64
+    slots = [_fp4_slot(rng, dim, inter) for _ in range(4)]
+    x = oracle.bf16_round(rng.standard_normal((2, dim)).astype(np.float32))
+    picks = [[0, 2, 1], [3, 0, 2]]
+    wts = np.array([[0.5, 0.3, 0.2], [0.6, 0.25, 0.15]], np.float32)
+    a = oracle.moe_fp4([[slots[e][0] for e in row] for row in picks], wts, slots[3][0], dim, inter, x, 2.0, True)
+    b = oracle.moe_deq([[slots[e][1] for e in row] for row in picks], wts, slots[3][1], x, 2.0, True)
+    assert np.all(np.abs(a - b) <= np.abs(a) * 2.0 ** -7 + 1e-30)
+    assert np.mean(a == b) > 0.99
 
 
 # ---- expert LRU bookkeeping ------------------------------------------------------------------------------
