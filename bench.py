@@ -35,7 +35,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="all", help="fp4 (headline only) | gemv | ffn | gemm | moe | all")
+    ap.add_argument("--only", default="all",
+                    help="fp4 (headline only) | gemv | batch | ffn | gemm | moe | moeallhit | refabi | all")
     ap.add_argument("--moe-steps", type=int, default=200)
     ap.add_argument("--moe-warmup", type=int, default=1000)
     ap.add_argument("--eager", action="store_true", help="also time launches issued one by one from Python")
@@ -219,28 +220,38 @@ def moe_workload(torch, tokens, steps, warmup_steps):
             "refill_GB_s": (st1["refill_bytes"] - st0["refill_bytes"]) / el / 1e9}
 
 
-def moe_allhit_workload(torch, tokens, steps, warmup):
+def moe_allhit_workload(torch, tokens, steps, warmup, v41=False):
     """C4's expert kernels alone with every expert resident (the kernel bound of the layer): per
     step, each token's 8 routed experts are drawn from 64 resident slots (1.5 GB, so weights come
-    from HBM) plus the shared expert; algorithmic bytes = every distinct expert's weights once."""
+    from HBM) plus the shared expert; algorithmic bytes = every distinct expert's weights once.
+    v41: the reference engine's own MoE instead (stbl/model.cu:426-594 at stbl/bench_gemv.py:15's
+    shapes): dim 5120, inter 2304, top-6 FP4 experts + an FP8 E8M0 shared expert, official numerics
+    (act_quant of the input and of the SwiGLU output), SwiGLU limit 10."""
     import numpy as np
 
     from stblarge_amd import data, ops
 
     dev = torch.device("cuda:0")
     dim, inter, topk, nres = data.DIM, data.INTER, data.TOPK, data.CACHE_SLOTS
+    if v41:
+        dim, inter, topk = 5120, 2304, 6
     fmt = ops.FP4
+    sfmt = ops.FP8_E8M0 if v41 else fmt
     base = ops.quant_expert(data.weight(inter, dim, 21, dev), data.weight(inter, dim, 22, dev),
                             data.weight(dim, inter, 23, dev), fmt)
-    res = [base.clone() for _ in range(nres + 1)]
-    wbytes = sum(ops._mat_bytes(fmt, r, k) for r, k in ((inter, dim), (inter, dim), (dim, inter)))
+    res = [base.clone() for _ in range(nres)]
+    res.append(ops.quant_expert(data.weight(inter, dim, 24, dev), data.weight(inter, dim, 25, dev),
+                                data.weight(dim, inter, 26, dev), sfmt))
+    shapes = ((inter, dim), (inter, dim), (dim, inter))
+    wbytes = sum(ops._mat_bytes(fmt, r, k) for r, k in shapes)
+    sbytes = sum(ops._mat_bytes(sfmt, r, k) for r, k in shapes)
     rng = np.random.default_rng(5)
     plans = []
     for _ in range(16):
         pick = [list(rng.choice(nres, size=topk, replace=False)) for _ in range(tokens)]
         uniq = sorted({e for row in pick for e in row})
         slot_of = {e: i for i, e in enumerate(uniq)}
-        plans.append(([res[e] for e in uniq] + [res[nres]], [[slot_of[e] for e in row] for row in pick], len(uniq) + 1))
+        plans.append(([res[e] for e in uniq] + [res[nres]], [[slot_of[e] for e in row] for row in pick], len(uniq)))
     w = [[1.0 / topk] * topk for _ in range(tokens)]
     x = data.activation(tokens, dim, seed=24, device=dev)
     y = torch.empty((tokens, dim), dtype=torch.bfloat16, device=dev)
@@ -248,13 +259,62 @@ def moe_allhit_workload(torch, tokens, steps, warmup):
 
     def launch(i):
         sl, pick, _ = plans[i]
-        ops.moe_experts(x, sl, pick, w, fmt, dim, inter, shared=len(sl) - 1, work=work, out=y)
+        ops.moe_experts(x, sl, pick, w, fmt, dim, inter, shared=len(sl) - 1, work=work, out=y, shared_fmt=sfmt,
+                        official=v41, limit=10.0 if v41 else 0.0)
 
     ms, n = timed_steps(torch, launch, len(plans), steps, warmup)
-    alg = np.mean([p[2] for p in plans]) * wbytes + 4 * dim * tokens
+    alg = np.mean([p[2] for p in plans]) * wbytes + sbytes + 4 * dim * tokens
     gbs = alg / (ms * 1e-3) / 1e9
-    return {"workload": f"moe_experts_allhit_t{tokens}_fp4", "ms_per_step": ms, "steps": n, "tokens_per_s":
+    name = f"moe_v41_allhit_t{tokens}_fp4_top6_fp8e8m0_shared" if v41 else f"moe_experts_allhit_t{tokens}_fp4"
+    return {"workload": name, "ms_per_step": ms, "steps": n, "tokens_per_s":
             tokens / (ms * 1e-3), "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS}
+
+
+def compat_gemv_workload(torch, kind, rows, k, steps, warmup):
+    """The reference ABI's GEMVs at the reference's own benchmark shapes (stbl/bench_gemv.py:15,
+    :35-48, :93-95): stbl_gemv_mxfp4 on GGUF rows (scale bytes 120, random codes), stbl_gemv_fp8 on
+    E8M0 32x32 FP8 (codes < 120, scale bytes 120), fp32 x and y, round_out; stbl_gemv_f32 for the
+    router. Unlike the reference's loop, every launch reads a different weight copy (>= 512 MB)."""
+    from stblarge_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(rows + k)
+    if kind == "mxfp4":
+        w = torch.randint(0, 256, (rows, k // 32 * 17), dtype=torch.uint8, device=dev, generator=g)
+        w[:, ::17] = 120
+        s = None
+        wb = w.numel()
+    elif kind == "fp8":
+        w = torch.randint(0, 120, (rows, k), dtype=torch.uint8, device=dev, generator=g)
+        s = torch.full(((rows + 31) // 32, k // 32), 120, dtype=torch.uint8, device=dev)
+        wb = w.numel() + s.numel()
+    else:
+        w = torch.randn((rows, k), device=dev, generator=g) * 0.02
+        s = None
+        wb = w.numel() * 4
+    copies = max(2, math.ceil(ROTATE_BYTES / wb))
+    ws = [w.clone() for _ in range(copies)]
+    x = torch.randn(k, device=dev, generator=g)
+    y = torch.empty(rows, device=dev)
+    lib = _lib.load()
+    st = ops._stream
+
+    def launch(i):
+        if kind == "mxfp4":
+            lib.stbl_gemv_mxfp4(ops._ptr(y), ops._ptr(ws[i]), ops._ptr(x), rows, k, st())
+        elif kind == "fp8":
+            lib.stbl_gemv_fp8(ops._ptr(y), ops._ptr(ws[i]), ops._ptr(s), ops._ptr(x), rows, k, 1, st())
+        else:
+            lib.stbl_gemv_f32(ops._ptr(y), ops._ptr(ws[i]), ops._ptr(x), rows, k, 0, st())
+
+    launch(0)
+    _lib.check(None, f"stbl_gemv_{kind}")
+    ms, n = timed_steps(torch, launch, copies, steps, warmup)
+    alg = wb + 4 * k + 4 * rows
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"workload": f"ref_abi_gemv_{kind}_{rows}x{k}", "ms_per_step": ms, "steps": n, "alg_bytes": alg,
+            "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS, "weight_copies": copies}
 
 
 def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168, prequant=False):
@@ -384,9 +444,16 @@ def main():
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s, "
                   f"{r['TFLOP_s']:.0f} TFLOP/s ({100 * r['frac_mfma_peak']:.1f}% MFMA)", file=sys.stderr, flush=True)
+    if args.only in ("all", "refabi"):
+        for kind, rows, k in (("mxfp4", 2304, 5120), ("mxfp4", 5120, 2304), ("fp8", 2304, 5120), ("fp8", 5120, 2304),
+                              ("f32", 256, 5120)):
+            r = compat_gemv_workload(torch, kind, rows, k, args.steps, args.warmup)
+            extra[r["workload"]] = r
+            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
+                  flush=True)
     if args.only in ("all", "moe", "moeallhit"):
-        for t in (1, 4):
-            r = moe_allhit_workload(torch, t, max(100, args.steps // 10), 32)
+        for t, v41 in ((1, False), (4, False), (1, True), (4, True)):
+            r = moe_allhit_workload(torch, t, max(100, args.steps // 10), 32, v41=v41)
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s, "
                   f"{r['GB_s']:.0f} GB/s", file=sys.stderr, flush=True)

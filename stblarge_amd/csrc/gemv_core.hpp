@@ -144,10 +144,18 @@ __device__ __forceinline__ void act_quant_chunk(float (&xf)[M][CH]) {
         if constexpr (CH == 16)
             a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0xB1, 0xF, 0xF, false)));
         const float s = pow2_ceil(fmaxf(a, 1e-4f) * (1.0f / 448.0f));
+        // 1/s is a power of two too (s lies in [2^-22, 2^120]), so x * inv is x / s exactly; the
+        // hardware conversion rounds to nearest even like the reference's cast (it equals the
+        // software encoder f32_to_e4m3 on every bf16 input, and x / s of a bf16 x is a bf16 value);
+        // e4m3(q) * s is exact and bf16-representable, so bf16(e4m3(q) * s) needs no rounding step.
+        const float inv = __uint_as_float((254u - ((__float_as_uint(s) >> 23) & 0xffu)) << 23);
 #pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const float q = fminf(fmaxf(xf[t][i] / s, -448.f), 448.f);  // exact: s is a power of two
-            xf[t][i] = bf16_round(e4m3_to_f32(f32_to_e4m3(q)) * s);
+        for (int i = 0; i < CH; i += 2) {
+            const float q0 = fminf(fmaxf(xf[t][i] * inv, -448.f), 448.f);
+            const float q1 = fminf(fmaxf(xf[t][i + 1] * inv, -448.f), 448.f);
+            const f32x2 d = e4m3x2((uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0, false), false);
+            xf[t][i] = d.x * s;
+            xf[t][i + 1] = d.y * s;
         }
     }
 }
