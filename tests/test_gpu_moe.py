@@ -81,6 +81,23 @@ def test_moe_experts_fp4(gpu, t, official):
     assert u.max() <= 1 and u.mean() < 0.02, (u.max(), u.mean())
 
 
+@pytest.mark.parametrize("v41", [False, True])
+def test_moe_one_token_equals_two_identical_tokens(gpu, v41):
+    # one token runs the single-token kernels, the same token twice the two-token ones: every token's
+    # sums use the same lanes in the same order, so the results agree bit for bit
+    dim, inter, topk, n = (5120, 2304, 6, 8) if v41 else (1024, 512, 4, 6)
+    sfmt = ops.FP8_E8M0 if v41 else ops.FP4
+    experts = [make_expert(ops.FP4, dim, inter, seed=700 + 3 * i, gpu=gpu) for i in range(n - 1)]
+    experts.append(make_expert(sfmt, dim, inter, seed=790, gpu=gpu))
+    pick = [[3, 0, 5, 1, 2, 4][:topk]]
+    w = [[0.3, 0.25, 0.2, 0.1, 0.1, 0.05][:topk]]
+    x = data.activation(1, dim, seed=71).to(gpu)
+    kw = dict(shared=n - 1, limit=10.0, official=v41, shared_fmt=sfmt)
+    y1 = ops.moe_experts(x, [e[0] for e in experts], pick, w, ops.FP4, dim, inter, **kw)
+    y2 = ops.moe_experts(torch.cat([x, x]), [e[0] for e in experts], pick * 2, w * 2, ops.FP4, dim, inter, **kw)
+    assert torch.equal(y1[0], y2[0]) and torch.equal(y1[0], y2[1])
+
+
 def test_moe_experts_shared_token_groups(gpu):
     # six tokens all routed to the same two experts: jobs of <= 4 tokens are split (4 + 2)
     dim, inter, topk = 256, 128, 2
