@@ -300,10 +300,13 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
 
 static inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
-template <WFmt F, int M>
-static hipError_t launch_gateup(const MoeJobs &jobs, int n, const ExpertLayout &L, const uint16_t *x, uint16_t *h,
-                                int dim, int inter, float limit, int official, hipStream_t st) {
-    constexpr int R = 4;  // gate + up: 8 rows share the x chunk (2 rows for M > 1 measured 6-11% slower at T=4)
+// Rows per workgroup. Several experts per launch: 4 gate and 4 up rows share a lane's x chunk, and
+// 8 down rows (4 with 4 tokens), measured best for the MoE steps (2 rows for more than one token
+// was 6-11% slower at T=4). One expert per launch (the FFN on its own): 2 and 2, which keep 4x more
+// workgroups in flight (measured 4-6% faster for one FP4 / FP8 expert).
+template <WFmt F, int M, int R>
+static hipError_t launch_gateup_r(const MoeJobs &jobs, int n, const ExpertLayout &L, const uint16_t *x, uint16_t *h,
+                                  int dim, int inter, float limit, int official, hipStream_t st) {
     const int waves = ceil_div(dim / WTraits<F>::CH, 64);
     hipLaunchKernelGGL((k_moe_gateup<F, M, R>), dim3(ceil_div(inter, R), n), dim3(64 * waves), 0, st, jobs, L, x, h,
                        dim, inter, limit, official);
@@ -311,13 +314,26 @@ static hipError_t launch_gateup(const MoeJobs &jobs, int n, const ExpertLayout &
 }
 
 template <WFmt F, int M>
-static hipError_t launch_down(const MoeJobs &jobs, int n, const ExpertLayout &L, const uint16_t *h, void *o, int dim,
-                              int inter, int official, int out_f32, hipStream_t st) {
-    constexpr int R = M == 4 ? 4 : 8;  // measured best at T=4 over R = 2 for M > 1
+static hipError_t launch_gateup(const MoeJobs &jobs, int n, const ExpertLayout &L, const uint16_t *x, uint16_t *h,
+                                int dim, int inter, float limit, int official, hipStream_t st) {
+    if (n == 1) return launch_gateup_r<F, M, 2>(jobs, n, L, x, h, dim, inter, limit, official, st);
+    return launch_gateup_r<F, M, 4>(jobs, n, L, x, h, dim, inter, limit, official, st);
+}
+
+template <WFmt F, int M, int R>
+static hipError_t launch_down_r(const MoeJobs &jobs, int n, const ExpertLayout &L, const uint16_t *h, void *o, int dim,
+                                int inter, int official, int out_f32, hipStream_t st) {
     const int waves = ceil_div(inter / WTraits<F>::CH, 64);
     hipLaunchKernelGGL((k_moe_down<F, M, R>), dim3(ceil_div(dim, R), n), dim3(64 * waves), 0, st, jobs, L, h, o, dim,
                        inter, official, out_f32);
     return hipGetLastError();
+}
+
+template <WFmt F, int M>
+static hipError_t launch_down(const MoeJobs &jobs, int n, const ExpertLayout &L, const uint16_t *h, void *o, int dim,
+                              int inter, int official, int out_f32, hipStream_t st) {
+    if (n == 1) return launch_down_r<F, M, 2>(jobs, n, L, h, o, dim, inter, official, out_f32, st);
+    return launch_down_r<F, M, M == 4 ? 4 : 8>(jobs, n, L, h, o, dim, inter, official, out_f32, st);
 }
 
 // Runs the jobs (sorted into launches by token count) through gate/up and down.
