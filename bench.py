@@ -270,11 +270,12 @@ def moe_allhit_workload(torch, tokens, steps, warmup, v41=False):
             tokens / (ms * 1e-3), "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS}
 
 
-def compat_gemv_workload(torch, kind, rows, k, steps, warmup):
+def compat_gemv_workload(torch, kind, rows, k, steps, warmup, group_rows=0):
     """The reference ABI's GEMVs at the reference's own benchmark shapes (stbl/bench_gemv.py:15,
-    :35-48, :93-95): stbl_gemv_mxfp4 on GGUF rows (scale bytes 120, random codes), stbl_gemv_fp8 on
-    E8M0 32x32 FP8 (codes < 120, scale bytes 120), fp32 x and y, round_out; stbl_gemv_f32 for the
-    router. Unlike the reference's loop, every launch reads a different weight copy (>= 512 MB)."""
+    :35-62, :80-85, :93-107): stbl_gemv_mxfp4 on GGUF rows (scale bytes 120, random codes),
+    stbl_gemv_fp8 on E8M0 32x32 FP8 (codes < 120, scale bytes 120), stbl_gemv_bf16 (optionally
+    grouped x), fp32 x and y, round_out; stbl_gemv_f32 for the router. Unlike the reference's loop,
+    every launch reads a different weight copy (>= 512 MB)."""
     from stblarge_amd import _lib, ops
 
     dev = torch.device("cuda:0")
@@ -289,13 +290,18 @@ def compat_gemv_workload(torch, kind, rows, k, steps, warmup):
         w = torch.randint(0, 120, (rows, k), dtype=torch.uint8, device=dev, generator=g)
         s = torch.full(((rows + 31) // 32, k // 32), 120, dtype=torch.uint8, device=dev)
         wb = w.numel() + s.numel()
+    elif kind == "bf16":
+        w = (torch.randn((rows, k), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        s = None
+        wb = w.numel() * 2
     else:
         w = torch.randn((rows, k), device=dev, generator=g) * 0.02
         s = None
         wb = w.numel() * 4
     copies = max(2, math.ceil(ROTATE_BYTES / wb))
     ws = [w.clone() for _ in range(copies)]
-    x = torch.randn(k, device=dev, generator=g)
+    xrows = (rows + group_rows - 1) // group_rows if group_rows else 1
+    x = torch.randn(xrows * k, device=dev, generator=g)
     y = torch.empty(rows, device=dev)
     lib = _lib.load()
     st = ops._stream
@@ -305,15 +311,18 @@ def compat_gemv_workload(torch, kind, rows, k, steps, warmup):
             lib.stbl_gemv_mxfp4(ops._ptr(y), ops._ptr(ws[i]), ops._ptr(x), rows, k, st())
         elif kind == "fp8":
             lib.stbl_gemv_fp8(ops._ptr(y), ops._ptr(ws[i]), ops._ptr(s), ops._ptr(x), rows, k, 1, st())
+        elif kind == "bf16":
+            lib.stbl_gemv_bf16(ops._ptr(y), ops._ptr(ws[i]), ops._ptr(x), rows, k, 1, group_rows, st())
         else:
             lib.stbl_gemv_f32(ops._ptr(y), ops._ptr(ws[i]), ops._ptr(x), rows, k, 0, st())
 
     launch(0)
     _lib.check(None, f"stbl_gemv_{kind}")
     ms, n = timed_steps(torch, launch, copies, steps, warmup)
-    alg = wb + 4 * k + 4 * rows
+    alg = wb + 4 * k * xrows + 4 * rows
     gbs = alg / (ms * 1e-3) / 1e9
-    return {"workload": f"ref_abi_gemv_{kind}_{rows}x{k}", "ms_per_step": ms, "steps": n, "alg_bytes": alg,
+    name = f"ref_abi_gemv_{kind}_{rows}x{k}" + (f"_group{group_rows}" if group_rows else "")
+    return {"workload": name, "ms_per_step": ms, "steps": n, "alg_bytes": alg,
             "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS, "weight_copies": copies}
 
 
@@ -445,9 +454,11 @@ def main():
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s, "
                   f"{r['TFLOP_s']:.0f} TFLOP/s ({100 * r['frac_mfma_peak']:.1f}% MFMA)", file=sys.stderr, flush=True)
     if args.only in ("all", "refabi"):
-        for kind, rows, k in (("mxfp4", 2304, 5120), ("mxfp4", 5120, 2304), ("fp8", 2304, 5120), ("fp8", 5120, 2304),
-                              ("f32", 256, 5120)):
-            r = compat_gemv_workload(torch, kind, rows, k, args.steps, args.warmup)
+        for kind, rows, k, grp in (("mxfp4", 2304, 5120, 0), ("mxfp4", 5120, 2304, 0), ("fp8", 2304, 5120, 0),
+                                   ("fp8", 5120, 2304, 0), ("bf16", 4096, 5120, 0), ("fp8", 32768, 1280, 0),
+                                   ("fp8", 5120, 8192, 0), ("fp8", 1280, 5120, 0), ("fp8", 512, 5120, 0),
+                                   ("bf16", 8192, 4096, 1024), ("f32", 256, 5120, 0)):
+            r = compat_gemv_workload(torch, kind, rows, k, args.steps, args.warmup, grp)
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
                   flush=True)

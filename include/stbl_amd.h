@@ -46,6 +46,12 @@ void stbl_gemv_fp8(float *y, const void *w, const void *scale, const float *x, i
  * 16+i high nibble]); y = bf16(W x) stored as fp32. k % 256 == 0, k <= 16384, w 8-byte aligned. */
 void stbl_gemv_mxfp4(float *y, const void *w, const float *x, int rows, int k, hipStream_t st);
 
+/* y[r] = sum_i x_r[i] * w[r][i] in fp32 (bf16-rounded when round_out), bf16 weights [rows][k]; x_r = x
+ * + (r / group_rows) * k when group_rows > 0, else x. Replaces stbl_gemv_bf16 (stbl/kernels.h:21-22,
+ * stbl/kernels.cu:193-204): the attention output projection (grouped) and the head. */
+void stbl_gemv_bf16(float *y, const void *w, const float *x, int rows, int k, int round_out, int group_rows,
+                    hipStream_t st);
+
 /* y[r] = sum_k x[k] * w[r][k] in fp32 (bf16-rounded when round_out), fp32 weights [rows][k]: the
  * router's logits. Replaces stbl_gemv_f32 (stbl/kernels.h:23, stbl/kernels.cu:206-214). */
 void stbl_gemv_f32(float *y, const float *w, const float *x, int rows, int k, int round_out, hipStream_t st);

@@ -174,6 +174,62 @@ __global__ __launch_bounds__(256) void k_gemv_f32(float *__restrict__ y, const f
     }
 }
 
+// bf16-weight GEMV (stbl/kernels.cu:193-204, the attention output and the head): y[r] = sum_i
+// x_r[i] * w[r][i] with x_r = x + (r / group_rows) * k when group_rows > 0 (the block-diagonal wo_a
+// product), fp32 accumulation, bf16-rounded when round_out. A wave owns R rows (which share one x
+// row: group_rows % R == 0); with VEC (k % 8 == 0, 16-byte aligned w rows and x) every lane streams
+// 16-byte units of 8 weights, U units of each row in flight, else one element at a time.
+template <int R, bool VEC>
+__global__ __launch_bounds__(256) void k_gemv_bf16(float *__restrict__ y, const uint16_t *__restrict__ w,
+                                                   const float *__restrict__ x, int rows, int k, int round_out,
+                                                   int group_rows) {
+    constexpr int U = 4;
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+    if (row0 >= rows) return;  // a whole wave
+    const float *xr = x + (group_rows > 0 ? (size_t)(row0 / group_rows) * k : 0);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
+    if constexpr (VEC) {
+        const int n8 = k >> 3;
+        for (int base = lane; base < n8; base += 64 * U) {
+            u32x4 wv[R][U];
+            f32x4 xv[U][2];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int i = base + 64 * u, ic = i < n8 ? i : 0;
+                xv[u][0] = *(const f32x4 *)(xr + 8 * (size_t)ic);
+                xv[u][1] = *(const f32x4 *)(xr + 8 * (size_t)ic + 4);
+#pragma unroll
+                for (int r = 0; r < R; r++)
+                    wv[r][u] = ld_stream(w + (size_t)min(row0 + r, rows - 1) * k + 8 * (size_t)ic);
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                if (base + 64 * u >= n8) continue;
+#pragma unroll
+                for (int r = 0; r < R; r++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        acc[r] = fmaf(xv[u][j >> 1][2 * (j & 1)], bf16_lo(wv[r][u][j]), acc[r]);
+                        acc[r] = fmaf(xv[u][j >> 1][2 * (j & 1) + 1], bf16_hi(wv[r][u][j]), acc[r]);
+                    }
+            }
+        }
+    } else {
+        for (int i = lane; i < k; i += 64)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                acc[r] = fmaf(xr[i], bf16_bits_to_f32(w[(size_t)min(row0 + r, rows - 1) * k + i]), acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const float tot = dpp_sum(acc[r]);
+        if (lane == 63 && row0 + r < rows) y[row0 + r] = round_out ? bf16_round(tot) : tot;
+    }
+}
+
 static inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 template <WFmt F, bool XF32, int M, int R>
@@ -302,6 +358,25 @@ void stbl_gemv_mxfp4_batch(float *const *y, const void *const *w, const float *c
 // stbl/kernels.h:16.
 void stbl_gemv_mxfp4(float *y, const void *w, const float *x, int rows, int k, hipStream_t st) {
     stbl_gemv_mxfp4_batch(&y, &w, &x, 1, rows, k, st);
+}
+
+// stbl/kernels.h:21-22 (bf16 weights; group_rows > 0: row r reads x + (r / group_rows) * k). Any k;
+// the 16-byte path when k % 8 == 0 and w, x are 16-byte aligned.
+void stbl_gemv_bf16(float *y, const void *w, const float *x, int rows, int k, int round_out, int group_rows,
+                    hipStream_t st) {
+    if (!y || !w || !x || rows <= 0 || k <= 0 || group_rows < 0) {
+        abi_fail(hipErrorInvalidValue, "stbl_gemv_bf16: bad arguments (rows=%d k=%d group_rows=%d)", rows, k, group_rows);
+        return;
+    }
+    const bool vec = k % 8 == 0 && aligned16(w) && aligned16(x);
+    const bool two = group_rows == 0 || group_rows % 2 == 0;  // two rows per wave must share an x row
+    const dim3 grid(ceil_div(rows, 4 * (two ? 2 : 1)));
+    const uint16_t *wb = (const uint16_t *)w;
+    if (vec && two) hipLaunchKernelGGL((k_gemv_bf16<2, true>), grid, dim3(256), 0, st, y, wb, x, rows, k, round_out, group_rows);
+    else if (vec) hipLaunchKernelGGL((k_gemv_bf16<1, true>), grid, dim3(256), 0, st, y, wb, x, rows, k, round_out, group_rows);
+    else if (two) hipLaunchKernelGGL((k_gemv_bf16<2, false>), grid, dim3(256), 0, st, y, wb, x, rows, k, round_out, group_rows);
+    else hipLaunchKernelGGL((k_gemv_bf16<1, false>), grid, dim3(256), 0, st, y, wb, x, rows, k, round_out, group_rows);
+    abi_status(hipGetLastError(), "stbl_gemv_bf16 launch");
 }
 
 // stbl/kernels.h:23 (the router's logits, stbl/model.cu:430). Any k; the 16-byte path when k % 4 == 0

@@ -258,6 +258,20 @@ def stbl_gemv_f32(y, w, x, rows, k, round_out=0):
     return y
 
 
+def stbl_gemv_bf16(y, w, x, rows, k, round_out=0, group_rows=0):
+    """bf16-weight GEMV of the reference ABI: y [rows] = w [rows, k] . x_r with x_r the (r /
+    group_rows)-th k-long row of x when group_rows > 0."""
+    _need(y, torch.float32, "y")
+    _need(w, torch.bfloat16, "w")
+    _need(x, torch.float32, "x")
+    xrows = (rows + group_rows - 1) // group_rows if group_rows > 0 else 1
+    if y.numel() < rows or w.numel() < rows * k or x.numel() < xrows * k:
+        raise ValueError("stbl_gemv_bf16: buffer sizes do not match rows/k/group_rows")
+    _lib.load().stbl_gemv_bf16(_ptr(y), _ptr(w), _ptr(x), rows, k, int(round_out), int(group_rows), _stream())
+    _lib.check(None, "stbl_gemv_bf16")
+    return y
+
+
 def stbl_swiglu(out, g, u, weight, limit, n):
     return stbl_swiglu_batch(out, g, u, [weight], limit, n)
 

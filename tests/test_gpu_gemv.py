@@ -83,7 +83,9 @@ def test_gemv_fp4_zero_and_extreme_inputs(gpu):
 
 # ---- the reference engine's ABI ------------------------------------------------------------------
 
-@pytest.mark.parametrize("rows,k,round_out", [(1000, 1280, 1), (2048, 7168, 0), (64, 96, 1)])
+@pytest.mark.parametrize("rows,k,round_out", [(1000, 1280, 1), (2048, 7168, 0), (64, 96, 1),
+                                               # the attention-side shapes of stbl/bench_gemv.py:103-107
+                                               (32768, 1280, 1), (5120, 8192, 1), (1280, 5120, 0), (512, 5120, 1)])
 def test_stbl_gemv_fp8_e8m0(gpu, rows, k, round_out):
     # stbl/test_kernels.py:82-98 input idiom: e4m3 weights, E8M0 scales 2^U[-14,-7] per 32x32
     rng = np.random.default_rng(rows)
@@ -164,6 +166,31 @@ def test_stbl_gemv_f32(gpu, rows, k, round_out):
     want = oracle.gemm(x.numpy()[None], w.numpy())[0]
     y = torch.empty(rows, device=gpu)
     ops.stbl_gemv_f32(y, w.to(gpu), x.to(gpu), rows, k, round_out)
+    got = np_(y)
+    if round_out:
+        assert np.array_equal(got, oracle.bf16_round(got))
+        assert np.max(np.abs(got - want)) <= np.max(np.abs(want)) * (1e-5 + 2.0 ** -8)
+    else:
+        assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
+
+
+@pytest.mark.parametrize("rows,k,round_out,group_rows", [(4096, 5120, 1, 0), (8192, 4096, 1, 1024), (100, 1001, 0, 0),
+                                                         (33, 520, 0, 11), (64, 256, 0, 16)])
+def test_stbl_gemv_bf16(gpu, rows, k, round_out, group_rows):
+    # bf16 weights (stbl/kernels.cu:193-204): the head (4096 x 5120, stbl/bench_gemv.py:96) and the
+    # block-diagonal wo_a product (8192 x 4096, groups of 1024 rows, :80-85); odd shapes take the
+    # one-element path and the one-row-per-wave path (group_rows odd)
+    w = data.normal((rows, k), 0.02, seed=rows + k).to(torch.bfloat16)
+    xrows = (rows + group_rows - 1) // group_rows if group_rows else 1
+    x = data.normal((xrows, k), 1.0, seed=k + 1)
+    wf, xf = w.float().numpy(), x.numpy()
+    want = np.array([oracle.gemm(xf[(r // group_rows) if group_rows else 0][None], wf[r:r + 1])[0, 0]
+                     for r in range(rows)]) if rows * k <= 2 ** 20 else None
+    if want is None:
+        want = np.concatenate([oracle.gemm(xf[g][None], wf[g * (group_rows or rows):(g + 1) * (group_rows or rows)])[0]
+                               for g in range(xrows)])
+    y = torch.empty(rows, device=gpu)
+    ops.stbl_gemv_bf16(y, w.to(gpu), x.to(gpu), rows, k, round_out, group_rows)
     got = np_(y)
     if round_out:
         assert np.array_equal(got, oracle.bf16_round(got))
