@@ -248,7 +248,8 @@ int stbl_amd_cache_fail_refill_after(void *cache, int n);
  * launches, stbl/kernels.cu:545-640). */
 int stbl_amd_last_error(char *buf, int len);
 
-/* ABI version of this library. */
+/* ABI version of this library, raised whenever an exported function's signature or meaning changes
+ * (stblarge_amd/cmp_builds.py compares two builds only at equal versions). */
 int stbl_amd_version(void);
 
 #ifdef __cplusplus

@@ -28,6 +28,7 @@ int stbl_amd_last_error(char *buf, int len) {
     return code;
 }
 
-int stbl_amd_version(void) { return 1; }
+// The ABI version: raised whenever the signature or meaning of an exported function changes.
+int stbl_amd_version(void) { return 2; }
 
 }  // extern "C"
