@@ -36,7 +36,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="all",
-                    help="fp4 (headline only) | gemv | batch | ffn | gemm | moe | moeallhit | refabi | all")
+                    help="fp4 (headline only) | gemv | batch | ffn | gemm | moe | moeallhit | refabi | file | all")
     ap.add_argument("--moe-steps", type=int, default=200)
     ap.add_argument("--moe-warmup", type=int, default=1000)
     ap.add_argument("--eager", action="store_true", help="also time launches issued one by one from Python")
@@ -364,6 +364,62 @@ def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168, prequant=Fals
             "TFLOP_s": flops / (ms * 1e-3) / 1e12, "frac_mfma_peak": flops / (ms * 1e-3) / 1e12 / peak_tf}
 
 
+def file_tier_workload(torch, mode, readers=8, n_experts=40, per_lookup=1, lookups=30):
+    """The expert cache's file tier: misses read from a GGUF file of V4.1 routed experts (dim 5120,
+    inter 2304, MXFP4: 18,800,640 bytes per expert, the size the reference's SSD bench reads,
+    scripts/ssd_expert_bench.py:10) in 2 MiB pieces by `readers` threads, copied to the device and
+    repacked into FP4 slots. Each lookup asks for per_lookup experts that are not cached; the time
+    is host wall clock from the lookup to the end of the repack. mode: "direct" (O_DIRECT reads from
+    the disk), "cold" (buffered reads after the file's pages were dropped from the page cache) or
+    "warm" (buffered reads of a file the page cache holds: the pipeline without the disk)."""
+    import shutil
+    import time as _t
+
+    import numpy as np
+
+    from stblarge_amd import gguf
+    from stblarge_amd.moe import ExpertCache
+
+    dim, inter = 5120, 2304
+    d = os.path.join(ROOT, "_direct_io_tmp")
+    os.makedirs(d, exist_ok=True)
+    path = os.path.join(d, "bench_experts.gguf")
+    part = dim * inter // 32 * 17
+    rng = np.random.default_rng(5)
+    tensors = [(gguf.expert_tensor(0, p), gguf.QT_MXFP4, [dim, inter, n_experts] if p != "down" else [inter, dim, n_experts],
+                lambda: (np.frombuffer(rng.bytes(part), np.uint8) for _ in range(n_experts))) for p in ("gate", "up", "down")]
+    gguf.write(path, tensors, alignment=16384)
+    if mode == "cold":
+        fd = os.open(path, os.O_RDONLY)
+        os.fsync(fd)
+        os.posix_fadvise(fd, 0, 0, os.POSIX_FADV_DONTNEED)
+        os.close(fd)
+    try:
+        cache = ExpertCache.from_gguf(2 * per_lookup, path, readers=readers, direct=mode == "direct")
+        info0 = cache.file_info()
+        order = list(np.random.default_rng(6).permutation(n_experts))
+        lat = []
+        for i in range(lookups):
+            ids = [int(order[(i * per_lookup + j) % n_experts]) for j in range(per_lookup)]
+            t0 = _t.perf_counter()
+            cache.lookup(ids)
+            torch.cuda.synchronize()
+            lat.append(_t.perf_counter() - t0)
+            cache.mark_used()
+        info = cache.file_info()
+        cache.close()
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    lat.sort()
+    med = lat[len(lat) // 2]
+    return {"workload": f"expert_file_{mode}_v41_{per_lookup}x_r{readers}",
+            "mode": mode, "direct": bool(info["direct"]), "readers": readers, "experts_per_lookup": per_lookup,
+            "expert_bytes": 3 * part, "lookups": lookups, "ms_per_lookup_median": med * 1e3,
+            "ms_per_lookup_p90": lat[int(0.9 * len(lat))] * 1e3, "ms_per_expert": med * 1e3 / per_lookup,
+            "GB_s": 3 * part * per_lookup / med / 1e9,
+            "read_share": (info["read_ns"] - info0["read_ns"]) / 1e9 / sum(lat)}
+
+
 def measured_traffic():
     """HBM bytes per launch of the headline kernel from the committed rocprofv3 counter summary
     (profiles/gemv_fp4_2048x7168_traffic.md, line `traffic_bytes_per_launch: N`), or None."""
@@ -473,6 +529,14 @@ def main():
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step']:.3f} ms/step, {r['tokens_per_s']:.0f} tok/s, hit rate "
                   f"{r['hit_rate']:.3f}, {r['misses_per_token']:.2f} misses/token, refill {r['refill_GB_s']:.1f} GB/s",
+                  file=sys.stderr, flush=True)
+    if args.only in ("all", "file"):
+        for mode, per, readers in (("direct", 1, 8), ("direct", 6, 8), ("direct", 1, 4), ("direct", 1, 16),
+                                   ("cold", 1, 8), ("cold", 6, 8), ("warm", 1, 8), ("warm", 6, 8)):
+            r = file_tier_workload(torch, mode, readers, per_lookup=per)
+            extra[r["workload"]] = r
+            print(f"# {r['workload']}: {r['ms_per_lookup_median']:.2f} ms/lookup (p90 {r['ms_per_lookup_p90']:.2f}), "
+                  f"{r['ms_per_expert']:.2f} ms/expert, {r['GB_s']:.2f} GB/s, reading {100 * r['read_share']:.0f}%",
                   file=sys.stderr, flush=True)
     if args.eager:
         r = gemv_workload(torch, "fp4", 2048, 7168, 1, args.steps, args.warmup, use_graph=False)

@@ -211,11 +211,26 @@ int stbl_amd_act_quant_e4m3(const void *x, int rows, int k, int block, void *cod
 /* ---- v2: HBM expert cache (stbl/model.cu:99-106, 347-422 ExpertCache / expert() / take_slot) -------- */
 
 /* Creates an LRU cache of `slots` expert slots of slot_bytes on the current device (allocates the
- * slots, a copy stream and events: the only allocating calls of this library). host_pool: pinned
+ * slots, a copy stream and events; with stbl_amd_cache_create_gguf and stbl_amd_gguf_open the only
+ * allocating calls of this library). host_pool: pinned
  * host memory holding n_layers * n_experts experts host_stride bytes apart, alive as long as the
  * cache. Returns NULL on failure. */
 void *stbl_amd_cache_create(int slots, uint64_t slot_bytes, const void *host_pool, uint64_t host_stride, int n_experts,
                             int n_layers);
+
+/* File-backed cache over a GGUF file (stbl/model.cu:283-308 read_range / read_pieces, :383-422 the
+ * demand read of an expert): the routed experts of GGUF blocks first_layer .. first_layer+n_layers-1
+ * (blk.N.ffn_{gate,up,down}_exps.weight, MXFP4 [dim, inter, experts] / [inter, dim, experts], the
+ * reference converter's tensors) are read on misses in 2 MiB pieces by `readers` threads (1..16),
+ * with O_DIRECT when direct = 1 and the file system allows it, and repacked on the device into FP4
+ * (OCP) slots of stbl_amd_expert_layout(STBL_AMD_FP4, dim, inter) bytes; lookup then blocks the
+ * host until its misses are read. Cache layer l is GGUF block first_layer + l. NULL on failure. */
+void *stbl_amd_cache_create_gguf(int slots, const char *path, int first_layer, int n_layers, int readers, int direct);
+
+/* File-backed caches only: out[0..7] = dim, inter, experts, slot bytes, 1 if O_DIRECT, bytes read
+ * from the file, nanoseconds spent reading, experts read. No reference counterpart (the reference
+ * prints its read time per token, stbl/model.cu:250-258). */
+int stbl_amd_cache_file_info(void *cache, uint64_t *out);
 
 /* Frees the cache after its copies finished. */
 void stbl_amd_cache_destroy(void *cache);
@@ -240,6 +255,29 @@ void *stbl_amd_cache_peek(void *cache, int layer, int expert);
 
 /* Test hook: the refill after n more refills fails on the host without copying (n = -1 disables). */
 int stbl_amd_cache_fail_refill_after(void *cache, int n);
+
+/* ---- v2: GGUF reader (stbl/gguf.h:9-31, stbl/gguf.cpp) ------------------------------------------------- */
+
+/* Parses a GGUF (version >= 2) file's header with pread: metadata and the tensor table; tensor
+ * offsets become absolute file offsets (data start aligned to general.alignment, 32 if absent).
+ * Returns a handle or NULL (the reason in stbl_amd_last_error). */
+void *stbl_amd_gguf_open(const char *path);
+void stbl_amd_gguf_close(void *g);
+
+/* A tensor's type (GGUF type id: 0 F32, 1 F16, 24 I8, 30 BF16, 39 MXFP4, 200 E4M3, 201 E8M0), dims
+ * (innermost first, up to 4 written), absolute file offset and byte size (0 for other types).
+ * 0, or -hipErrorNotFound without recording an error when the tensor is absent. */
+int stbl_amd_gguf_tensor(void *g, const char *name, uint32_t *type, uint64_t *dims, int *ndims, uint64_t *offset,
+                         uint64_t *nbytes);
+
+/* Scalar metadata (stbl/gguf.h:28-29 u32 / f32): 0, or -hipErrorNotFound when the key is absent or
+ * of another type. */
+int stbl_amd_gguf_u32(void *g, const char *key, uint32_t *v);
+int stbl_amd_gguf_f32(void *g, const char *key, float *v);
+
+/* A u32 or u64 array (stbl/gguf.h:31 uints): up to cap values into out (may be NULL); returns the
+ * array's length, or -hipErrorNotFound when the key is absent or holds another type. */
+int64_t stbl_amd_gguf_uints(void *g, const char *key, uint64_t *out, int64_t cap);
 
 /* ---- library ------------------------------------------------------------------------------------------ */
 

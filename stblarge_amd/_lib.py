@@ -54,7 +54,15 @@ SIGNATURES = {
     "stbl_amd_gemm_work_bytes": (U64, [I, I, I]),
     "stbl_amd_act_quant_e4m3": (I, [P, I, I, I, P, P, P]),
     "stbl_amd_cache_create": (P, [I, U64, P, U64, I, I]),
+    "stbl_amd_cache_create_gguf": (P, [I, ctypes.c_char_p, I, I, I, I]),
+    "stbl_amd_cache_file_info": (I, [P, PU64]),
     "stbl_amd_cache_destroy": (None, [P]),
+    "stbl_amd_gguf_open": (P, [ctypes.c_char_p]),
+    "stbl_amd_gguf_close": (None, [P]),
+    "stbl_amd_gguf_tensor": (I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32), PU64, PI, PU64, PU64]),
+    "stbl_amd_gguf_u32": (I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32)]),
+    "stbl_amd_gguf_f32": (I, [P, ctypes.c_char_p, PF]),
+    "stbl_amd_gguf_uints": (ctypes.c_int64, [P, ctypes.c_char_p, PU64, ctypes.c_int64]),
     "stbl_amd_cache_lookup": (I, [P, PI, I, I, PP, PI, P]),
     "stbl_amd_cache_mark_used": (I, [P, P]),
     "stbl_amd_cache_stats": (I, [P, PU64]),

@@ -15,13 +15,62 @@
 // an event on the compute stream after those kernels; a later refill of the slot waits for it on the
 // copy stream. Events come from a ring, so a recycled event only makes a refill wait longer.
 // One host thread drives a cache; lookups of different caches may run on different threads.
+//
+// File tier (stbl_amd_cache_create_gguf): the experts come from a GGUF file instead of a host pool,
+// as in the reference engine (stbl/model.cu:283-308, :383-422): each expert's gate, up and down MXFP4
+// blocks are read in 2 MiB pieces by reader threads (O_DIRECT where the file system allows it, at
+// 4 KiB-aligned offsets) into per-reader pinned stages and copied on per-reader streams into a device
+// staging area; a repack kernel on the copy stream then turns the 17-byte GGUF blocks into the slot's
+// OCP layout (codes, then scales), so the routed-expert kernels read file-refilled and pool-refilled
+// slots alike. The misses of one lookup are read together, up to kStageExperts at a time; the host
+// thread returns once the reads have landed in pinned memory and every copy and repack is queued.
+#include <errno.h>
+#include <fcntl.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+#include <atomic>
+#include <chrono>
 #include <list>
+#include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
 #include "abi_util.hpp"
+#include "expert_layout.hpp"
+#include "gemv_core.hpp"
+
+extern "C" {
+void *stbl_amd_gguf_open(const char *path);
+void stbl_amd_gguf_close(void *g);
+int stbl_amd_gguf_tensor(void *g, const char *name, uint32_t *type, uint64_t *dims, int *ndims, uint64_t *offset,
+                         uint64_t *nbytes);
+}
 
 namespace stbl {
+
+constexpr uint64_t kPiece = 2u << 20, kAlign = 4096;
+constexpr int kStageExperts = 8, kMaxReaders = 16;
+
+// The file tier's state: the expert tensors of each layer and the read path.
+struct FileTier {
+    int fd = -1, dfd = -1;      // buffered and O_DIRECT descriptors (dfd -1: buffered reads only)
+    std::vector<uint64_t> part_off;  // [layer][gate, up, down]: file offset of the layer's expert tensor
+    uint64_t part_bytes = 0;     // bytes of one expert's part (the three are equal: inter * dim / 32 * 17)
+    int dim = 0, inter = 0;
+    uint8_t *dstage = nullptr;   // device: kStageExperts experts of 3 parts
+    std::vector<uint8_t *> pinned;       // per reader: two halves of kPiece bytes
+    std::vector<uint8_t *> bounce;       // per reader, O_DIRECT only: kPiece + 2 kAlign page-aligned bytes
+    std::vector<hipStream_t> rstream;    // per reader
+    std::vector<hipEvent_t> half_done;   // per reader and half: the copy out of it
+    std::vector<int> half_used;          // whether half_done was recorded
+    std::vector<hipEvent_t> rdone;       // per reader: its copies of a batch
+    hipEvent_t repacked = nullptr;       // the repacks of the last batch (dstage free again)
+    bool repack_pending = false;
+    uint64_t bytes_read = 0, read_ns = 0, experts_read = 0;
+};
 
 struct ExpertCache {
     int device = 0;
@@ -44,7 +93,34 @@ struct ExpertCache {
     std::vector<int> touched;  // slots of the last lookup
     uint64_t hits = 0, misses = 0, refill_bytes = 0, lookups = 0;
     int fail_in = -1;  // test hook: the refill after this many more fails (host side, nothing copied)
+    FileTier *file = nullptr;
 };
+
+// GGUF MXFP4 blocks (byte 0: E8M0 scale; byte 1+i: element i in the low nibble, element 16+i in the
+// high one) to the OCP slot layout (codes: element 2j in the low nibble of byte j, 2j+1 in the high
+// one; scales: one byte per 32). Block g of a part is row g / (k/32), column g % (k/32), so its codes
+// go to byte 16 g of the part's codes and its scale to byte g of its scales, whatever the shape.
+// One thread per block; the three parts are numbered gate, up, down, n_blocks each.
+__global__ void k_gguf17_to_ocp(const uint8_t *src, uint8_t *slot, uint64_t n_blocks, uint64_t c0, uint64_t s0,
+                                uint64_t c1, uint64_t s1, uint64_t c2, uint64_t s2) {
+    const uint64_t g = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= 3 * n_blocks) return;
+    const int p = (int)(g / n_blocks);
+    const uint64_t b = g - (uint64_t)p * n_blocks;
+    uint32_t sc;
+    u32x4 c;
+    load_gguf_block(src + g * 17, sc, c);
+    // 4 bytes holding one nibble each -> 2 bytes of nibble pairs
+    auto pk = [](uint32_t w) { return (w & 0xfu) | ((w >> 4) & 0xf0u) | ((w >> 8) & 0xf00u) | ((w >> 12) & 0xf000u); };
+    u32x4 o;
+    o[0] = pk(c[0] & 0x0f0f0f0fu) | pk(c[1] & 0x0f0f0f0fu) << 16;
+    o[1] = pk(c[2] & 0x0f0f0f0fu) | pk(c[3] & 0x0f0f0f0fu) << 16;
+    o[2] = pk((c[0] >> 4) & 0x0f0f0f0fu) | pk((c[1] >> 4) & 0x0f0f0f0fu) << 16;
+    o[3] = pk((c[2] >> 4) & 0x0f0f0f0fu) | pk((c[3] >> 4) & 0x0f0f0f0fu) << 16;
+    const uint64_t co = p == 0 ? c0 : p == 1 ? c1 : c2, so = p == 0 ? s0 : p == 1 ? s1 : s2;
+    *(u32x4 *)(slot + co + 16 * b) = o;
+    slot[so + b] = (uint8_t)sc;
+}
 
 static int take_slot(ExpertCache &c) {
     if (!c.free_slots.empty()) {
@@ -56,6 +132,26 @@ static int take_slot(ExpertCache &c) {
     return -1;  // caller evicts
 }
 
+static void destroy_file(FileTier *f) {
+    if (!f) return;
+    for (auto s : f->rstream)
+        if (s) (void)hipStreamSynchronize(s);
+    for (auto s : f->rstream)
+        if (s) (void)hipStreamDestroy(s);
+    for (auto e : f->half_done)
+        if (e) (void)hipEventDestroy(e);
+    for (auto e : f->rdone)
+        if (e) (void)hipEventDestroy(e);
+    if (f->repacked) (void)hipEventDestroy(f->repacked);
+    for (auto p : f->pinned)
+        if (p) (void)hipHostFree(p);
+    for (auto p : f->bounce) free(p);
+    if (f->dstage) (void)hipFree(f->dstage);
+    if (f->fd >= 0) close(f->fd);
+    if (f->dfd >= 0) close(f->dfd);
+    delete f;
+}
+
 // Teardown is best effort: a failure here cannot be reported to anyone who could act on it.
 static void destroy(ExpertCache *c) {
     if (!c) return;
@@ -63,6 +159,7 @@ static void destroy(ExpertCache *c) {
     (void)hipGetDevice(&prev);
     (void)hipSetDevice(c->device);
     if (c->copy) (void)hipStreamSynchronize(c->copy);
+    destroy_file(c->file);
     for (auto &e : c->ring)
         if (e) (void)hipEventDestroy(e);
     if (c->ready) (void)hipEventDestroy(c->ready);
@@ -70,6 +167,159 @@ static void destroy(ExpertCache *c) {
     if (c->mem) (void)hipFree(c->mem);
     (void)hipSetDevice(prev);
     delete c;
+}
+
+struct Piece {
+    uint8_t *dst;  // device
+    uint64_t off, bytes;
+};
+
+// Reads `bytes` at file offset `off` into `dst` (a pinned half). Buffered reads go straight into it.
+// An O_DIRECT read covers the enclosing 4 KiB-aligned range (it may run past the end of the file,
+// which ends it short) and must land in pageable memory: the kernel refuses to pin pages of
+// hipHostMalloc memory for direct I/O (EFAULT), so it lands in the reader's page-aligned bounce
+// buffer and the payload is copied into dst. Returns 0 or an errno value (-1: end of file).
+static int read_range(const FileTier &f, uint8_t *bounce, uint8_t *dst, uint64_t off, uint64_t bytes) {
+    const bool direct = f.dfd >= 0;
+    const uint64_t start = direct ? off & ~(kAlign - 1) : off;
+    const uint64_t need = off - start + bytes, len = direct ? (need + kAlign - 1) & ~(kAlign - 1) : need;
+    uint8_t *buf = direct ? bounce : dst;
+    for (uint64_t got = 0; got < need;) {
+        const ssize_t r = pread(direct ? f.dfd : f.fd, buf + got, len - got, (off_t)(start + got));
+        if (r < 0 && errno == EINTR) continue;
+        if (r <= 0) return r == 0 ? -1 : errno;
+        got += (uint64_t)r;
+    }
+    if (direct) memcpy(dst, bounce + (off - start), bytes);
+    return 0;
+}
+
+// Reads the pieces with every reader thread and queues their copies into device staging; `copy`
+// is then made to wait for the copies. Each reader alternates between the two halves of its pinned
+// stage and waits for the copy out of a half before reading into it again.
+static hipError_t read_pieces(ExpertCache &c, const std::vector<Piece> &ps, std::string &err) {
+    FileTier &f = *c.file;
+    const int nr = (int)std::min<size_t>(f.pinned.size(), ps.size());
+    for (int w = 0; w < nr && f.repack_pending; w++) {
+        const hipError_t e = hipStreamWaitEvent(f.rstream[w], f.repacked, 0);  // staging still read by repacks
+        if (e != hipSuccess) return err = "ordering reads after repacks", e;
+    }
+    std::atomic<size_t> next{0};
+    std::atomic<int> failed{0};  // 0, or 1 + the failing piece's index
+    std::atomic<int> status{(int)hipSuccess}, read_errno{0};
+    auto work = [&](int w) {
+        hipError_t e = w > 0 ? hipSetDevice(c.device) : hipSuccess;  // new threads start on device 0
+        int half = 0;
+        for (size_t j; e == hipSuccess && !failed && (j = next++) < ps.size(); half ^= 1) {
+            const int h = 2 * w + half;
+            uint8_t *stage = f.pinned[w] + (uint64_t)half * kPiece;
+            if (f.half_used[h]) e = hipEventSynchronize(f.half_done[h]);
+            if (e != hipSuccess) break;
+            const int rc = read_range(f, f.bounce.empty() ? nullptr : f.bounce[w], stage, ps[j].off, ps[j].bytes);
+            if (rc) {
+                read_errno = rc;
+                failed = 1 + (int)j;
+                break;
+            }
+            e = hipMemcpyAsync(ps[j].dst, stage, ps[j].bytes, hipMemcpyHostToDevice, f.rstream[w]);
+            if (e == hipSuccess) e = hipEventRecord(f.half_done[h], f.rstream[w]);
+            if (e == hipSuccess) f.half_used[h] = 1;
+        }
+        if (e != hipSuccess) status = (int)e, failed = 1;
+    };
+    const auto t0 = std::chrono::steady_clock::now();
+    std::vector<std::thread> pool;
+    for (int w = 1; w < nr; w++) pool.emplace_back(work, w);
+    work(0);
+    for (auto &t : pool) t.join();
+    f.read_ns += (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t0).count();
+    if (failed) {
+        if (status != (int)hipSuccess) return err = "copying a piece", (hipError_t)status.load();
+        const Piece &p = ps[failed - 1];
+        err = "reading " + std::to_string(p.bytes) + " bytes at file offset " + std::to_string(p.off) + ": " +
+              (read_errno == -1 ? std::string("end of file") : std::string(strerror(read_errno)));
+        return hipErrorFileNotFound;
+    }
+    for (int w = 0; w < nr; w++) {
+        hipError_t e = hipEventRecord(f.rdone[w], f.rstream[w]);
+        if (e == hipSuccess) e = hipStreamWaitEvent(c.copy, f.rdone[w], 0);
+        if (e != hipSuccess) return err = "ordering the repacks after the copies", e;
+    }
+    for (const Piece &p : ps) f.bytes_read += p.bytes;
+    return hipSuccess;
+}
+
+struct PendingRead {
+    int expert, slot;
+};
+
+// Serves the file misses of one lookup: reads them in batches of kStageExperts, then repacks each
+// into its slot on the copy stream after the slot's last use. Returns how many were served (a prefix
+// of `pend`); on failure `err` says why.
+static size_t serve_file_misses(ExpertCache &c, int layer, const std::vector<PendingRead> &pend, hipError_t &status,
+                                std::string &err) {
+    FileTier &f = *c.file;
+    const ExpertLayout L = expert_layout(EXPERT_FP4, f.dim, f.inter);
+    const uint64_t n_blocks = f.part_bytes / 17;
+    size_t done = 0;
+    status = hipSuccess;
+    while (done < pend.size()) {
+        const size_t n = std::min<size_t>(kStageExperts, pend.size() - done);
+        std::vector<Piece> ps;
+        for (size_t i = 0; i < n; i++) {
+            if (c.fail_in >= 0 && c.fail_in-- == 0) {
+                status = hipErrorUnknown;
+                err = "injected refill failure";
+                return done;
+            }
+            for (int p = 0; p < 3; p++) {
+                const uint64_t off = f.part_off[3 * layer + p] + (uint64_t)pend[done + i].expert * f.part_bytes;
+                uint8_t *dst = f.dstage + (3 * i + p) * f.part_bytes;
+                for (uint64_t at = 0; at < f.part_bytes; at += kPiece)
+                    ps.push_back({dst + at, off + at, std::min<uint64_t>(kPiece, f.part_bytes - at)});
+            }
+        }
+        status = read_pieces(c, ps, err);
+        if (status != hipSuccess) return done;
+        for (size_t i = 0; i < n && status == hipSuccess; i++) {
+            const int s = pend[done + i].slot;
+            if (c.slot_use[s] >= 0) status = hipStreamWaitEvent(c.copy, c.ring[c.slot_use[s]], 0);
+            if (status != hipSuccess) break;
+            hipLaunchKernelGGL(k_gguf17_to_ocp, dim3((unsigned)((3 * n_blocks + 255) / 256)), dim3(256), 0, c.copy,
+                               f.dstage + 3 * i * f.part_bytes, c.mem + (uint64_t)s * c.slot_bytes, n_blocks, L.off[0],
+                               L.off[1], L.off[2], L.off[3], L.off[4], L.off[5]);
+            status = hipGetLastError();
+        }
+        if (status == hipSuccess) status = hipEventRecord(f.repacked, c.copy);
+        if (status != hipSuccess) {
+            err = "queueing the repacks";
+            return done;
+        }
+        f.repack_pending = true;
+        f.experts_read += n;
+        done += n;
+    }
+    return done;
+}
+
+static ExpertCache *new_cache(int slots, uint64_t slot_bytes, int n_experts, int n_layers) {
+    ExpertCache *c = new ExpertCache();
+    c->slots = slots;
+    c->slot_bytes = slot_bytes;
+    c->n_experts = n_experts;
+    c->n_layers = n_layers;
+    c->slot_use.assign(slots, -1);
+    hipError_t e = hipGetDevice(&c->device);
+    if (e == hipSuccess) e = hipMalloc(&c->mem, (size_t)slots * slot_bytes);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ready, hipEventDisableTiming);
+    for (int i = 0; i < ExpertCache::kRing && e == hipSuccess; i++) e = hipEventCreateWithFlags(&c->ring[i], hipEventDisableTiming);
+    if (e != hipSuccess) {
+        abi_status(e, "cache_create");
+        destroy(c);
+        return nullptr;
+    }
+    return c;
 }
 
 }  // namespace stbl
@@ -87,25 +337,108 @@ void *stbl_amd_cache_create(int slots, uint64_t slot_bytes, const void *host_poo
         abi_fail(hipErrorInvalidValue, "cache_create: bad arguments");
         return nullptr;
     }
-    ExpertCache *c = new ExpertCache();
-    c->slots = slots;
-    c->slot_bytes = slot_bytes;
-    c->host = (const uint8_t *)host_pool;
-    c->host_stride = host_stride;
-    c->n_experts = n_experts;
-    c->n_layers = n_layers;
-    c->slot_use.assign(slots, -1);
-    hipError_t e = hipGetDevice(&c->device);
-    if (e == hipSuccess) e = hipMalloc(&c->mem, (size_t)slots * slot_bytes);
-    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ready, hipEventDisableTiming);
-    for (int i = 0; i < ExpertCache::kRing && e == hipSuccess; i++) e = hipEventCreateWithFlags(&c->ring[i], hipEventDisableTiming);
+    ExpertCache *c = new_cache(slots, slot_bytes, n_experts, n_layers);
+    if (c) {
+        c->host = (const uint8_t *)host_pool;
+        c->host_stride = host_stride;
+    }
+    return c;
+}
+
+// File-backed cache: the routed experts of GGUF blocks first_layer .. first_layer + n_layers - 1
+// (tensors blk.N.ffn_{gate,up,down}_exps.weight, MXFP4, dims [dim, inter, experts] for gate and up and
+// [inter, dim, experts] for down, as the reference's converter writes them) are read from `path` on
+// misses by `readers` threads (1..16) into FP4 (OCP) slots. direct = 1 reads with O_DIRECT where the
+// file system supports it (falling back to buffered reads where it does not), 0 always buffered.
+// Cache layer l is GGUF block first_layer + l. NULL on failure.
+void *stbl_amd_cache_create_gguf(int slots, const char *path, int first_layer, int n_layers, int readers, int direct) {
+    if (slots < 1 || !path || first_layer < 0 || n_layers < 1 || readers < 1 || readers > kMaxReaders) {
+        abi_fail(hipErrorInvalidValue, "cache_create_gguf: bad arguments");
+        return nullptr;
+    }
+    void *g = stbl_amd_gguf_open(path);
+    if (!g) return nullptr;  // the reader recorded why
+    FileTier *f = new FileTier();
+    int n_experts = 0;
+    std::string err;
+    static const char *kParts[3] = {"gate", "up", "down"};
+    for (int l = 0; l < n_layers && err.empty(); l++)
+        for (int p = 0; p < 3 && err.empty(); p++) {
+            const std::string name = "blk." + std::to_string(first_layer + l) + ".ffn_" + kParts[p] + "_exps.weight";
+            uint32_t type = 0;
+            uint64_t dims[4] = {}, off = 0, nbytes = 0;
+            int nd = 0;
+            if (stbl_amd_gguf_tensor(g, name.c_str(), &type, dims, &nd, &off, &nbytes) != 0) {
+                err = "no tensor " + name;
+                break;
+            }
+            const uint64_t k = dims[0], rows = dims[1], e = dims[2];
+            if (type != 39 || nd != 3 || k % 32 || !rows || !e || k > (1u << 20) || rows > (1u << 20) || e > (1u << 16)) {
+                err = name + ": want MXFP4 [k, rows, experts] with k % 32 == 0";
+                break;
+            }
+            if (l == 0 && p == 0) f->dim = (int)k, f->inter = (int)rows, n_experts = (int)e;
+            const bool down = p == 2;
+            if (f->dim % 32 || f->inter % 32) {
+                err = name + ": dim and inter must be multiples of 32";
+                break;
+            }
+            if ((int)k != (down ? f->inter : f->dim) || (int)rows != (down ? f->dim : f->inter) || (int)e != n_experts) {
+                err = name + ": shape differs from the first layer's gate";
+                break;
+            }
+            f->part_bytes = rows * k / 32 * 17;
+            f->part_off.push_back(off);
+        }
+    stbl_amd_gguf_close(g);
+    ExpertCache *c = nullptr;
+    if (err.empty()) c = new_cache(slots, expert_layout(EXPERT_FP4, f->dim, f->inter).bytes, n_experts, n_layers);
+    if (!c) {
+        if (!err.empty()) abi_fail(hipErrorInvalidValue, "cache_create_gguf: %s: %s", path, err.c_str());
+        destroy_file(f);
+        return nullptr;
+    }
+    c->file = f;
+    f->fd = open(path, O_RDONLY);
+    if (direct) f->dfd = open(path, O_RDONLY | O_DIRECT);  // -1 where the file system refuses it
+    hipError_t e = f->fd >= 0 ? hipSuccess : hipErrorFileNotFound;
+    if (e == hipSuccess) e = hipMalloc(&f->dstage, (size_t)kStageExperts * 3 * f->part_bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(c->mem, 0, (size_t)c->slots * c->slot_bytes, c->copy);  // padding reads as 0
+    f->pinned.assign(readers, nullptr);
+    f->rstream.assign(readers, nullptr);
+    f->rdone.assign(readers, nullptr);
+    f->half_done.assign(2 * readers, nullptr);
+    f->half_used.assign(2 * readers, 0);
+    for (int w = 0; w < readers && e == hipSuccess; w++) {
+        e = hipHostMalloc((void **)&f->pinned[w], 2 * kPiece, hipHostMallocDefault);
+        if (e == hipSuccess && f->dfd >= 0) {
+            void *b = nullptr;
+            if (posix_memalign(&b, kAlign, kPiece + 2 * kAlign)) e = hipErrorOutOfMemory;
+            f->bounce.push_back((uint8_t *)b);
+        }
+        if (e == hipSuccess) e = hipStreamCreateWithFlags(&f->rstream[w], hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&f->rdone[w], hipEventDisableTiming);
+        for (int h = 0; h < 2 && e == hipSuccess; h++) e = hipEventCreateWithFlags(&f->half_done[2 * w + h], hipEventDisableTiming);
+    }
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&f->repacked, hipEventDisableTiming);
     if (e != hipSuccess) {
-        abi_status(e, "cache_create");
+        abi_status(e, "cache_create_gguf");
         destroy(c);
         return nullptr;
     }
     return c;
+}
+
+// File tier facts: out[0..7] = dim, inter, experts, slot bytes, 1 if reads use O_DIRECT, bytes read
+// from the file, nanoseconds spent reading (wall time of the reader threads), experts read.
+int stbl_amd_cache_file_info(void *cache, uint64_t *out) {
+    ExpertCache *c = (ExpertCache *)cache;
+    if (!c || !out || !c->file) return abi_fail(hipErrorInvalidValue, "cache_file_info: not a file-backed cache");
+    const FileTier &f = *c->file;
+    const uint64_t v[8] = {(uint64_t)f.dim, (uint64_t)f.inter, (uint64_t)c->n_experts, c->slot_bytes, f.dfd >= 0 ? 1u : 0u,
+                           f.bytes_read, f.read_ns, f.experts_read};
+    for (int i = 0; i < 8; i++) out[i] = v[i];
+    return 0;
 }
 
 void stbl_amd_cache_destroy(void *cache) { destroy((ExpertCache *)cache); }
@@ -131,6 +464,27 @@ int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **
     }
     c->touched.clear();
     int nmiss = 0;
+    std::vector<PendingRead> pend;  // file tier: misses mapped, not yet read
+    auto key_of = [&](const PendingRead &p) { return key(p.expert); };
+    auto unmap = [&](size_t from) {  // pending misses from `from` on stay unmapped
+        for (size_t j = from; j < pend.size(); j++) {
+            auto it = c->where.find(key_of(pend[j]));
+            c->lru.erase(it->second.second);
+            c->where.erase(it);
+            c->free_slots.push_back(pend[j].slot);
+            c->misses--;
+            c->refill_bytes -= c->slot_bytes;
+        }
+        pend.resize(from);
+    };
+    // A lookup that fails after queueing refills still orders `compute` after them: the refilled
+    // experts stay mapped, and a later lookup that hits them queues no wait of its own.
+    int queued = 0;
+    auto order_compute = [&]() {
+        hipError_t e = hipEventRecord(c->ready, c->copy);
+        if (e == hipSuccess) e = hipStreamWaitEvent(compute, c->ready, 0);
+        return e;
+    };
     for (int i = 0; i < n; i++) {
         const uint64_t k = key(ids[i]);
         auto it = c->where.find(k);
@@ -148,23 +502,33 @@ int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **
             const uint64_t victim = c->lru.back();
             bool needed = false;
             for (int j = 0; j < n; j++) needed |= key(ids[j]) == victim;
-            if (needed) return abi_fail(hipErrorOutOfMemory, "cache_lookup: every slot is held by this lookup (%d slots)", c->slots);
+            if (needed) {
+                unmap(0);
+                if (queued) (void)order_compute();
+                return abi_fail(hipErrorOutOfMemory, "cache_lookup: every slot is held by this lookup (%d slots)", c->slots);
+            }
             s = c->where[victim].first;
             c->where.erase(victim);
             c->lru.pop_back();
         }
         uint8_t *dst = c->mem + (uint64_t)s * c->slot_bytes;
-        const uint8_t *src = c->host + ((uint64_t)layer * c->n_experts + ids[i]) * c->host_stride;
-        hipError_t e = hipSuccess;
-        if (c->slot_use[s] >= 0) e = hipStreamWaitEvent(c->copy, c->ring[c->slot_use[s]], 0);
-        if (e == hipSuccess) {
-            if (c->fail_in == 0) e = hipErrorUnknown;
-            else e = hipMemcpyAsync(dst, src, c->slot_bytes, hipMemcpyHostToDevice, c->copy);
-            if (c->fail_in >= 0) c->fail_in--;
-        }
-        if (e != hipSuccess) {
-            c->free_slots.push_back(s);  // slot stays unmapped: the next lookup misses again
-            return abi_fail(e, "cache_lookup: refill of expert %d failed: %s", ids[i], hipGetErrorString(e));
+        if (!c->file) {
+            const uint8_t *src = c->host + ((uint64_t)layer * c->n_experts + ids[i]) * c->host_stride;
+            hipError_t e = hipSuccess;
+            if (c->slot_use[s] >= 0) e = hipStreamWaitEvent(c->copy, c->ring[c->slot_use[s]], 0);
+            if (e == hipSuccess) {
+                if (c->fail_in == 0) e = hipErrorUnknown;
+                else e = hipMemcpyAsync(dst, src, c->slot_bytes, hipMemcpyHostToDevice, c->copy);
+                if (c->fail_in >= 0) c->fail_in--;
+            }
+            if (e != hipSuccess) {
+                c->free_slots.push_back(s);  // slot stays unmapped: the next lookup misses again
+                if (queued) (void)order_compute();
+                return abi_fail(e, "cache_lookup: refill of expert %d failed: %s", ids[i], hipGetErrorString(e));
+            }
+            queued++;
+        } else {
+            pend.push_back({ids[i], s});
         }
         c->lru.push_front(k);
         c->where[k] = {s, c->lru.begin()};
@@ -175,9 +539,20 @@ int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **
         c->touched.push_back(s);
         nmiss++;
     }
+    if (!pend.empty()) {
+        hipError_t e;
+        std::string err;
+        const size_t served = serve_file_misses(*c, layer, pend, e, err);
+        if (served < pend.size()) {
+            const int first = pend[served].expert;
+            unmap(served);
+            if (queued + served) (void)order_compute();
+            return abi_fail(e == hipSuccess ? hipErrorUnknown : e, "cache_lookup: reading expert %d of layer %d failed: %s",
+                            first, layer, err.c_str());
+        }
+    }
     if (nmiss > 0) {
-        hipError_t e = hipEventRecord(c->ready, c->copy);
-        if (e == hipSuccess) e = hipStreamWaitEvent(compute, c->ready, 0);
+        const hipError_t e = order_compute();
         if (e != hipSuccess) return abi_status(e, "cache_lookup: ordering the compute stream after the refills");
     }
     return nmiss;

@@ -15,7 +15,8 @@ from . import _lib, ops
 
 
 class ExpertCache:
-    """HBM LRU cache of expert slots over a pinned host pool (stbl_amd_cache_*)."""
+    """HBM LRU cache of expert slots over a pinned host pool (stbl_amd_cache_*), or over a GGUF file
+    (from_gguf)."""
 
     def __init__(self, slots, slot_bytes, host_pool, n_experts, n_layers=1, host_stride=None):
         if not isinstance(host_pool, torch.Tensor) or host_pool.is_cuda or not host_pool.is_pinned():
@@ -29,6 +30,27 @@ class ExpertCache:
                                                         stride, n_experts, n_layers)
         if not self.handle:
             _lib.check(-1, "cache_create")
+
+    @classmethod
+    def from_gguf(cls, slots, path, first_layer=0, n_layers=1, readers=8, direct=True):
+        """A cache whose misses are read from the routed-expert tensors of a GGUF file (layers
+        first_layer .. first_layer + n_layers - 1) into FP4 (OCP) slots."""
+        self = cls.__new__(cls)
+        self.pool = None
+        self.handle = _lib.load().stbl_amd_cache_create_gguf(slots, str(path).encode(), first_layer, n_layers, readers,
+                                                             1 if direct else 0)
+        if not self.handle:
+            _lib.check(-1, "cache_create_gguf")
+        info = self.file_info()
+        self.slots, self.slot_bytes, self.n_experts, self.n_layers = slots, info["slot_bytes"], info["experts"], n_layers
+        self.dim, self.inter = info["dim"], info["inter"]
+        return self
+
+    def file_info(self):
+        out = (ctypes.c_uint64 * 8)()
+        _lib.check(_lib.load().stbl_amd_cache_file_info(self.handle, out), "cache_file_info")
+        keys = ("dim", "inter", "experts", "slot_bytes", "direct", "bytes_read", "read_ns", "experts_read")
+        return dict(zip(keys, [int(v) for v in out]))
 
     def lookup(self, ids, layer=0, stream=None):
         """Slots (device addresses) and hit flags of expert ids, in order; returns (ptrs, hits, misses)."""
@@ -71,8 +93,9 @@ class ExpertCache:
 
 
 class MoELayer:
-    """One routed MoE layer: n_experts routed experts in a pinned host pool behind an HBM LRU cache,
-    plus an always-on shared expert resident in HBM.
+    """One routed MoE layer: n_experts routed experts in a pinned host pool (or a GGUF file: pass
+    cache=ExpertCache.from_gguf(...) and the cache layer) behind an HBM LRU cache, plus an always-on
+    shared expert resident in HBM.
 
     forward(x, logits): x bf16 [t, dim] and router logits fp32 [t, n_experts] on the device; returns
     y bf16 [t, dim]. Routing follows the reference: top-k of score + bias, ties to the lower id,
@@ -82,12 +105,16 @@ class MoELayer:
 
     def __init__(self, fmt, dim, inter, host_pool, n_experts, topk, cache_slots, shared_slot=None, bias=None,
                  route_scale=1.0, limit=0.0, official=False, max_tokens=4, score_fn=ops.SCORE_SIGMOID,
-                 shared_fmt=None):
+                 shared_fmt=None, cache=None, layer=0):
         self.fmt, self.dim, self.inter, self.topk = fmt, dim, inter, topk
         self.score_fn = score_fn
         self.shared_fmt = fmt if shared_fmt is None else shared_fmt
         self.slot_bytes, _ = ops.expert_layout(fmt, dim, inter)
-        self.cache = ExpertCache(cache_slots, self.slot_bytes, host_pool, n_experts)
+        if cache is None:
+            cache = ExpertCache(cache_slots, self.slot_bytes, host_pool, n_experts)
+        elif cache.slot_bytes != self.slot_bytes:
+            raise ValueError("the cache's slots do not hold experts of this format and shape")
+        self.cache, self.layer = cache, layer
         self.shared = shared_slot
         self.bias, self.route_scale, self.limit, self.official = bias, route_scale, limit, official
         dev = torch.device("cuda", torch.cuda.current_device())
@@ -110,7 +137,7 @@ class MoELayer:
             for e in row:
                 if e not in uniq:
                     uniq.append(e)
-        ptrs, _, _ = self.cache.lookup(uniq, stream=stream)
+        ptrs, _, _ = self.cache.lookup(uniq, layer=self.layer, stream=stream)
         slot_of = {e: i for i, e in enumerate(uniq)}
         slots = list(ptrs)
         shared = -1

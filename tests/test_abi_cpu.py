@@ -18,7 +18,7 @@ def header_functions():
         if name.endswith(".h"):
             src += open(os.path.join(ROOT, "include", name)).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return set(re.findall(r"^\s*(?:void|int|void\s*\*|uint64_t|const\s+char\s*\*)\s*\**\s*(stbl_\w+)\s*\(", src, re.M))
+    return set(re.findall(r"^\s*(?:void|int|int64_t|void\s*\*|uint64_t|const\s+char\s*\*)\s*\**\s*(stbl_\w+)\s*\(", src, re.M))
 
 
 def test_library_exists():

@@ -16,7 +16,7 @@ import torch
 import oracle
 from stblarge_amd import data, ops
 from stblarge_amd.moe import ExpertCache, MoELayer
-from util import assert_gemv, bf16_ulps, np_
+from util import assert_gemv, bf16_ulps, np_, read_device
 
 pytestmark = pytest.mark.gpu
 
@@ -218,25 +218,11 @@ def test_cache_lru_matches_oracle(gpu):
         cache.mark_used()
         torch.cuda.synchronize()
         for e, p in zip(ids, ptrs):
-            head = torch.empty(8, dtype=torch.uint8, device=gpu)
-            torch.cuda.current_stream().synchronize()
-            _copy_from_addr(head, p)
-            assert head.cpu().tolist()[:4] == [e, 255 - e, 7, 9]
+            assert read_device(p, 8).tolist()[:4] == [e, 255 - e, 7, 9]
     st = cache.stats()
     assert st["hits"] + st["misses"] == 800 and st["in_use"] == slots
     assert st["refill_bytes"] == st["misses"] * sb
     cache.close()
-
-
-def _copy_from_addr(dst, addr):
-    """dst <- bytes at device address addr (a slot handed out by the cache), through the HIP runtime
-    torch already loaded (the same one libstbl_amd.so binds to)."""
-    import ctypes
-    import os
-
-    hip = ctypes.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
-    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
-    assert hip.hipMemcpy(ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(addr), dst.numel(), 3) == 0
 
 
 def test_cache_refill_failure_leaves_slot_unmapped(gpu):

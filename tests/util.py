@@ -49,3 +49,16 @@ def assert_gemv(got_f32, got_bf16, want, tol=1e-3):
         assert u.max() <= 1, f"bf16 output {u.max()} steps away"
         assert np.mean(u) < 0.05, f"{np.mean(u):.3f} of bf16 outputs flipped"
     return e
+
+
+def read_device(addr, n):
+    """n bytes at device address addr (a slot handed out by an expert cache) as a uint8 tensor,
+    through the HIP runtime torch already loaded (the one libstbl_amd.so binds to)."""
+    import ctypes
+    import os
+
+    hip = ctypes.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    dst = torch.empty(n, dtype=torch.uint8)
+    assert hip.hipMemcpy(ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(addr), n, 2) == 0  # device to host
+    return dst
