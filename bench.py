@@ -36,7 +36,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="all",
-                    help="fp4 (headline only) | gemv | batch | ffn | gemm | moe | moeallhit | refabi | file | all")
+                    help="fp4 (headline only) | gemv | batch | ffn | gemm | moe | moeallhit | refabi | file | "
+                         "filestack | all")
     ap.add_argument("--moe-steps", type=int, default=200)
     ap.add_argument("--moe-warmup", type=int, default=1000)
     ap.add_argument("--eager", action="store_true", help="also time launches issued one by one from Python")
@@ -420,6 +421,76 @@ def file_tier_workload(torch, mode, readers=8, n_experts=40, per_lookup=1, looku
             "read_share": (info["read_ns"] - info0["read_ns"]) / 1e9 / sum(lat)}
 
 
+def file_stack_workload(torch, guess_quality, n_layers=4, n_experts=24, topk=6, slots=16, tokens=6, readers=4,
+                        pf_readers=8, pf_m=8):
+    """Decode through n_layers routed MoE layers whose experts (V4.1 shape, 18.8 MB each) live in one
+    GGUF file behind a 16-slot file-backed cache, reading misses with O_DIRECT. guess_quality None:
+    no prefetch; q in [0, 1]: after each layer, pf_m guesses for the next layer are queued, each of
+    its true top-k experts included with probability q, the rest drawn at random (the reference's
+    stale-router prefetch, stbl/model.cu:555-586, with a controlled guess accuracy). Time per token
+    = all layers' lookups and kernels, host wall clock."""
+    import shutil
+    import time as _t
+
+    import numpy as np
+
+    from stblarge_amd import data, gguf, ops
+    from stblarge_amd.moe import ExpertCache, MoELayer
+
+    dim, inter = 5120, 2304
+    dev = torch.device("cuda:0")
+    d = os.path.join(ROOT, "_direct_io_tmp")
+    os.makedirs(d, exist_ok=True)
+    path = os.path.join(d, "bench_stack.gguf")
+    nb = dim * inter // 32
+    rng = np.random.default_rng(7)
+
+    def blocks():  # valid MXFP4 blocks: random codes, scale bytes 118..125
+        for _ in range(n_experts):
+            b = np.frombuffer(rng.bytes(nb * 17), np.uint8).reshape(nb, 17).copy()
+            b[:, 0] = 118 + (b[:, 0] & 7)
+            yield b
+    tensors = []
+    for l in range(n_layers):
+        for p in ("gate", "up", "down"):
+            tensors.append((gguf.expert_tensor(l, p), gguf.QT_MXFP4,
+                            [dim, inter, n_experts] if p != "down" else [inter, dim, n_experts], blocks))
+    gguf.write(path, tensors, alignment=16384)
+    try:
+        cache = ExpertCache.from_gguf(slots, path, n_layers=n_layers, readers=readers, direct=True)
+        if guess_quality is not None:
+            cache.enable_prefetch(pf_readers)
+        stack = [MoELayer(ops.FP4, dim, inter, None, n_experts, topk, slots, cache=cache, layer=l) for l in range(n_layers)]
+        grng = np.random.default_rng(8)
+        logits = [[data.zipf_logits(1, n_experts, seed=100 * t + l).to(dev) for l in range(n_layers)] for t in range(tokens + 1)]
+        true = [[[int(e) for e in torch.topk(logits[t][l][0], topk).indices] for l in range(n_layers)] for t in range(tokens + 1)]
+        x = data.activation(1, dim, seed=9, device=dev)
+        times = []
+        for t in range(tokens + 1):  # token 0 warms the caches and readers
+            torch.cuda.synchronize()
+            t0 = _t.perf_counter()
+            for l in range(n_layers):
+                stack[l].forward(x, logits[t][l])
+                nt, nl = (t, l + 1) if l + 1 < n_layers else (t + 1, 0)
+                if guess_quality is not None and nt <= tokens:
+                    keep = [e for e in true[nt][nl] if grng.random() < guess_quality]
+                    rest = [int(e) for e in grng.permutation(n_experts) if e not in keep]
+                    cache.prefetch((keep + rest)[:pf_m], nl)
+            torch.cuda.synchronize()
+            times.append(_t.perf_counter() - t0)
+        st = cache.stats()
+        pst = cache.prefetch_stats() if guess_quality is not None else None
+        info = cache.file_info()
+        cache.close()
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    ms = 1e3 * sum(times[1:]) / tokens
+    name = "off" if guess_quality is None else f"q{guess_quality:g}"
+    return {"workload": f"expert_file_stack_{n_layers}l_v41_top{topk}_prefetch_{name}", "ms_per_token": ms,
+            "tokens_per_s": 1e3 / ms, "hit_rate": st["hits"] / max(1, st["hits"] + st["misses"]),
+            "demand_GB_read": info["bytes_read"] / 1e9, "prefetch": pst, "direct": bool(info["direct"])}
+
+
 def measured_traffic():
     """HBM bytes per launch of the headline kernel from the committed rocprofv3 counter summary
     (profiles/gemv_fp4_2048x7168_traffic.md, line `traffic_bytes_per_launch: N`), or None."""
@@ -533,11 +604,17 @@ def main():
     if args.only in ("all", "file"):
         for mode, per, readers in (("direct", 1, 8), ("direct", 6, 8), ("direct", 1, 4), ("direct", 1, 16),
                                    ("cold", 1, 8), ("cold", 6, 8), ("warm", 1, 8), ("warm", 6, 8)):
-            r = file_tier_workload(torch, mode, readers, per_lookup=per)
+            r = file_tier_workload(torch, mode, readers, per_lookup=per, lookups=30 if per == 1 else 6)
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_lookup_median']:.2f} ms/lookup (p90 {r['ms_per_lookup_p90']:.2f}), "
                   f"{r['ms_per_expert']:.2f} ms/expert, {r['GB_s']:.2f} GB/s, reading {100 * r['read_share']:.0f}%",
                   file=sys.stderr, flush=True)
+    if args.only in ("all", "filestack"):
+        for q in (None, 0.0, 0.5, 1.0):
+            r = file_stack_workload(torch, q)
+            extra[r["workload"]] = r
+            print(f"# {r['workload']}: {r['ms_per_token']:.1f} ms/token, hit rate {r['hit_rate']:.2f}, demand reads "
+                  f"{r['demand_GB_read']:.2f} GB, prefetch {r['prefetch']}", file=sys.stderr, flush=True)
     if args.eager:
         r = gemv_workload(torch, "fp4", 2048, 7168, 1, args.steps, args.warmup, use_graph=False)
         extra["fp4_gemv_2048x7168_m1_eager"] = r

@@ -232,6 +232,26 @@ void *stbl_amd_cache_create_gguf(int slots, const char *path, int first_layer, i
  * prints its read time per token, stbl/model.cu:250-258). */
 int stbl_amd_cache_file_info(void *cache, uint64_t *out);
 
+/* File-backed caches: starts `readers` (1..16) background prefetch readers (the reference's
+ * STBL_PREFETCH readers, stbl/model.cu:310-345, 1007-1015), with device staging for 16 experts in
+ * flight. Once per cache. */
+int stbl_amd_cache_enable_prefetch(void *cache, int readers);
+
+/* Queues background reads of experts of `layer` (HOST ids, best guess first; the stale-router guess
+ * of stbl/model.cu:432-475, 555-586) that are not cached. Each is mapped to a slot at once (never a
+ * slot of the last lookup); prefetch readers wait while a lookup reads on demand. A lookup that
+ * routes a prefetched expert waits for it if it is being read and reads it itself if it had not
+ * started; the lookup of its layer cancels it if not routed and not started (stbl/model.cu:478-496).
+ * Returns the number queued (at most 16 in flight) or a negative hipError_t. */
+int stbl_amd_cache_prefetch(void *cache, const int *ids, int n, int layer);
+
+/* out[0..5] = issued, routed after landing, routed while still reading, cancelled, taken over by a
+ * demand read, bytes read by prefetch readers (stbl_prefetch, stbl/model.cu:1103-1105). */
+int stbl_amd_cache_prefetch_stats(void *cache, uint64_t *out);
+
+/* Test hook: paused != 0 stops prefetch readers from starting queued jobs. */
+int stbl_amd_cache_prefetch_pause(void *cache, int paused);
+
 /* Frees the cache after its copies finished. */
 void stbl_amd_cache_destroy(void *cache);
 

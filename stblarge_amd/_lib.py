@@ -56,6 +56,10 @@ SIGNATURES = {
     "stbl_amd_cache_create": (P, [I, U64, P, U64, I, I]),
     "stbl_amd_cache_create_gguf": (P, [I, ctypes.c_char_p, I, I, I, I]),
     "stbl_amd_cache_file_info": (I, [P, PU64]),
+    "stbl_amd_cache_enable_prefetch": (I, [P, I]),
+    "stbl_amd_cache_prefetch": (I, [P, PI, I, I]),
+    "stbl_amd_cache_prefetch_stats": (I, [P, PU64]),
+    "stbl_amd_cache_prefetch_pause": (I, [P, I]),
     "stbl_amd_cache_destroy": (None, [P]),
     "stbl_amd_gguf_open": (P, [ctypes.c_char_p]),
     "stbl_amd_gguf_close": (None, [P]),

@@ -30,9 +30,14 @@
 #include <string.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <atomic>
 #include <chrono>
+#include <condition_variable>
+#include <deque>
 #include <list>
+#include <memory>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <unordered_map>
@@ -72,6 +77,46 @@ struct FileTier {
     uint64_t bytes_read = 0, read_ns = 0, experts_read = 0;
 };
 
+struct Piece {
+    uint8_t *dst;  // device
+    uint64_t off, bytes;
+};
+
+// Background reads of guessed experts (stbl_amd_cache_prefetch; the reference's STBL_PREFETCH jobs,
+// stbl/model.cu:88-97, :310-345, :478-496). A job owns a slot, mapped as soon as it is queued, and a
+// staging area; prefetch readers take its pieces from a queue, waiting while a demand read runs, and
+// the reader that lands the last piece queues the repack into the slot on its own stream.
+enum PfState { PF_QUEUED, PF_READING, PF_LANDED, PF_CANCELLED, PF_FAILED, PF_TAKEN };
+constexpr int kPfStages = 16;  // prefetch jobs in flight at most
+
+struct PfJob {
+    int layer = 0, expert = 0, slot = 0, stage = 0;
+    std::vector<Piece> ps;
+    std::atomic<int> state{PF_QUEUED};
+    std::atomic<int> done{0};  // pieces landed
+    std::atomic<int> busy{0};  // readers inside a piece of this job
+};
+
+struct Prefetcher {
+    std::vector<std::thread> threads;
+    std::vector<uint8_t *> pinned, bounce;  // per reader: kPiece pinned bytes; O_DIRECT bounce buffer
+    std::vector<hipStream_t> stream;        // per reader
+    uint8_t *stage_mem = nullptr;           // device: kPfStages experts of 3 parts
+    hipEvent_t ready[kPfStages] = {};       // per stage: the repack of its last job
+    hipEvent_t slot_free[kPfStages] = {};   // per stage: recorded on the copy stream after its job's slot was free
+    std::vector<int> free_stages;
+    std::unordered_map<uint64_t, std::shared_ptr<PfJob>> jobs;  // the lookup thread's
+    std::deque<std::pair<std::shared_ptr<PfJob>, int>> queue;   // (job, piece) under mu, best guesses first
+    std::mutex mu;
+    std::condition_variable cv;
+    std::atomic<bool> stop{false};
+    std::atomic<int> demand{0};  // demand reads in flight: readers wait before starting a piece
+    std::atomic<bool> paused{false};  // test hook: readers start no job (pieces of started jobs go on)
+    std::atomic<uint64_t> bytes_read{0};
+    // issued, routed and landed, routed while still reading, cancelled, taken over by a demand read
+    uint64_t stat[5] = {};
+};
+
 struct ExpertCache {
     int device = 0;
     int slots = 0;
@@ -94,6 +139,7 @@ struct ExpertCache {
     uint64_t hits = 0, misses = 0, refill_bytes = 0, lookups = 0;
     int fail_in = -1;  // test hook: the refill after this many more fails (host side, nothing copied)
     FileTier *file = nullptr;
+    Prefetcher *pf = nullptr;
 };
 
 // GGUF MXFP4 blocks (byte 0: E8M0 scale; byte 1+i: element i in the low nibble, element 16+i in the
@@ -132,6 +178,30 @@ static int take_slot(ExpertCache &c) {
     return -1;  // caller evicts
 }
 
+// Stops the prefetch readers (each finishes the piece it is in) and frees their resources.
+static void destroy_pf(Prefetcher *P) {
+    if (!P) return;
+    {
+        std::lock_guard<std::mutex> lk(P->mu);
+        P->stop = true;
+    }
+    P->cv.notify_all();
+    for (auto &t : P->threads) t.join();
+    for (auto st : P->stream)
+        if (st) (void)hipStreamSynchronize(st);
+    for (auto st : P->stream)
+        if (st) (void)hipStreamDestroy(st);
+    for (int i = 0; i < kPfStages; i++) {
+        if (P->ready[i]) (void)hipEventDestroy(P->ready[i]);
+        if (P->slot_free[i]) (void)hipEventDestroy(P->slot_free[i]);
+    }
+    for (auto p : P->pinned)
+        if (p) (void)hipHostFree(p);
+    for (auto p : P->bounce) free(p);
+    if (P->stage_mem) (void)hipFree(P->stage_mem);
+    delete P;
+}
+
 static void destroy_file(FileTier *f) {
     if (!f) return;
     for (auto s : f->rstream)
@@ -158,6 +228,7 @@ static void destroy(ExpertCache *c) {
     int prev = 0;
     (void)hipGetDevice(&prev);
     (void)hipSetDevice(c->device);
+    destroy_pf(c->pf);  // before the file tier: its readers read the file
     if (c->copy) (void)hipStreamSynchronize(c->copy);
     destroy_file(c->file);
     for (auto &e : c->ring)
@@ -168,11 +239,6 @@ static void destroy(ExpertCache *c) {
     (void)hipSetDevice(prev);
     delete c;
 }
-
-struct Piece {
-    uint8_t *dst;  // device
-    uint64_t off, bytes;
-};
 
 // Reads `bytes` at file offset `off` into `dst` (a pinned half). Buffered reads go straight into it.
 // An O_DIRECT read covers the enclosing 4 KiB-aligned range (it may run past the end of the file,
@@ -279,7 +345,9 @@ static size_t serve_file_misses(ExpertCache &c, int layer, const std::vector<Pen
                     ps.push_back({dst + at, off + at, std::min<uint64_t>(kPiece, f.part_bytes - at)});
             }
         }
+        if (c.pf) c.pf->demand++;
         status = read_pieces(c, ps, err);
+        if (c.pf) c.pf->demand--;
         if (status != hipSuccess) return done;
         for (size_t i = 0; i < n && status == hipSuccess; i++) {
             const int s = pend[done + i].slot;
@@ -300,6 +368,156 @@ static size_t serve_file_misses(ExpertCache &c, int layer, const std::vector<Pen
         done += n;
     }
     return done;
+}
+
+// ---- prefetch ------------------------------------------------------------------------------------------
+
+static void launch_repack(const ExpertCache &c, const uint8_t *src, int slot, hipStream_t st) {
+    const FileTier &f = *c.file;
+    const ExpertLayout L = expert_layout(EXPERT_FP4, f.dim, f.inter);
+    const uint64_t n_blocks = f.part_bytes / 17;
+    hipLaunchKernelGGL(k_gguf17_to_ocp, dim3((unsigned)((3 * n_blocks + 255) / 256)), dim3(256), 0, st, src,
+                       c.mem + (uint64_t)slot * c.slot_bytes, n_blocks, L.off[0], L.off[1], L.off[2], L.off[3], L.off[4],
+                       L.off[5]);
+}
+
+// A prefetch reader: takes (job, piece) from the queue, skips pieces of jobs no longer wanted, reads
+// the piece into its pinned stage and copies it into the job's staging (waiting for the stage's
+// previous repack first). The reader that lands a job's last piece queues the repack into the slot
+// after the slot is free, records the stage's `ready` event and marks the job landed.
+static void pf_reader(ExpertCache *c, int w) {
+    Prefetcher &P = *c->pf;
+    const FileTier &f = *c->file;
+    hipError_t e = hipSetDevice(c->device);
+    for (;;) {
+        std::shared_ptr<PfJob> job;
+        int piece = 0;
+        {
+            std::unique_lock<std::mutex> lk(P.mu);
+            P.cv.wait(lk, [&] { return P.stop.load() || !P.queue.empty(); });
+            if (P.stop) return;
+            std::tie(job, piece) = P.queue.front();
+            P.queue.pop_front();
+        }
+        while ((P.demand.load() > 0 || (P.paused.load() && job->state.load() == PF_QUEUED)) && !P.stop.load())
+            std::this_thread::sleep_for(std::chrono::microseconds(20));
+        job->busy++;
+        int st = PF_QUEUED;
+        if (!job->state.compare_exchange_strong(st, PF_READING) && st != PF_READING) {
+            job->busy--;  // cancelled, taken over or failed
+            continue;
+        }
+        const Piece &pc = job->ps[piece];
+        bool ok = e == hipSuccess && hipStreamWaitEvent(P.stream[w], P.ready[job->stage], 0) == hipSuccess;
+        ok = ok && read_range(f, P.bounce.empty() ? nullptr : P.bounce[w], P.pinned[w], pc.off, pc.bytes) == 0;
+        ok = ok && hipMemcpyAsync(pc.dst, P.pinned[w], pc.bytes, hipMemcpyHostToDevice, P.stream[w]) == hipSuccess;
+        ok = ok && hipStreamSynchronize(P.stream[w]) == hipSuccess;  // the pinned stage is reused next
+        if (ok) {
+            P.bytes_read += pc.bytes;
+            if (++job->done == (int)job->ps.size()) {
+                ok = hipStreamWaitEvent(P.stream[w], P.slot_free[job->stage], 0) == hipSuccess;
+                if (ok) {
+                    launch_repack(*c, P.stage_mem + (uint64_t)job->stage * 3 * f.part_bytes, job->slot, P.stream[w]);
+                    ok = hipGetLastError() == hipSuccess && hipEventRecord(P.ready[job->stage], P.stream[w]) == hipSuccess;
+                }
+                if (ok) job->state = PF_LANDED;
+            }
+        }
+        if (!ok) job->state = PF_FAILED;
+        job->busy--;
+    }
+}
+
+static void pf_release(ExpertCache &c, const std::shared_ptr<PfJob> &j) {
+    while (j->busy.load() > 0) std::this_thread::yield();  // a reader still inside a piece of it
+    c.pf->free_stages.push_back(j->stage);
+}
+
+// A landed job becomes an ordinary cache entry: the copy stream (and through it the compute stream,
+// see order_compute) waits for its repack.
+static hipError_t pf_retire_landed(ExpertCache &c, std::unordered_map<uint64_t, std::shared_ptr<PfJob>>::iterator jt) {
+    const hipError_t e = hipStreamWaitEvent(c.copy, c.pf->ready[jt->second->stage], 0);
+    pf_release(c, jt->second);
+    c.pf->jobs.erase(jt);
+    return e;
+}
+
+// Before a lookup of `layer` (stbl/model.cu:478-496): queued guesses of this layer that were not
+// routed are cancelled and their slots freed; landed jobs of earlier layers and failed jobs that are
+// not routed now become ordinary entries or free slots.
+static hipError_t pf_settle(ExpertCache &c, int layer, const int *ids, int n) {
+    Prefetcher &P = *c.pf;
+    hipError_t e = hipSuccess;
+    for (auto it = P.jobs.begin(); it != P.jobs.end() && e == hipSuccess;) {
+        PfJob &j = *it->second;
+        bool routed = false;
+        for (int i = 0; i < n && j.layer == layer; i++) routed |= ids[i] == j.expert;
+        int st = PF_QUEUED;
+        const bool cancel = j.layer == layer && !routed && j.state.compare_exchange_strong(st, PF_CANCELLED);
+        const bool drop_failed = !routed && j.state.load() == PF_FAILED;
+        if (cancel || drop_failed) {
+            auto w = c.where.find(it->first);
+            c.lru.erase(w->second.second);
+            c.where.erase(w);
+            c.free_slots.push_back(j.slot);
+            pf_release(c, it->second);
+            if (cancel) P.stat[3]++;
+            it = P.jobs.erase(it);
+        } else if (j.layer < layer && j.state.load() == PF_LANDED) {
+            auto next = std::next(it);
+            e = pf_retire_landed(c, it);
+            it = next;
+        } else {
+            ++it;
+        }
+    }
+    return e;
+}
+
+// A routed expert that a prefetch job holds: 0 when its bytes are (or will be, in stream order) in
+// the slot; 1 when the caller must read it on demand (the job had not started, or failed); <0 error.
+static int pf_claim(ExpertCache &c, std::unordered_map<uint64_t, std::shared_ptr<PfJob>>::iterator jt) {
+    std::shared_ptr<PfJob> j = jt->second;
+    int st = PF_QUEUED;
+    bool waited = false;
+    if (!j->state.compare_exchange_strong(st, PF_TAKEN))
+        while (st == PF_READING) {  // stbl/model.cu:550-553: wait for the reading job
+            waited = true;
+            std::this_thread::yield();
+            st = j->state.load();
+        }
+    if (st == PF_LANDED) {
+        c.pf->stat[waited ? 2 : 1]++;
+        return pf_retire_landed(c, jt) == hipSuccess ? 0 : -1;
+    }
+    c.pf->stat[4]++;  // not started (now taken) or failed
+    pf_release(c, j);
+    c.pf->jobs.erase(jt);
+    return 1;
+}
+
+// The least recently used entry that may be evicted, skipping prefetch jobs still queued or reading
+// and entries `keep` names; a landed prefetch evicted unused is retired first. Slot, -1 if none, -2 on
+// a runtime error.
+template <class Keep>
+static int evict_lru(ExpertCache &c, Keep keep) {
+    for (auto it = c.lru.end(); it != c.lru.begin();) {
+        --it;
+        const uint64_t key = *it;
+        const int slot = c.where[key].first;
+        if (keep(key, slot)) continue;
+        if (c.pf) {
+            auto jt = c.pf->jobs.find(key);
+            if (jt != c.pf->jobs.end()) {
+                if (jt->second->state.load() != PF_LANDED) continue;
+                if (pf_retire_landed(c, jt) != hipSuccess) return -2;
+            }
+        }
+        c.where.erase(key);
+        c.lru.erase(it);
+        return slot;
+    }
+    return -1;
 }
 
 static ExpertCache *new_cache(int slots, uint64_t slot_bytes, int n_experts, int n_layers) {
@@ -457,6 +675,22 @@ int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **
         if (ids[i] < 0 || ids[i] >= c->n_experts) return abi_fail(hipErrorInvalidValue, "cache_lookup: expert id %d out of range", ids[i]);
     c->lookups++;
     auto key = [&](int e) { return (uint64_t)layer << 32 | (uint32_t)e; };
+    // A lookup that fails after queueing refills still orders `compute` after them: the refilled
+    // experts stay mapped, and a later lookup that hits them queues no wait of its own.
+    bool order = false;
+    auto order_compute = [&]() {
+        hipError_t e = hipEventRecord(c->ready, c->copy);
+        if (e == hipSuccess) e = hipStreamWaitEvent(compute, c->ready, 0);
+        return e;
+    };
+    if (c->pf) {
+        const hipError_t e = pf_settle(*c, layer, ids, n);
+        order = true;  // retired prefetches made the copy stream wait
+        if (e != hipSuccess) {
+            (void)order_compute();
+            return abi_status(e, "cache_lookup: settling prefetches");
+        }
+    }
     // 1. touch every cached expert of this lookup first
     for (int i = 0; i < n; i++) {
         auto it = c->where.find(key(ids[i]));
@@ -465,10 +699,9 @@ int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **
     c->touched.clear();
     int nmiss = 0;
     std::vector<PendingRead> pend;  // file tier: misses mapped, not yet read
-    auto key_of = [&](const PendingRead &p) { return key(p.expert); };
     auto unmap = [&](size_t from) {  // pending misses from `from` on stay unmapped
         for (size_t j = from; j < pend.size(); j++) {
-            auto it = c->where.find(key_of(pend[j]));
+            auto it = c->where.find(key(pend[j].expert));
             c->lru.erase(it->second.second);
             c->where.erase(it);
             c->free_slots.push_back(pend[j].slot);
@@ -477,62 +710,73 @@ int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **
         }
         pend.resize(from);
     };
-    // A lookup that fails after queueing refills still orders `compute` after them: the refilled
-    // experts stay mapped, and a later lookup that hits them queues no wait of its own.
-    int queued = 0;
-    auto order_compute = [&]() {
-        hipError_t e = hipEventRecord(c->ready, c->copy);
-        if (e == hipSuccess) e = hipStreamWaitEvent(compute, c->ready, 0);
-        return e;
+    auto fail = [&](hipError_t e, const char *fmt, int a, const char *b) {
+        if (order) (void)order_compute();
+        return abi_fail(e, fmt, a, b);
     };
     for (int i = 0; i < n; i++) {
         const uint64_t k = key(ids[i]);
         auto it = c->where.find(k);
+        int s = -1;
         if (it != c->where.end()) {
             c->lru.splice(c->lru.begin(), c->lru, it->second.second);
-            slot_ptrs[i] = c->mem + (uint64_t)it->second.first * c->slot_bytes;
-            if (hit) hit[i] = 1;
-            c->hits++;
-            c->touched.push_back(it->second.first);
-            continue;
-        }
-        // 2. miss: a free slot, or the least recently used entry not needed by this lookup
-        int s = take_slot(*c);
-        if (s < 0) {
-            const uint64_t victim = c->lru.back();
-            bool needed = false;
-            for (int j = 0; j < n; j++) needed |= key(ids[j]) == victim;
-            if (needed) {
+            s = it->second.first;
+            int claim = 0;
+            if (c->pf) {
+                auto jt = c->pf->jobs.find(k);
+                if (jt != c->pf->jobs.end()) claim = pf_claim(*c, jt);
+            }
+            if (claim < 0) {
                 unmap(0);
-                if (queued) (void)order_compute();
-                return abi_fail(hipErrorOutOfMemory, "cache_lookup: every slot is held by this lookup (%d slots)", c->slots);
+                return fail(hipErrorUnknown, "cache_lookup: expert %d: waiting for its prefetch failed%s", ids[i], "");
             }
-            s = c->where[victim].first;
-            c->where.erase(victim);
-            c->lru.pop_back();
-        }
-        uint8_t *dst = c->mem + (uint64_t)s * c->slot_bytes;
-        if (!c->file) {
-            const uint8_t *src = c->host + ((uint64_t)layer * c->n_experts + ids[i]) * c->host_stride;
-            hipError_t e = hipSuccess;
-            if (c->slot_use[s] >= 0) e = hipStreamWaitEvent(c->copy, c->ring[c->slot_use[s]], 0);
-            if (e == hipSuccess) {
-                if (c->fail_in == 0) e = hipErrorUnknown;
-                else e = hipMemcpyAsync(dst, src, c->slot_bytes, hipMemcpyHostToDevice, c->copy);
-                if (c->fail_in >= 0) c->fail_in--;
+            if (claim == 0) {
+                slot_ptrs[i] = c->mem + (uint64_t)s * c->slot_bytes;
+                if (hit) hit[i] = 1;
+                c->hits++;
+                c->touched.push_back(s);
+                continue;
             }
-            if (e != hipSuccess) {
-                c->free_slots.push_back(s);  // slot stays unmapped: the next lookup misses again
-                if (queued) (void)order_compute();
-                return abi_fail(e, "cache_lookup: refill of expert %d failed: %s", ids[i], hipGetErrorString(e));
-            }
-            queued++;
+            pend.push_back({ids[i], s});  // a prefetch that had not started or failed: read it now
         } else {
-            pend.push_back({ids[i], s});
+            // 2. miss: a free slot, or the least recently used entry not needed by this lookup
+            s = take_slot(*c);
+            if (s < 0)
+                s = evict_lru(*c, [&](uint64_t key_, int) {
+                    for (int j = 0; j < n; j++)
+                        if (key(ids[j]) == key_) return true;
+                    return false;
+                });
+            if (s == -2) {
+                unmap(0);
+                return fail(hipErrorUnknown, "cache_lookup: expert %d: retiring a prefetch failed%s", ids[i], "");
+            }
+            if (s < 0) {
+                unmap(0);
+                return fail(hipErrorOutOfMemory, "cache_lookup: every slot is held by this lookup or a prefetch (%d slots)%s",
+                            c->slots, "");
+            }
+            if (!c->file) {
+                const uint8_t *src = c->host + ((uint64_t)layer * c->n_experts + ids[i]) * c->host_stride;
+                hipError_t e = hipSuccess;
+                if (c->slot_use[s] >= 0) e = hipStreamWaitEvent(c->copy, c->ring[c->slot_use[s]], 0);
+                if (e == hipSuccess) {
+                    if (c->fail_in == 0) e = hipErrorUnknown;
+                    else e = hipMemcpyAsync(c->mem + (uint64_t)s * c->slot_bytes, src, c->slot_bytes, hipMemcpyHostToDevice, c->copy);
+                    if (c->fail_in >= 0) c->fail_in--;
+                }
+                if (e != hipSuccess) {
+                    c->free_slots.push_back(s);  // slot stays unmapped: the next lookup misses again
+                    return fail(e, "cache_lookup: refill of expert %d failed: %s", ids[i], hipGetErrorString(e));
+                }
+                order = true;
+            } else {
+                pend.push_back({ids[i], s});
+            }
+            c->lru.push_front(k);
+            c->where[k] = {s, c->lru.begin()};
         }
-        c->lru.push_front(k);
-        c->where[k] = {s, c->lru.begin()};
-        slot_ptrs[i] = dst;
+        slot_ptrs[i] = c->mem + (uint64_t)s * c->slot_bytes;
         if (hit) hit[i] = 0;
         c->misses++;
         c->refill_bytes += c->slot_bytes;
@@ -543,19 +787,137 @@ int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **
         hipError_t e;
         std::string err;
         const size_t served = serve_file_misses(*c, layer, pend, e, err);
+        order |= served > 0;
         if (served < pend.size()) {
             const int first = pend[served].expert;
             unmap(served);
-            if (queued + served) (void)order_compute();
+            if (order) (void)order_compute();
             return abi_fail(e == hipSuccess ? hipErrorUnknown : e, "cache_lookup: reading expert %d of layer %d failed: %s",
                             first, layer, err.c_str());
         }
     }
-    if (nmiss > 0) {
+    if (order) {
         const hipError_t e = order_compute();
         if (e != hipSuccess) return abi_status(e, "cache_lookup: ordering the compute stream after the refills");
     }
     return nmiss;
+}
+
+// Starts `readers` (1..16) background prefetch readers on a file-backed cache, with staging for
+// kPfStages experts in flight. Once per cache.
+int stbl_amd_cache_enable_prefetch(void *cache, int readers) {
+    ExpertCache *c = (ExpertCache *)cache;
+    if (!c || !c->file || readers < 1 || readers > kMaxReaders)
+        return abi_fail(hipErrorInvalidValue, "cache_enable_prefetch: needs a file-backed cache and 1..%d readers", kMaxReaders);
+    if (c->pf) return abi_fail(hipErrorInvalidValue, "cache_enable_prefetch: already enabled");
+    Prefetcher *P = new Prefetcher();
+    const FileTier &f = *c->file;
+    hipError_t e = hipMalloc(&P->stage_mem, (size_t)kPfStages * 3 * f.part_bytes);
+    for (int i = 0; i < kPfStages && e == hipSuccess; i++) {
+        e = hipEventCreateWithFlags(&P->ready[i], hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&P->slot_free[i], hipEventDisableTiming);
+        P->free_stages.push_back(kPfStages - 1 - i);
+    }
+    P->pinned.assign(readers, nullptr);
+    P->stream.assign(readers, nullptr);
+    for (int w = 0; w < readers && e == hipSuccess; w++) {
+        e = hipHostMalloc((void **)&P->pinned[w], kPiece, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipStreamCreateWithFlags(&P->stream[w], hipStreamNonBlocking);
+        if (e == hipSuccess && f.dfd >= 0) {
+            void *b = nullptr;
+            if (posix_memalign(&b, kAlign, kPiece + 2 * kAlign)) e = hipErrorOutOfMemory;
+            P->bounce.push_back((uint8_t *)b);
+        }
+    }
+    if (e != hipSuccess) {
+        destroy_pf(P);
+        return abi_status(e, "cache_enable_prefetch");
+    }
+    c->pf = P;
+    for (int w = 0; w < readers; w++) P->threads.emplace_back(pf_reader, c, w);
+    return 0;
+}
+
+// Queues background reads of the given experts of `layer` (HOST array, best guess first; the
+// reference's stale-router guesses, stbl/model.cu:555-586) that are not cached. Each gets a slot
+// (never one of the last lookup's, so the kernels queued for it keep their weights) and is mapped at
+// once; a later lookup that routes it waits for it, reads it itself if it had not started, and the
+// lookup of its layer cancels it if it is not routed and has not started. Stops early when kPfStages
+// jobs are in flight or no slot can be taken. Returns the number queued or a negative hipError_t.
+int stbl_amd_cache_prefetch(void *cache, const int *ids, int n, int layer) {
+    ExpertCache *c = (ExpertCache *)cache;
+    if (!c || !c->pf || !ids || n < 0 || layer < 0 || layer >= c->n_layers)
+        return abi_fail(hipErrorInvalidValue, "cache_prefetch: bad arguments or prefetch not enabled");
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= c->n_experts) return abi_fail(hipErrorInvalidValue, "cache_prefetch: expert id %d out of range", ids[i]);
+    Prefetcher &P = *c->pf;
+    const FileTier &f = *c->file;
+    std::vector<std::shared_ptr<PfJob>> fresh;
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < n && !P.free_stages.empty(); i++) {
+        const uint64_t key = (uint64_t)layer << 32 | (uint32_t)ids[i];
+        if (c->where.count(key)) continue;
+        int s = take_slot(*c);
+        if (s < 0)
+            s = evict_lru(*c, [&](uint64_t, int slot) {
+                return std::find(c->touched.begin(), c->touched.end(), slot) != c->touched.end();
+            });
+        if (s == -2) {
+            e = hipErrorUnknown;
+            break;
+        }
+        if (s < 0) break;
+        auto j = std::make_shared<PfJob>();
+        j->layer = layer, j->expert = ids[i], j->slot = s, j->stage = P.free_stages.back();
+        // the slot is free once the compute stream's last use of it is done
+        if (c->slot_use[s] >= 0) e = hipStreamWaitEvent(c->copy, c->ring[c->slot_use[s]], 0);
+        if (e == hipSuccess) e = hipEventRecord(P.slot_free[j->stage], c->copy);
+        if (e != hipSuccess) {
+            c->free_slots.push_back(s);
+            break;
+        }
+        P.free_stages.pop_back();
+        uint8_t *stage = P.stage_mem + (uint64_t)j->stage * 3 * f.part_bytes;
+        for (int p = 0; p < 3; p++) {
+            const uint64_t off = f.part_off[3 * layer + p] + (uint64_t)ids[i] * f.part_bytes;
+            for (uint64_t at = 0; at < f.part_bytes; at += kPiece)
+                j->ps.push_back({stage + p * f.part_bytes + at, off + at, std::min<uint64_t>(kPiece, f.part_bytes - at)});
+        }
+        c->lru.push_front(key);
+        c->where[key] = {s, c->lru.begin()};
+        P.jobs[key] = j;
+        fresh.push_back(j);
+        P.stat[0]++;
+    }
+    if (!fresh.empty()) {
+        {
+            std::lock_guard<std::mutex> lk(P.mu);
+            for (auto &j : fresh)
+                for (int pc = 0; pc < (int)j->ps.size(); pc++) P.queue.emplace_back(j, pc);
+        }
+        P.cv.notify_all();
+    }
+    if (e != hipSuccess) return abi_status(e, "cache_prefetch");
+    return (int)fresh.size();
+}
+
+// Test hook: while paused, prefetch readers start no queued job (a started one is finished).
+int stbl_amd_cache_prefetch_pause(void *cache, int paused) {
+    ExpertCache *c = (ExpertCache *)cache;
+    if (!c || !c->pf) return abi_fail(hipErrorInvalidValue, "cache_prefetch_pause: prefetch not enabled");
+    c->pf->paused = paused != 0;
+    return 0;
+}
+
+// out[0..5] = prefetches issued, routed after landing, routed while still reading (the lookup
+// waited), cancelled unrouted, taken over by a demand read (not started or failed), bytes read by
+// the prefetch readers (the reference's stbl_prefetch counters, stbl/model.cu:1103-1105).
+int stbl_amd_cache_prefetch_stats(void *cache, uint64_t *out) {
+    ExpertCache *c = (ExpertCache *)cache;
+    if (!c || !c->pf || !out) return abi_fail(hipErrorInvalidValue, "cache_prefetch_stats: prefetch not enabled");
+    for (int i = 0; i < 5; i++) out[i] = c->pf->stat[i];
+    out[5] = c->pf->bytes_read.load();
+    return 0;
 }
 
 // Marks every slot of the last lookup as read by the work queued so far on `compute`: a later

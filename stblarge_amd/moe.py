@@ -52,6 +52,28 @@ class ExpertCache:
         keys = ("dim", "inter", "experts", "slot_bytes", "direct", "bytes_read", "read_ns", "experts_read")
         return dict(zip(keys, [int(v) for v in out]))
 
+    def enable_prefetch(self, readers=8):
+        """Background prefetch readers for a file-backed cache (stbl_amd_cache_enable_prefetch)."""
+        _lib.check(_lib.load().stbl_amd_cache_enable_prefetch(self.handle, readers), "cache_enable_prefetch")
+
+    def prefetch(self, ids, layer):
+        """Queues background reads of guessed experts of `layer`, best first; returns how many."""
+        n = len(ids)
+        arr = (ctypes.c_int * max(n, 1))(*[int(i) for i in ids])
+        r = _lib.load().stbl_amd_cache_prefetch(self.handle, arr, n, layer)
+        if r < 0:
+            _lib.check(r, "cache_prefetch")
+        return r
+
+    def prefetch_stats(self):
+        out = (ctypes.c_uint64 * 6)()
+        _lib.check(_lib.load().stbl_amd_cache_prefetch_stats(self.handle, out), "cache_prefetch_stats")
+        keys = ("issued", "routed_landed", "routed_reading", "cancelled", "taken_over", "bytes_read")
+        return dict(zip(keys, [int(v) for v in out]))
+
+    def prefetch_pause(self, paused):
+        _lib.check(_lib.load().stbl_amd_cache_prefetch_pause(self.handle, 1 if paused else 0), "cache_prefetch_pause")
+
     def lookup(self, ids, layer=0, stream=None):
         """Slots (device addresses) and hit flags of expert ids, in order; returns (ptrs, hits, misses)."""
         n = len(ids)

@@ -175,3 +175,92 @@ def test_moe_layer_over_file_equals_host_pool(gpu, file_dir):
     assert over_file.cache.stats() == over_pool.cache.stats()
     over_pool.close()
     over_file.close()
+
+
+# ---- prefetch (stbl/model.cu:310-345, :478-496, :550-586) -----------------------------------------------
+
+def _wait_for(cond, seconds=60.0):
+    import time
+    end = time.monotonic() + seconds
+    while not cond():
+        assert time.monotonic() < end, "prefetch readers did not finish"
+        time.sleep(0.005)
+
+
+def test_prefetch_cancel_take_over_and_land(gpu, tmp_path):
+    dim, inter, n = 256, 128, 10
+    path = tmp_path / "pf.gguf"
+    parts = expert_file(path, dim, inter, 2, n, seed=11)
+    want = {k: direct_slot(v, dim, inter, gpu) for k, v in parts.items()}
+    expert_bytes = 3 * (inter * dim // 32 * 17)
+    cache = ExpertCache.from_gguf(8, path, n_layers=2, readers=2)
+    cache.enable_prefetch(3)
+    cache.prefetch_pause(True)  # every job stays queued
+    assert cache.prefetch([0, 1, 2, 3], layer=1) == 4
+    assert cache.prefetch([0, 3], layer=1) == 0  # already mapped
+    ptrs, hits, nmiss = cache.lookup([0, 5], layer=1)
+    # 0 was queued and not started: the lookup took it over (a miss into the job's slot);
+    # 1, 2 and 3 were not routed and not started: cancelled, their slots free again
+    assert hits == [False, False] and nmiss == 2
+    st = cache.prefetch_stats()
+    assert (st["issued"], st["taken_over"], st["cancelled"], st["routed_landed"], st["bytes_read"]) == (4, 1, 3, 0, 0)
+    assert all(cache.peek(e, layer=1) is None for e in (1, 2, 3))
+    torch.cuda.synchronize()
+    for e, p in zip((0, 5), ptrs):
+        assert torch.equal(read_device(p, cache.slot_bytes), want[1, e])
+    cache.mark_used()
+    cache.prefetch_pause(False)
+    assert cache.prefetch([6, 7], layer=0) == 2
+    _wait_for(lambda: cache.prefetch_stats()["bytes_read"] == 2 * expert_bytes)
+    ptrs, hits, nmiss = cache.lookup([6, 7, 8], layer=0)
+    assert hits == [True, True, False] and nmiss == 1
+    st = cache.prefetch_stats()
+    assert st["routed_landed"] + st["routed_reading"] == 2 and st["issued"] == 6
+    torch.cuda.synchronize()
+    for e, p in zip((6, 7, 8), ptrs):
+        assert torch.equal(read_device(p, cache.slot_bytes), want[0, e])
+    cache.mark_used()
+    # a guess queued for the next layer lands before that layer is looked up: a hit
+    assert cache.prefetch([9], layer=1) == 1
+    _wait_for(lambda: cache.prefetch_stats()["bytes_read"] == 3 * expert_bytes)
+    ptrs, hits, _ = cache.lookup([9], layer=1)
+    assert hits == [True]
+    torch.cuda.synchronize()
+    assert torch.equal(read_device(ptrs[0], cache.slot_bytes), want[1, 9])
+    cache.close()
+
+
+def test_moe_stack_with_prefetch_equals_without(gpu, file_dir):
+    # three layers over one file: decode tokens layer by layer, with and without stale-router guesses
+    # for the next layer queued after each layer; the outputs must be bit-identical
+    d, _ = file_dir
+    dim, inter, n, topk, slots, n_layers = 256, 128, 16, 3, 12, 3
+    path = d / "stack.gguf"
+    expert_file(path, dim, inter, n_layers, n, seed=41, make=quantized_parts)
+    sparts = quantized_parts(dim, inter, 77)
+    shared = direct_slot(sparts, dim, inter, gpu).to(gpu)
+    plain = ExpertCache.from_gguf(slots, path, n_layers=n_layers, readers=2)
+    ahead = ExpertCache.from_gguf(slots, path, n_layers=n_layers, readers=2)
+    ahead.enable_prefetch(3)
+    mk = lambda cache, l: MoELayer(ops.FP4, dim, inter, None, n, topk, slots, shared_slot=shared, cache=cache, layer=l)
+    stack_plain = [mk(plain, l) for l in range(n_layers)]
+    stack_ahead = [mk(ahead, l) for l in range(n_layers)]
+    rng = np.random.default_rng(3)
+    for token in range(10):
+        x = data.activation(1, dim, seed=500 + token).to(gpu)
+        for l in range(n_layers):
+            logits = data.zipf_logits(1, n, seed=1000 * token + l).to(gpu)
+            y_plain = stack_plain[l].forward(x, logits)
+            y_ahead = stack_ahead[l].forward(x, logits)
+            assert torch.equal(y_plain, y_ahead), f"token {token} layer {l}"
+            if l + 1 < n_layers:  # a guess: the next layer's true top-k mixed with random experts
+                nxt = data.zipf_logits(1, n, seed=1000 * token + l + 1)
+                true = [int(e) for e in torch.topk(nxt[0], topk).indices]
+                guess = true[:2] + [int(e) for e in rng.choice(n, 3, replace=False)]
+                ahead.prefetch(list(dict.fromkeys(guess)), l + 1)
+            x = y_plain
+    st = ahead.prefetch_stats()
+    assert st["issued"] > 0 and st["routed_landed"] + st["routed_reading"] + st["taken_over"] > 0
+    assert plain.stats()["hits"] + plain.stats()["misses"] == ahead.stats()["hits"] + ahead.stats()["misses"]
+    plain.close()
+    ahead.close()
