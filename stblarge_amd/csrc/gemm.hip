@@ -12,9 +12,10 @@
 //                     e2m1 weights. The activation scales (powers of two) and the FP4 weight scales
 //                     (E8M0) are the MFMA's own per-32 scale operands, so the hardware applies them
 //                     exactly; the FP8 weights' fp32 block scale multiplies each 128-K step's product
-//                     in fp32. Split K with the cross-slice sum fused (last workgroup per tile), so
-//                     the GEMM proper is one launch; stbl_amd_gemm_q takes already quantized
-//                     activations, stbl_amd_gemm quantizes X first (two launches).
+//                     in fp32. Split K: each workgroup writes its K slice's partial tile and
+//                     k_gemm_reduce adds the slices in order (the kernel boundary is the
+//                     synchronization point); stbl_amd_gemm_q takes already quantized activations,
+//                     stbl_amd_gemm quantizes X first (one more launch).
 // Operand layout of the 16x16x128 f8f6f4 MFMA (probed on gfx950): lane l = r + 16 g holds row r of A
 // (column r of B); e4m3 operands hold K bytes [16g, 16g+16) and [64+16g, 64+16g+16) of the 128-K
 // step, e2m1 operands K elements [32g, 32g+32) (low nibble first); the lane's E8M0 scale covers K
@@ -205,8 +206,19 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const f32x4 *__restrict__ p
     if (i >= ntiles * kGemmTileVecs) return;
     const int tile = i / kGemmTileVecs, q = i % kGemmTileVecs;
     const f32x4 *tp = part + (size_t)tile * slices * kGemmTileVecs + q;
+    // slices are loaded up to 8 at a time, all loads issued before the first add (a plain loop waits
+    // for each load in turn), and added in slice order
+    constexpr int kBatch = 8;
     f32x4 s = tp[0];
-    for (int sl = 1; sl < slices; sl++) s += tp[(size_t)sl * kGemmTileVecs];
+    for (int sl0 = 1; sl0 < slices; sl0 += kBatch) {
+        f32x4 v[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; i++)
+            if (sl0 + i < slices) v[i] = tp[(size_t)(sl0 + i) * kGemmTileVecs];
+#pragma unroll
+        for (int i = 0; i < kBatch; i++)
+            if (sl0 + i < slices) s += v[i];
+    }
     // q = tid + 256 j of the producing workgroup: m-tile j, n-tile tid / 64, lane tid % 64
     const int j = q >> 8, t = q & 255, r = t & 15, g = (t >> 4) & 3, w = t >> 6;
     const int n = tile * 64 + 16 * w + r;
