@@ -74,6 +74,11 @@ void stbl_swiglu_batch(float *out, const float *g, const float *u, const float *
 /* stbl/kernels.h:39 -- y += a * x (fp32). */
 void stbl_axpy(float *y, const float *x, float a, int n, hipStream_t st);
 
+/* stbl/kernels.h:34 (stbl/kernels.cu:436-442): s[i] = sqrt(softplus(s[i])) in place, softplus with
+ * torch's threshold of 20 -- the engine's router scores after stbl_gemv_f32. The same scores
+ * stbl_amd_route computes with score_fn = 1. */
+void stbl_sqrt_softplus(float *s, int n, hipStream_t st);
+
 /* ---- v2: quantized GEMV (ref/kernel.py:85-102 with M <= 4 activation rows) ------------------------- */
 
 /* y[m][rows] = x[m][k] . Wdeq^T with fp32 accumulation, Wdeq = e2m1(codes) * 2^(scales-127).

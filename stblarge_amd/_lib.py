@@ -28,6 +28,7 @@ SIGNATURES = {
     "stbl_gemv_mxfp4": (None, [P, P, P, I, I, P]),
     "stbl_gemv_mxfp4_batch": (None, [PP, PP, PP, I, I, I, P]),
     "stbl_gemv_f32": (None, [P, P, P, I, I, I, P]),
+    "stbl_sqrt_softplus": (None, [P, I, P]),
     "stbl_gemv_bf16": (None, [P, P, P, I, I, I, I, P]),
     "stbl_swiglu": (None, [P, P, P, F, F, I, P]),
     "stbl_swiglu_batch": (None, [P, P, P, PF, I, F, I, P]),

@@ -235,6 +235,15 @@ __global__ void k_moe_combine(PickTable picks, int npick, const uint16_t *__rest
 
 // ---- router -------------------------------------------------------------------------------------
 
+// The reference engine's router score sqrt(softplus(l)), softplus with torch's threshold of 20
+// (stbl/kernels.cu:436-442); k_route and stbl_sqrt_softplus share it, so their scores are identical.
+__device__ __forceinline__ float sqrt_softplus(float l) { return sqrtf(l > 20.f ? l : log1pf(expf(l))); }
+
+__global__ __launch_bounds__(256) void k_sqrt_softplus(float *__restrict__ s, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) s[i] = sqrt_softplus(s[i]);
+}
+
 // One workgroup of 256 threads per token. score = 1 / (1 + exp(-logit)) (score_fn 0, the
 // configuration's router) or sqrt(softplus(logit)) with softplus(l) = l above 20, else
 // log1p(exp(l)) (score_fn 1, stbl/kernels.cu:436-442); the top-k of score + bias (ties to the lower
@@ -251,7 +260,7 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
     const int t = blockIdx.x, tid = threadIdx.x;
     for (int e = tid; e < n_exp; e += 256) {
         const float l = logits[(size_t)t * n_exp + e];
-        const float s = score_fn == 1 ? sqrtf(l > 20.f ? l : log1pf(expf(l))) : __fdiv_rn(1.f, 1.f + expf(-l));
+        const float s = score_fn == 1 ? sqrt_softplus(l) : __fdiv_rn(1.f, 1.f + expf(-l));
         sc[e] = s;
         if (scores) scores[(size_t)t * n_exp + e] = s;
     }
@@ -487,6 +496,16 @@ int stbl_amd_moe_experts(int fmt, void *y, const void *x, int t, int dim, int in
 uint64_t stbl_amd_moe_work_bytes(int t, int topk, int dim, int inter) {
     const uint64_t pairs = (uint64_t)t * (topk + 1);
     return align256(pairs * inter * 2) + align256(pairs * dim * 2);
+}
+
+// stbl/kernels.h:34: s[i] = sqrt(softplus(s[i])) in place, the engine's router scores.
+void stbl_sqrt_softplus(float *s, int n, hipStream_t st) {
+    if (!s || n <= 0) {
+        abi_fail(hipErrorInvalidValue, "stbl_sqrt_softplus: bad arguments (n=%d)", n);
+        return;
+    }
+    hipLaunchKernelGGL(k_sqrt_softplus, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, n);
+    abi_status(hipGetLastError(), "stbl_sqrt_softplus launch");
 }
 
 int stbl_amd_route(const float *logits, const float *bias, int t, int n_exp, int topk, float route_scale, int score_fn,

@@ -258,6 +258,17 @@ def stbl_gemv_f32(y, w, x, rows, k, round_out=0):
     return y
 
 
+def stbl_sqrt_softplus(s, n=None):
+    """The reference ABI's router scores in place: s = sqrt(softplus(s)) (fp32, device)."""
+    _need(s, torch.float32, "s")
+    n = s.numel() if n is None else n
+    if n > s.numel():
+        raise ValueError("stbl_sqrt_softplus: n exceeds the buffer")
+    _lib.load().stbl_sqrt_softplus(_ptr(s), n, _stream())
+    _lib.check(None, "stbl_sqrt_softplus")
+    return s
+
+
 def stbl_gemv_bf16(y, w, x, rows, k, round_out=0, group_rows=0):
     """bf16-weight GEMV of the reference ABI: y [rows] = w [rows, k] . x_r with x_r the (r /
     group_rows)-th k-long row of x when group_rows > 0."""

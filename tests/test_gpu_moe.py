@@ -179,6 +179,22 @@ def test_route_sqrt_softplus(gpu):
     assert np.allclose(np_(w), ow, rtol=8 * 2.0 ** -24, atol=0)
 
 
+def test_stbl_sqrt_softplus(gpu):
+    # the reference ABI's in-place scores (stbl/test_kernels.py:208-211: 384 values of N(0, 8), bar
+    # 1e-6 of max |want|); also bit-identical to the scores stbl_amd_route reports for the same logits
+    score = lambda v: np.array([oracle.route_score(float(x), oracle.SCORE_SQRT_SOFTPLUS) for x in v], np.float32)
+    s = data.normal((384,), 8.0, seed=21)
+    got = ops.stbl_sqrt_softplus(s.clone().to(gpu))
+    want = score(s.numpy())
+    assert np.max(np.abs(np_(got) - want)) <= 1e-6 * np.max(np.abs(want))
+    _, _, sc = ops.route(s.view(1, 384).to(gpu), 6, want_scores=True, score_fn=ops.SCORE_SQRT_SOFTPLUS)
+    assert np.array_equal(np_(sc).ravel().view(np.uint32), np_(got).view(np.uint32))
+    edge = torch.tensor([-200.0, -30.0, 0.0, 19.999, 20.0, 20.001, 88.0, 1e30], dtype=torch.float32)
+    got = np_(ops.stbl_sqrt_softplus(edge.clone().to(gpu)))
+    want = score(edge.numpy())
+    assert np.all(np.abs(got - want) <= 1e-6 * np.maximum(np.abs(want), 1.0))
+
+
 def test_route(gpu):
     t, e, topk = 4, 256, 8
     logits = data.zipf_logits(t, e, seed=5)
