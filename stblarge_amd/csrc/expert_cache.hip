@@ -253,7 +253,7 @@ static int read_range(const FileTier &f, uint8_t *bounce, uint8_t *dst, uint64_t
     for (uint64_t got = 0; got < need;) {
         const ssize_t r = pread(direct ? f.dfd : f.fd, buf + got, len - got, (off_t)(start + got));
         if (r < 0 && errno == EINTR) continue;
-        if (r <= 0) return r == 0 ? -1 : errno;
+        if (r <= 0) return r == 0 ? -1 : (errno ? errno : EIO);
         got += (uint64_t)r;
     }
     if (direct) memcpy(dst, bounce + (off - start), bytes);
