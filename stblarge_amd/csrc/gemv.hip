@@ -33,28 +33,35 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     const int cc = active ? c : 0;
     const int row0 = blockIdx.x * R;
 
-    // 0. OCP FP4 scales: the tile's rows hold one contiguous block of R * nch scale bytes, fetched
-    //    with one 16-byte load per thread (from the block's 16-byte units; such a load never crosses
-    //    a page, so the bytes around the block are safe to read) and handed out through LDS, instead
-    //    of one byte load per row per lane. Issued first, so waiting for it does not wait for W.
-    constexpr bool kStageScales = F == WFmt::FP4_OCP;
+    // 0. OCP FP4 scales. Tiles of 4 or more rows stage them: the tile's rows hold one contiguous
+    //    block of R * nch scale bytes, fetched with one 16-byte load per thread (from the block's
+    //    16-byte units; such a load never crosses a page, so the bytes around the block are safe to
+    //    read) and handed out through LDS, instead of one byte load per row per lane. With 8 rows
+    //    (batched matrices) the block is loaded before the weights, so each row's products start as
+    //    soon as that row arrives; with 4 rows (3-4 tokens) it is loaded after them and the tile
+    //    waits for all its loads at once; tiles of 1-2 rows load each lane's scale bytes directly.
+    //    (Measured: each choice is the fastest of the three for its tile size.)
+    constexpr bool kStageScales = F == WFmt::FP4_OCP && R >= 4;
+    constexpr bool kScalesEarly = R >= 8;
     static_assert(!kStageScales || R <= kMaxStageRows, "the staged scale block holds at most kMaxStageRows rows");
     constexpr int kScaleLoads = R > 8 ? 2 : 1;  // units <= R nch / 16 + 2 <= kScaleLoads * threads
-    __shared__ u32x4 lds_sc[kStageScales ? kMaxScaleUnits : 1];
+    // One slot past the block takes the writes of threads without a unit, so the LDS write is
+    // unconditional: a conditional one lets the compiler sink the load into the branch.
+    __shared__ u32x4 lds_sc[kStageScales ? kMaxScaleUnits + 1 : 1];
     u32x4 scv[kScaleLoads] = {};
-    uintptr_t sc_a0 = 0;
     size_t sc_len = 0;
     int sc_units = 0;
-    if constexpr (kStageScales) {
+    auto load_scale_block = [&]() {
+        // pointer arithmetic (no integer round trip), so these stay global loads
         const uint8_t *blk = (const uint8_t *)J.s + (size_t)row0 * nch;
         sc_len = (size_t)(min(row0 + R, rows) - row0) * nch;
-        sc_a0 = (uintptr_t)blk & ~(uintptr_t)15;
-        const uintptr_t a1 = ((uintptr_t)blk + sc_len - 1) & ~(uintptr_t)15;
-        sc_units = (int)((a1 - sc_a0) >> 4) + 1;
+        const uint8_t *p0 = blk - ((uintptr_t)blk & 15);
+        sc_units = (int)((((uintptr_t)blk & 15) + sc_len - 1) >> 4) + 1;
 #pragma unroll
         for (int i = 0; i < kScaleLoads; i++)
-            scv[i] = ld_stream((const void *)min(sc_a0 + 16 * (uintptr_t)(threadIdx.x + i * blockDim.x), a1));
-    }
+            scv[i] = ld_stream(p0 + 16 * (size_t)min((int)threadIdx.x + i * (int)blockDim.x, sc_units - 1));
+    };
+    if constexpr (kStageScales && kScalesEarly) load_scale_block();
     // 1. loads: x first (it is needed by every row), then every row of the tile. fp32 activations
     //    (the reference ABI) are widened once and use exact FMAs; bf16 activations stay packed for
     //    the dot2 path (gemv_core.hpp).
@@ -64,6 +71,10 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     else load_x_packed<M, CH>(xw, (const uint16_t *)J.x, k, cc * CH);
     u32x4 w[R];
     uint32_t sb[R];
+    if constexpr (F == WFmt::FP4_OCP && !kStageScales) {  // tiles of 1-2 rows: each lane's bytes
+#pragma unroll
+        for (int r = 0; r < R; r++) sb[r] = ld_stream_u8((const uint8_t *)J.s + (size_t)min(row0 + r, rows - 1) * nch + cc);
+    }
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const size_t row = (size_t)min(row0 + r, rows - 1);
@@ -75,6 +86,11 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
             w[r] = ld_stream(J.w + row * k + (size_t)cc * 16);
         }
     }
+    if constexpr (kStageScales && !kScalesEarly) load_scale_block();
+    // With 2-4 tokens every load above is issued before anything below runs: without this fence the
+    // scheduler trades registers for issue order and holds x loads of later tokens back behind the
+    // first waits (4 tokens: 6.7 instead of 6.0 us at 2048x7168). One token gains nothing from it.
+    if constexpr (M >= 2) __builtin_amdgcn_sched_barrier(0);
     float lscale = 1.f;  // FP8: one block scale per lane for the whole tile
     if constexpr (F == WFmt::FP8_B128)
         lscale = ((const float *)J.s)[(size_t)(row0 >> 7) * ((k + 127) >> 7) + ((cc * 16) >> 7)];
@@ -84,7 +100,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
 #pragma unroll
         for (int i = 0; i < kScaleLoads; i++) {
             const int u = threadIdx.x + i * blockDim.x;
-            if (u < sc_units) lds_sc[u] = scv[i];
+            lds_sc[u < sc_units ? u : kMaxScaleUnits] = scv[i];
         }
         __syncthreads();
         const uint8_t *sl = (const uint8_t *)lds_sc + (((uintptr_t)J.s + (size_t)row0 * nch) & 15);
