@@ -107,6 +107,11 @@ __global__ __launch_bounds__(512) void k_moe_gateup(MoeJobs jobs, ExpertLayout L
     const int cc = active ? c : 0;
     const int row0 = blockIdx.x * R;
     const int m = J.m;
+    // the output row and route weight of the (token, row) this thread may finish, read now: indexed
+    // by thread they are memory loads, which at the end would add a round trip to every workgroup
+    const int t_out = min((int)(threadIdx.x >> 1) / R, M - 1);
+    const int pair_out = J.pair[t_out];
+    const float w_out = J.w[t_out];
 
     uint32_t xw[M][CH / 2];
 #pragma unroll
@@ -154,7 +159,7 @@ __global__ __launch_bounds__(512) void k_moe_gateup(MoeJobs jobs, ExpertLayout L
         uv = fminf(fmaxf(uv, -limit), limit);
         gv = fminf(gv, limit);
     }
-    h[(size_t)J.pair[t] * inter + row0 + r] = f32_to_bf16_bits(__fdiv_rn(gv, 1.f + expf(-gv)) * uv * J.w[t]);
+    h[(size_t)pair_out * inter + row0 + r] = f32_to_bf16_bits(__fdiv_rn(gv, 1.f + expf(-gv)) * uv * w_out);
 }
 
 // ---- down ------------------------------------------------------------------------------------------
@@ -172,6 +177,7 @@ __global__ __launch_bounds__(512) void k_moe_down(MoeJobs jobs, ExpertLayout L, 
     const int cc = active ? c : 0;
     const int row0 = blockIdx.x * R;
     const int m = J.m;
+    const int pair_out = J.pair[min((int)threadIdx.x / R, M - 1)];  // read early, as in k_moe_gateup
 
     uint32_t xw[M][CH / 2];
 #pragma unroll
@@ -203,7 +209,7 @@ __global__ __launch_bounds__(512) void k_moe_down(MoeJobs jobs, ExpertLayout L, 
     if (!wave_total<M * R>(tot, red, &v)) return;
     const int t = threadIdx.x / R, r = threadIdx.x % R;
     if (t >= m || row0 + r >= dim) return;
-    const size_t at = (size_t)J.pair[t] * dim + row0 + r;
+    const size_t at = (size_t)pair_out * dim + row0 + r;
     if (out_f32) ((float *)o)[at] = v;
     else ((uint16_t *)o)[at] = f32_to_bf16_bits(v);
 }
