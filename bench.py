@@ -327,6 +327,57 @@ def compat_gemv_workload(torch, kind, rows, k, steps, warmup, group_rows=0):
             "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS, "weight_copies": copies}
 
 
+def ref_method_workload(torch, kind, rows, k, group_rows=0, reps=200):
+    """The reference ABI's GEMVs timed the way stbl/bench_gemv.py:18-28 times them, for a
+    like-for-like comparison with that script's output: the same weight tensor every launch (so it
+    stays in the 256 MB Infinity Cache), launches issued one by one, events around 200 of them after
+    10 warmups, and GB/s = weight-tensor bytes / time (stbl/bench_gemv.py:40,48,55,83: the GGUF rows
+    with their scale bytes, the FP8 codes without their scales, the bf16 weights). kind "copy" is
+    the script's 64 MiB device copy (read + write bytes, 50 launches, :58-61)."""
+    from stblarge_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(rows + k)
+    lib = _lib.load()
+    st = ops._stream
+    y = torch.empty(max(rows, 1), device=dev)
+    if kind == "copy":
+        a = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        fn, nbytes, reps = (lambda: b.copy_(a)), 2 * a.numel(), 50
+    elif kind == "mxfp4":
+        w = torch.randint(0, 256, (rows, k // 32 * 17), dtype=torch.uint8, device=dev, generator=g)
+        w[:, ::17] = 120
+        x = torch.randn(k, device=dev, generator=g)
+        fn, nbytes = (lambda: lib.stbl_gemv_mxfp4(ops._ptr(y), ops._ptr(w), ops._ptr(x), rows, k, st())), w.numel()
+    elif kind == "fp8":
+        w = torch.randint(0, 120, (rows, k), dtype=torch.uint8, device=dev, generator=g)
+        sc = torch.full((rows // 32 + 1, k // 32), 120, dtype=torch.uint8, device=dev)
+        x = torch.randn(k, device=dev, generator=g)
+        fn = lambda: lib.stbl_gemv_fp8(ops._ptr(y), ops._ptr(w), ops._ptr(sc), ops._ptr(x), rows, k, 1, st())
+        nbytes = w.numel()
+    else:  # bf16, optionally grouped
+        w = torch.randn((rows, k), device=dev, generator=g).to(torch.bfloat16)
+        xrows = rows // group_rows if group_rows else 1
+        x = torch.randn(xrows * k, device=dev, generator=g)
+        fn = lambda: lib.stbl_gemv_bf16(ops._ptr(y), ops._ptr(w), ops._ptr(x), rows, k, 1, group_rows, st())
+        nbytes = w.numel() * 2
+    for _ in range(10):
+        fn()
+    _lib.check(None, f"ref_method {kind}")
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a0.record()
+    for _ in range(reps):
+        fn()
+    a1.record()
+    torch.cuda.synchronize()
+    us = a0.elapsed_time(a1) / reps * 1000
+    name = "ref_method_" + ("device_copy_64MiB" if kind == "copy" else f"gemv_{kind}_{rows}x{k}" +
+                            (f"_group{group_rows}" if group_rows else ""))
+    return {"workload": name, "us": us, "GB_s": nbytes / us / 1e3, "bytes": nbytes, "reps": reps}
+
+
 def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168, prequant=False):
     """C5: multi-token expert GEMM, M = 64 tokens, W [2048 x 7168] FP4 or FP8 (scaled f8f6f4 MFMA).
     prequant: the activations are quantized outside the timed region and the GEMM proper is timed
@@ -589,6 +640,15 @@ def main():
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
                   flush=True)
+    if args.only in ("all", "refabi"):
+        # stbl/bench_gemv.py's own method and rows (:95-107): cache-resident weights, eager launches
+        for kind, rows, k, grp in (("mxfp4", 2304, 5120, 0), ("mxfp4", 5120, 2304, 0), ("fp8", 2304, 5120, 0),
+                                   ("fp8", 5120, 2304, 0), ("bf16", 4096, 5120, 0), ("bf16", 8192, 4096, 1024),
+                                   ("fp8", 32768, 1280, 0), ("fp8", 5120, 8192, 0), ("fp8", 1280, 5120, 0),
+                                   ("fp8", 512, 5120, 0), ("copy", 0, 0, 0)):
+            r = ref_method_workload(torch, kind, rows, k, grp)
+            extra[r["workload"]] = r
+            print(f"# {r['workload']}: {r['us']:.2f} us, {r['GB_s']:.1f} GB/s", file=sys.stderr, flush=True)
     if args.only in ("all", "moe", "moeallhit"):
         for t, v41 in ((1, False), (4, False), (1, True), (4, True)):
             r = moe_allhit_workload(torch, t, max(100, args.steps // 10), 32, v41=v41)
