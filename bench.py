@@ -578,8 +578,17 @@ def cpu_baseline(seconds):
         if el >= seconds:
             break
     del torch
+    model = "unknown CPU"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     return {"value": alg * reps / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} x fp4 GEMV 2048x7168 m=1 (oracle orc_gemv_fp4, scalar C, fp64 accumulate) in {el:.1f} s"}
+            "sample": f"{reps} x fp4 GEMV 2048x7168 m=1 (oracle orc_gemv_fp4, scalar C, fp64 accumulate) in {el:.1f} s "
+                      f"on one core of {model}"}
 
 
 def main():
