@@ -174,3 +174,54 @@ class MoELayer:
 
     def close(self):
         self.cache.close()
+
+
+class MoEStack:
+    """Decode through routed MoE layers whose experts share one cache, with the reference engine's
+    stale-router prefetch (stbl/model.cu:426-475, 555-586): after layer l, layer l+1's router is run
+    on layer l's input, its top `prefetch` experts are queued for background reads, and layer l+1's
+    lookup then finds them landed, waits for them, reads them itself or cancels the unrouted ones.
+
+    routers[l]: fp32 [n_experts, dim] router weights of layer l; the logits are stbl_gemv_f32 of the
+    layer's input, as in the engine (stbl/model.cu:430). Between layers the hidden state takes the
+    layer's output as a residual update (h = bf16(h + y)); the layers between MoE blocks (attention,
+    norms) are outside this path. step(h) returns the final hidden state, bf16 [t, dim]."""
+
+    def __init__(self, cache, fmt, dim, inter, n_experts, topk, routers, biases=None, shared_slots=None, prefetch=0,
+                 score_fn=ops.SCORE_SIGMOID, route_scale=1.0, limit=0.0, official=False, shared_fmt=None,
+                 max_tokens=4):
+        n_layers = len(routers)
+        biases = biases or [None] * n_layers
+        shared_slots = shared_slots or [None] * n_layers
+        self.cache, self.routers, self.biases = cache, routers, biases
+        self.dim, self.n_experts, self.topk, self.prefetch = dim, n_experts, topk, prefetch
+        self.score_fn, self.route_scale = score_fn, route_scale
+        self.layers = [MoELayer(fmt, dim, inter, None, n_experts, topk, cache.slots, shared_slot=shared_slots[l],
+                                bias=biases[l], route_scale=route_scale, limit=limit, official=official,
+                                max_tokens=max_tokens, score_fn=score_fn, shared_fmt=shared_fmt, cache=cache, layer=l)
+                       for l in range(n_layers)]
+        if prefetch:
+            cache.enable_prefetch()
+
+    def _logits(self, layer, hf):
+        t = hf.shape[0]
+        out = torch.empty((t, self.n_experts), dtype=torch.float32, device=hf.device)
+        for i in range(t):
+            ops.stbl_gemv_f32(out[i], self.routers[layer], hf[i], self.n_experts, self.dim)
+        return out
+
+    def step(self, h, stream=None):
+        n_layers = len(self.layers)
+        for l, layer in enumerate(self.layers):
+            hf = h.float()
+            y = layer.forward(h, self._logits(l, hf), stream=stream)
+            if self.prefetch and l + 1 < n_layers:
+                ids, _ = ops.route(self._logits(l + 1, hf), min(self.prefetch, self.n_experts), self.biases[l + 1],
+                                   self.route_scale, score_fn=self.score_fn)
+                guesses = list(dict.fromkeys(e for row in ids.cpu().tolist() for e in row))
+                self.cache.prefetch(guesses, l + 1)
+            h = (hf + y.float()).to(torch.bfloat16)
+        return h
+
+    def close(self):
+        self.cache.close()

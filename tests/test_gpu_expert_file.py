@@ -20,7 +20,7 @@ import torch
 
 import oracle
 from stblarge_amd import data, gguf, ops
-from stblarge_amd.moe import ExpertCache, MoELayer
+from stblarge_amd.moe import ExpertCache, MoELayer, MoEStack
 from util import bf16_ulps, np_, read_device
 
 pytestmark = pytest.mark.gpu
@@ -262,5 +262,29 @@ def test_moe_stack_with_prefetch_equals_without(gpu, file_dir):
     st = ahead.prefetch_stats()
     assert st["issued"] > 0 and st["routed_landed"] + st["routed_reading"] + st["taken_over"] > 0
     assert plain.stats()["hits"] + plain.stats()["misses"] == ahead.stats()["hits"] + ahead.stats()["misses"]
+    plain.close()
+    ahead.close()
+
+
+def test_moe_stack_stale_router_prefetch(gpu, tmp_path):
+    # the engine's own guesses: layer l+1's router run on layer l's input (stbl/model.cu:432-475),
+    # its top 6 queued after each layer; outputs bit-identical to the same stack without prefetch
+    dim, inter, n, topk, slots, n_layers = 256, 128, 16, 3, 12, 3
+    path = tmp_path / "stale.gguf"
+    expert_file(path, dim, inter, n_layers, n, seed=51, make=quantized_parts)
+    routers = [data.normal((n, dim), 0.05, seed=60 + l).to(gpu) for l in range(n_layers)]
+    shared = direct_slot(quantized_parts(dim, inter, 88), dim, inter, gpu).to(gpu)
+    mk = lambda pf: MoEStack(ExpertCache.from_gguf(slots, path, n_layers=n_layers, readers=2), ops.FP4, dim, inter, n,
+                             topk, routers, shared_slots=[shared] * n_layers, prefetch=pf)
+    plain, ahead = mk(0), mk(6)
+    for token in range(8):
+        h = data.activation(1 + token % 2, dim, seed=700 + token).to(gpu)
+        a, b = plain.step(h), ahead.step(h)
+        assert torch.equal(a, b), f"token {token}"
+        assert torch.isfinite(a.float()).all()
+    st = ahead.cache.prefetch_stats()
+    # small residual updates keep the next layer's routing close to the stale guess
+    assert st["issued"] > 0 and st["routed_landed"] + st["routed_reading"] > 0
+    assert plain.cache.stats()["hits"] + plain.cache.stats()["misses"] == ahead.cache.stats()["hits"] + ahead.cache.stats()["misses"]
     plain.close()
     ahead.close()
