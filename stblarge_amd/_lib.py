@@ -8,7 +8,8 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libstbl_amd.so")
+# STBL_AMD_LIB names another build of the library (for comparing builds); default the in-tree one
+LIB_PATH = os.environ.get("STBL_AMD_LIB") or os.path.join(HERE, "libstbl_amd.so")
 
 P = ctypes.c_void_p
 I = ctypes.c_int
