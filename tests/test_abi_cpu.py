@@ -51,6 +51,11 @@ def test_argument_checks_fail_without_touching_the_device():
     assert st < 0
     code, msg = _lib.last_error()
     assert code != 0 and "k % 32" in msg
+    # one chunk past the largest K a launch takes (8 waves x 64 chunks)
+    assert lib.stbl_amd_gemv_fp4(P(16), P(16), P(16), P(16), 1, 8, 16384 + 32, 0, None) < 0
+    assert "k <= 16384" in _lib.last_error()[1]
+    assert lib.stbl_amd_gemv_fp8(P(16), P(16), P(16), P(16), 1, 8, 8192 + 16, 0, None) < 0
+    assert "k <= 8192" in _lib.last_error()[1]
     # m out of range
     assert lib.stbl_amd_gemv_fp8(P(16), P(16), P(16), P(16), 5, 8, 64, 0, None) < 0
     assert "m must be" in _lib.last_error()[1]

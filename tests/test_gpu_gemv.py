@@ -58,6 +58,22 @@ def test_gemv_fp8(gpu, rows, k, m):
     assert_gemv(np_(y32), np_(y16), want)
 
 
+@pytest.mark.parametrize("fmt,k", [(0, 16384), (1, 8192)])
+@pytest.mark.parametrize("m", [1, 4])
+def test_gemv_maximum_k_and_ragged_rows(gpu, fmt, k, m):
+    # the largest K a launch takes (512 chunks of 32 FP4 / 16 FP8 elements: 8 waves) with row counts
+    # that fill no tile: one row, and 33 (one past a 32-row scale block for FP8)
+    q = oracle.quant_fp4 if fmt == 0 else oracle.quant_fp8_b128
+    ref = oracle.gemv_fp4 if fmt == 0 else oracle.gemv_fp8_b128
+    run = ops.gemv_fp4 if fmt == 0 else ops.gemv_fp8
+    for rows in (1, 33):
+        c, sc = q(data.weight(rows, k, seed=rows + k).numpy())
+        x = data.activation(m, k, seed=rows + m)
+        want = ref(c, sc, x.float().numpy())
+        dc, ds = torch.from_numpy(c).to(gpu), torch.from_numpy(sc).to(gpu)
+        assert_gemv(np_(run(dc, ds, x.to(gpu), out_f32=True)), np_(run(dc, ds, x.to(gpu))), want)
+
+
 def test_gemv_official_mode(gpu):
     # the reference engine quantizes the activation first (stbl/model.cu:236-242): act_quant per 32
     # then the GEMV on the dequantized activation
@@ -153,6 +169,24 @@ def test_gemv_batch(gpu, fmt):
         xs.append(x.to(gpu))
     ys = ops.gemv_batch(cs, ss, xs, fmt, out_f32=True)
     ys16 = ops.gemv_batch(cs, ss, xs, fmt)
+    for y, y16, want in zip(ys, ys16, wants):
+        assert_gemv(np_(y), np_(y16), want)
+
+
+def test_gemv_batch_ragged_rows_eight_row_tiles(gpu):
+    # 16 x 1100 rows at K = 7168 is enough workgroups for 8-row tiles; 1100 = 137 x 8 + 4 leaves the
+    # last tile half empty
+    rows, k, n = 1100, 7168, 16
+    cs, ss, xs, wants = [], [], [], []
+    for j in range(n):
+        c, s = oracle.quant_fp4(data.weight(rows, k, seed=700 + j).numpy())
+        x = data.activation(1, k, seed=800 + j)
+        wants.append(oracle.gemv_fp4(c, s, x.float().numpy()))
+        cs.append(torch.from_numpy(c).to(gpu))
+        ss.append(torch.from_numpy(s).to(gpu))
+        xs.append(x.to(gpu))
+    ys = ops.gemv_batch(cs, ss, xs, 0, out_f32=True)
+    ys16 = ops.gemv_batch(cs, ss, xs, 0)
     for y, y16, want in zip(ys, ys16, wants):
         assert_gemv(np_(y), np_(y16), want)
 

@@ -53,6 +53,20 @@ def test_expert_ffn(gpu, fmt, dim, inter, official):
         assert_gemv(y32[t], y16[t], raw)
 
 
+@pytest.mark.parametrize("fmt,dim,inter", [(ops.FP4, 160, 96), (ops.FP4, 16384, 64), (ops.FP8, 384, 640),
+                                            (ops.FP8, 8192, 128)])
+def test_expert_ffn_ragged_and_maximum_dims(gpu, fmt, dim, inter):
+    # dims that fill no row tile (160 = 5 x 32, 96 = 3 x 32; FP8 3 and 5 scale blocks), and the
+    # largest K each GEMV of the FFN takes (gate/up over dim = 16384 FP4 / 8192 FP8 elements)
+    slot, parts = make_expert(fmt, dim, inter, seed=dim + inter, gpu=gpu)
+    x = data.activation(2, dim, seed=9)
+    y16 = np_(ops.expert_ffn(slot, x.to(gpu), fmt, dim, inter, 0.61, 7.0, False))
+    y32 = np_(ops.expert_ffn(slot, x.to(gpu), fmt, dim, inter, 0.61, 7.0, False, out_f32=True))
+    for t in range(2):
+        _, raw = oracle_ffn(fmt, parts, dim, inter, x[t].float().numpy(), 0.61, 7.0, False)
+        assert_gemv(y32[t], y16[t], raw)
+
+
 def test_expert_ffn_m4_matches_m1(gpu):
     dim, inter = 1024, 512
     slot, _ = make_expert(ops.FP4, dim, inter, seed=3, gpu=gpu)
@@ -110,6 +124,23 @@ def test_moe_experts_shared_token_groups(gpu):
     packed = [np.concatenate([p.ravel() for p in e[1]]) for e in experts]
     want = oracle.moe_fp4([[packed[i] for i in row] for row in pick], w, None, dim, inter, x.float().numpy())
     assert bf16_ulps(y, want).max() <= 1
+
+
+def test_moe_experts_maximum_tokens_and_topk(gpu):
+    # the largest step a launch takes: 16 tokens x top-16 over 17 routed experts plus a shared one,
+    # so most experts get 14-16 tokens (jobs of 4 + 4 + 4 + 1..4)
+    dim, inter, topk, n = 256, 128, 16, 18
+    experts = [make_expert(ops.FP4, dim, inter, seed=300 + 3 * i, gpu=gpu) for i in range(n)]
+    rng = np.random.default_rng(16)
+    t = 16
+    pick = [list(rng.choice(n - 1, size=topk, replace=False)) for _ in range(t)]
+    w = (rng.random((t, topk)) / topk).astype(np.float32)
+    x = data.activation(t, dim, seed=13)
+    y = np_(ops.moe_experts(x.to(gpu), [e[0] for e in experts], pick, w.tolist(), ops.FP4, dim, inter, shared=n - 1))
+    packed = [np.concatenate([p.ravel() for p in e[1]]) for e in experts]
+    want = oracle.moe_fp4([[packed[i] for i in row] for row in pick], w, packed[n - 1], dim, inter, x.float().numpy())
+    u = bf16_ulps(y, want)
+    assert u.max() <= 1 and u.mean() < 0.02, (u.max(), u.mean())
 
 
 def deq_parts(fmt, parts):
