@@ -16,12 +16,16 @@
 //      masks dead lanes;
 //   3. reduces each (token, row) partial over the 64 lanes with DPP moves only, and over the waves
 //      through LDS in wave order, so the result is the same on every run.
+#include <atomic>
+
 #include "abi_util.hpp"
 #include "gemv_core.hpp"
 
 namespace stbl {
 
-template <WFmt F, bool XF32, int M, int R>
+// DW: OCP FP4 scales fetched as dwords and handed to the lanes by ds_bpermute (tiles of 4 rows
+// whose scale rows are dword-aligned: k % 128 == 0 and 4-byte aligned scales).
+template <WFmt F, bool XF32, int M, int R, bool DW>
 __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, int out_mode) {
     using T = WTraits<F>;
     constexpr int CH = T::CH;
@@ -33,15 +37,20 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     const int cc = active ? c : 0;
     const int row0 = blockIdx.x * R;
 
-    // 0. OCP FP4 scales. Tiles of 4 or more rows stage them: the tile's rows hold one contiguous
+    // 0. OCP FP4 scales. A wave's 64 chunks of one row have 64 consecutive scale bytes. When they
+    //    are dword-aligned (DW), lane j < 16 R loads dword j % 16 of row j / 16 (one instruction for
+    //    up to 4 rows) and each lane takes its byte from lane 16 r + lane / 4 with ds_bpermute.
+    //    Otherwise tiles of 4 or more rows stage them: the tile's rows hold one contiguous
     //    block of R * nch scale bytes, fetched with one 16-byte load per thread (from the block's
     //    16-byte units; such a load never crosses a page, so the bytes around the block are safe to
     //    read) and handed out through LDS, instead of one byte load per row per lane. With 8 rows
     //    (batched matrices) the block is loaded before the weights, so each row's products start as
-    //    soon as that row arrives; with 4 rows (3-4 tokens) it is loaded after them and the tile
-    //    waits for all its loads at once; tiles of 1-2 rows load each lane's scale bytes directly.
-    //    (Measured: each choice is the fastest of the three for its tile size.)
-    constexpr bool kStageScales = F == WFmt::FP4_OCP && R >= 4;
+    //    soon as that row arrives; with 4 rows it is loaded after them and the tile waits for all
+    //    its loads at once; tiles of 1-2 rows load each lane's scale bytes directly.
+    //    (Measured: dwords beat the LDS block by 5% at 4 rows x 4 tokens; at 2 rows they are up to
+    //    1.6% slower than bytes; the early LDS block is the fastest at 8 rows.)
+    static_assert(!DW || (F == WFmt::FP4_OCP && R <= 4), "dword scale loads: FP4 tiles of at most 4 rows");
+    constexpr bool kStageScales = F == WFmt::FP4_OCP && R >= 4 && !DW;
     constexpr bool kScalesEarly = R >= 8;
     static_assert(!kStageScales || R <= kMaxStageRows, "the staged scale block holds at most kMaxStageRows rows");
     constexpr int kScaleLoads = R > 8 ? 2 : 1;  // units <= R nch / 16 + 2 <= kScaleLoads * threads
@@ -71,7 +80,12 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     else load_x_packed<M, CH>(xw, (const uint16_t *)J.x, k, cc * CH);
     u32x4 w[R];
     uint32_t sb[R];
-    if constexpr (F == WFmt::FP4_OCP && !kStageScales) {  // tiles of 1-2 rows: each lane's bytes
+    uint32_t sdw = 0;
+    if constexpr (DW) {  // rows and dwords clamped into the matrix; lanes j >= 16 R repeat the last row
+        const int rr = min(lane >> 4, R - 1);
+        const int dwi = min(wave * 16 + (lane & 15), (nch >> 2) - 1);
+        sdw = __builtin_nontemporal_load((const uint32_t *)((const uint8_t *)J.s + (size_t)min(row0 + rr, rows - 1) * nch) + dwi);
+    } else if constexpr (F == WFmt::FP4_OCP && !kStageScales) {  // tiles of 1-2 rows: each lane's bytes
 #pragma unroll
         for (int r = 0; r < R; r++) sb[r] = ld_stream_u8((const uint8_t *)J.s + (size_t)min(row0 + r, rows - 1) * nch + cc);
     }
@@ -108,6 +122,13 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
         for (int r = 0; r < R; r++) sb[r] = sl[min((size_t)r * nch + cc, sc_len - 1)];
     }
 
+    if constexpr (DW) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t d = (uint32_t)__builtin_amdgcn_ds_bpermute((r * 16 + (lane >> 2)) << 2, (int)sdw);
+            sb[r] = (d >> (8 * (lane & 3))) & 255u;
+        }
+    }
     // 2. products, scales, masking; 3. lane reduction
     __shared__ float red[kMaxWaves][M * R];
     float tot[M * R];
@@ -250,16 +271,42 @@ static inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 template <WFmt F, bool XF32, int M, int R>
 static hipError_t launch_r(const GemvJobs &jobs, int njobs, int rows, int k, int out_mode, hipStream_t st) {
-    const int waves = ceil_div(k / WTraits<F>::CH, 64);
-    hipLaunchKernelGGL((k_gemv<F, XF32, M, R>), dim3(ceil_div(rows, R), njobs), dim3(64 * waves), 0, st, jobs, rows,
-                       k, out_mode);
+    const int nch = k / WTraits<F>::CH, waves = ceil_div(nch, 64);
+    const dim3 grid(ceil_div(rows, R), njobs), block(64 * waves);
+    if constexpr (F == WFmt::FP4_OCP && R == 4) {
+        bool dw = nch % 4 == 0;
+        for (int j = 0; j < njobs; j++) dw = dw && ((uintptr_t)jobs.j[j].s & 3) == 0;
+        if (dw) {
+            hipLaunchKernelGGL((k_gemv<F, XF32, M, R, true>), grid, block, 0, st, jobs, rows, k, out_mode);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((k_gemv<F, XF32, M, R, false>), grid, block, 0, st, jobs, rows, k, out_mode);
     return hipGetLastError();
 }
 
-// Rows per workgroup (M <= 2): 2 keeps a single matrix spread over every CU (1024+ workgroups at
-// the configurations' shapes); a launch with much more work (batched matrices) takes 8 rows per
+// Compute units of the current device (256 on MI355X), read once per device.
+static int device_cus() {
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// Rows per workgroup (M <= 2). A launch with much more work (batched matrices) takes 8 rows per
 // workgroup, so the fixed per-workgroup cost (x chunk, prologue, reduction) is spread over 4x the
-// weight bytes while still leaving thousands of workgroups.
+// weight bytes while still leaving thousands of workgroups. Otherwise 4 rows halve the x loads per
+// weight byte, unless that leaves the busiest CU more rows than 2-row tiles would (workgroups come
+// in whole rounds over the CUs: 2304 rows are 2.25 rounds of 4-row tiles but 4.5 of 2-row ones)
+// or a row takes too few waves: one wave (FP4 K <= 2048) or, for FP8, whose x chunk per weight
+// byte is half FP4's, two. Measured (M = 1, us, 2 -> 4 rows): FP4 2048x7168 4.01 -> 3.84,
+// 5120x2304 3.98 -> 3.84, 7168x2048 3.71 -> 3.99, 2304x5120 3.64 -> 3.84; FP8 2048x7168 4.73 ->
+// 4.66, 7168x2048 4.52 -> 4.58; M = 2 FP4 2048x7168 5.09 -> 4.51.
 template <WFmt F, bool XF32, int M>
 static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int out_mode, hipStream_t st) {
     if constexpr (M > 2) {
@@ -275,6 +322,12 @@ static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int o
     } else {
         const long wgs8 = (long)ceil_div(rows, 8) * njobs * ceil_div(k / WTraits<F>::CH, 64);
         if (wgs8 >= 8192) return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
+        const int cus = device_cus();
+        const long busiest2 = ceil_div(ceil_div(rows, 2) * njobs, cus) * 2L;
+        const long busiest4 = ceil_div(ceil_div(rows, 4) * njobs, cus) * 4L;
+        const int min_waves = F == WFmt::FP4_OCP ? 2 : 3;
+        if (ceil_div(k / WTraits<F>::CH, 64) >= min_waves && busiest4 <= busiest2)
+            return launch_r<F, XF32, M, 4>(jobs, njobs, rows, k, out_mode, st);
         return launch_r<F, XF32, M, 2>(jobs, njobs, rows, k, out_mode, st);
     }
 }
