@@ -244,14 +244,17 @@ static void destroy(ExpertCache *c) {
 // An O_DIRECT read covers the enclosing 4 KiB-aligned range (it may run past the end of the file,
 // which ends it short) and must land in pageable memory: the kernel refuses to pin pages of
 // hipHostMalloc memory for direct I/O (EFAULT), so it lands in the reader's page-aligned bounce
-// buffer and the payload is copied into dst. Returns 0 or an errno value (-1: end of file).
+// buffer and the payload is copied into dst. A direct read that returns short of a 4 KiB boundary
+// is finished with buffered reads (O_DIRECT needs aligned offsets). Returns 0 or an errno value
+// (-1: end of file).
 static int read_range(const FileTier &f, uint8_t *bounce, uint8_t *dst, uint64_t off, uint64_t bytes) {
     const bool direct = f.dfd >= 0;
     const uint64_t start = direct ? off & ~(kAlign - 1) : off;
     const uint64_t need = off - start + bytes, len = direct ? (need + kAlign - 1) & ~(kAlign - 1) : need;
     uint8_t *buf = direct ? bounce : dst;
     for (uint64_t got = 0; got < need;) {
-        const ssize_t r = pread(direct ? f.dfd : f.fd, buf + got, len - got, (off_t)(start + got));
+        const bool dio = direct && (got & (kAlign - 1)) == 0;
+        const ssize_t r = pread(dio ? f.dfd : f.fd, buf + got, (dio ? len : need) - got, (off_t)(start + got));
         if (r < 0 && errno == EINTR) continue;
         if (r <= 0) return r == 0 ? -1 : (errno ? errno : EIO);
         got += (uint64_t)r;

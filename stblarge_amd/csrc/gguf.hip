@@ -8,6 +8,8 @@
 #include <fcntl.h>
 #include <unistd.h>
 
+#include <stdint.h>
+
 #include <algorithm>
 #include <cstring>
 
@@ -152,7 +154,12 @@ static GgufFile *parse(const char *path, std::string &err) {
             const uint32_t nd = r.get<uint32_t>();
             if (nd > 8) throw std::string("tensor with more than 8 dims");
             uint64_t n = 1;
-            for (uint32_t d = 0; d < nd; d++) e.second.dims.push_back(r.get<uint64_t>()), n *= e.second.dims.back();
+            for (uint32_t d = 0; d < nd; d++) {
+                const uint64_t dim = r.get<uint64_t>();
+                if (dim && n > (UINT64_MAX >> 5) / dim) throw "tensor " + e.first + " has an implausible shape";
+                e.second.dims.push_back(dim);
+                n *= dim;
+            }
             e.second.type = r.get<uint32_t>();
             e.second.offset = r.get<uint64_t>();
             if (!tensor_bytes(e.second.type, n, &e.second.nbytes)) e.second.nbytes = 0;  // unsupported type
@@ -160,8 +167,10 @@ static GgufFile *parse(const char *path, std::string &err) {
         }
         const uint64_t data = (r.pos + alignment - 1) / alignment * alignment;
         for (auto &e : list) {
+            if (e.second.offset > g->size || data > g->size - e.second.offset ||
+                e.second.nbytes > g->size - data - e.second.offset)
+                throw "tensor " + e.first + " runs past the end of the file";
             e.second.offset += data;
-            if (e.second.offset + e.second.nbytes > g->size) throw "tensor " + e.first + " runs past the end of the file";
             g->tensors[e.first] = e.second;
         }
     } catch (const std::string &e) {

@@ -98,6 +98,21 @@ def test_reader_rejects_damaged_files(tmp_path, damage):
     assert "gguf_open" in str(e.value)
 
 
+@pytest.mark.parametrize("case", ["huge_dims", "huge_offset"])
+def test_reader_rejects_overflowing_tensor_infos(tmp_path, case):
+    # a shape whose element count overflows 64 bits, or an offset near 2^64, must not wrap around
+    # into a small in-bounds range
+    dims = (1 << 40, 1 << 40) if case == "huge_dims" else (4,)
+    off = 0 if case == "huge_dims" else (1 << 64) - 16
+    info = _s("t") + struct.pack("<I", len(dims)) + struct.pack(f"<{len(dims)}Q", *dims) + struct.pack("<IQ", 0, off)
+    head = struct.pack("<IIQQ", 0x46554747, 3, 1, 0) + info
+    base = (len(head) + 31) // 32 * 32
+    p = tmp_path / "ovf.gguf"
+    p.write_bytes(head + bytes(base - len(head)) + bytes(64))
+    with pytest.raises(RuntimeError, match="implausible shape|past the end"):
+        gguf.GgufFile(p)
+
+
 def test_reader_missing_file(tmp_path):
     with pytest.raises(RuntimeError, match="cannot open"):
         gguf.GgufFile(tmp_path / "nope.gguf")
