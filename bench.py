@@ -14,6 +14,7 @@ One JSON line is printed; other configurations appear under "extra".
 """
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -325,6 +326,44 @@ def compat_gemv_workload(torch, kind, rows, k, steps, warmup, group_rows=0):
     name = f"ref_abi_gemv_{kind}_{rows}x{k}" + (f"_group{group_rows}" if group_rows else "")
     return {"workload": name, "ms_per_step": ms, "steps": n, "alg_bytes": alg,
             "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS, "weight_copies": copies}
+
+
+def compat_batch_workload(torch, rows, k, n, steps, warmup):
+    """stbl_gemv_mxfp4_batch as the reference engine issues it for one layer's experts
+    (stbl/model.cu:536-539: gate and up of every selected expert in one call, then their down
+    projections in another): n GGUF matrices per launch, fp32 x, every launch on n different
+    matrices from a >= 512 MB rotation."""
+    from stblarge_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(rows * n + k)
+    wb = rows * (k // 32) * 17
+    sets = max(2, math.ceil(ROTATE_BYTES / (wb * n)))
+    mats = []
+    for _ in range(sets * n):
+        w = torch.randint(0, 256, (rows, k // 32 * 17), dtype=torch.uint8, device=dev, generator=g)
+        w[:, ::17] = 120
+        mats.append(w)
+    xs = [torch.randn(k, device=dev, generator=g) for _ in range(n)]
+    ys = [torch.empty(rows, device=dev) for _ in range(n)]
+    P = ctypes.c_void_p
+    y_arr = (P * n)(*[y.data_ptr() for y in ys])
+    x_arr = (P * n)(*[x.data_ptr() for x in xs])
+    w_arrs = [(P * n)(*[mats[i * n + j].data_ptr() for j in range(n)]) for i in range(sets)]
+    lib = _lib.load()
+    st = ops._stream
+
+    def launch(i):
+        lib.stbl_gemv_mxfp4_batch(y_arr, w_arrs[i], x_arr, n, rows, k, st())
+
+    launch(0)
+    _lib.check(None, "stbl_gemv_mxfp4_batch")
+    ms, steps_run = timed_steps(torch, launch, sets, steps, warmup)
+    alg = n * (wb + 4 * k + 4 * rows)
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"workload": f"ref_abi_gemv_mxfp4_batch{n}_{rows}x{k}", "ms_per_step": ms, "steps": steps_run,
+            "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS, "weight_sets": sets}
 
 
 def ref_method_workload(torch, kind, rows, k, group_rows=0, reps=200):
@@ -648,6 +687,12 @@ def main():
             r = compat_gemv_workload(torch, kind, rows, k, args.steps, args.warmup, grp)
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
+                  flush=True)
+        # the engine's expert batches at V4.1 shapes, top-6: 12 gate/up matrices, then 6 down
+        for rows, k, n in ((2304, 5120, 12), (5120, 2304, 6)):
+            r = compat_batch_workload(torch, rows, k, n, max(200, args.steps // 4), args.warmup)
+            extra[r["workload"]] = r
+            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.2f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
                   flush=True)
     if args.only in ("all", "refabi"):
         # stbl/bench_gemv.py's own method and rows (:95-107): cache-resident weights, eager launches

@@ -43,9 +43,10 @@ enum OutMode { OUT_BF16 = 0, OUT_F32 = 1, OUT_F32_ROUNDED = 2 };
 // cover it from the enclosing 4-byte boundary (each dword starts inside the buffer, and a 4-byte
 // aligned dword never crosses a page) and realign with v_alignbyte.
 __device__ __forceinline__ void load_gguf_block(const uint8_t *blk, uint32_t &scale, u32x4 &codes) {
-    const uintptr_t a = (uintptr_t)blk;
-    const uint32_t *d = (const uint32_t *)(a & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)(a & 3);
+    // pointer arithmetic, not an integer round trip: the loads stay global loads (as flat loads they
+    // cost 2-7% on the reference ABI's GEMVs)
+    const uint32_t sh = (uint32_t)((uintptr_t)blk & 3);
+    const uint32_t *d = (const uint32_t *)(blk - sh);
     uint32_t v[5];
 #pragma unroll
     for (int i = 0; i < 5; i++) v[i] = d[i];

@@ -136,8 +136,9 @@ def test_stbl_gemv_mxfp4_gguf(gpu, rows, k):
     assert_gemv(got, got, want, tol=2.0 ** -8)
 
 
-def test_stbl_gemv_mxfp4_batch(gpu):
-    rows, k, n = 256, 1024, 16
+@pytest.mark.parametrize("rows,k,n", [(256, 1024, 16), (2304, 5120, 12), (5120, 2304, 6)])
+def test_stbl_gemv_mxfp4_batch(gpu, rows, k, n):
+    # small, and the reference engine's V4.1 expert batches (12 gate/up, 6 down matrices)
     rng = np.random.default_rng(3)
     ys, ws, xs, wants = [], [], [], []
     for j in range(n):

@@ -41,13 +41,20 @@ def bf16_ulps(got_bf16, want_f64):
 
 
 def assert_gemv(got_f32, got_bf16, want, tol=1e-3):
-    """fp32 output within `tol` (normwise), bf16 output at most one bf16 step from bf16(want)."""
+    """fp32 output within `tol` (normwise), bf16 output at most one bf16 step from bf16(want).
+
+    The step check skips outputs below 2^-16 of the largest: those are sums that cancel to ~1e-5 of
+    their terms, whose last bf16 digits fp32 accumulation in any order cannot resolve (a row of 5120
+    random FP4 products summing to 5.9e-5 from an absolute sum of 608 came out 3.9e-7 from exact,
+    two bf16 steps). The normwise bound above still covers them."""
     e = rel_err(got_f32, want)
     assert e <= tol, f"relative error {e:.3e} > {tol}"
     if got_bf16 is not None:
         u = bf16_ulps(got_bf16, want)
-        assert u.max() <= 1, f"bf16 output {u.max()} steps away"
-        assert np.mean(u) < 0.05, f"{np.mean(u):.3f} of bf16 outputs flipped"
+        w = np.abs(np.asarray(want, np.float64))
+        resolved = w > 2.0 ** -16 * w.max()
+        assert u[resolved].max(initial=0) <= 1, f"bf16 output {u[resolved].max()} steps away"
+        assert np.mean(u[resolved]) < 0.05, f"{np.mean(u[resolved]):.3f} of bf16 outputs flipped"
     return e
 
 
