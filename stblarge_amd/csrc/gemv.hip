@@ -319,8 +319,12 @@ static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int o
         // fp32 activations (the reference ABI): a lane's x chunk is 4-8x its weight bytes per row, so
         // 4 rows share it (measured 2-8% faster than 2 at 2304x5120 and 5120x2304; 8 gains nothing
         // there), and 8 in launches with much more work: the engine's expert batches (12 x 2304x5120
-        // 32.7 -> 24.8 us, 6 x 5120x2304 17.0 -> 14.3, 16 x 2048x7168 52.2 -> 37.0)
+        // 32.7 -> 24.8 us, 6 x 5120x2304 17.0 -> 14.3, 16 x 2048x7168 52.2 -> 37.0). The largest GGUF
+        // FP4 launches take 16 (12 x 2304x5120 25.3 -> 23.3 us, 16 x 2048x7168 38.1 -> 31.5); FP8
+        // E8M0 at 32768x1280 was 5% slower with 16, so it keeps 8.
         const long wgs8 = (long)ceil_div(rows, 8) * njobs * ceil_div(k / WTraits<F>::CH, 64);
+        if constexpr (F == WFmt::FP4_GGUF)
+            if (wgs8 >= 8192) return launch_r<F, XF32, M, 16>(jobs, njobs, rows, k, out_mode, st);
         if (wgs8 >= 4096) return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
         return launch_r<F, XF32, M, 4>(jobs, njobs, rows, k, out_mode, st);
     } else {
