@@ -340,3 +340,54 @@ def test_moe_layer_reference_engine_semantics(gpu):
                               x.float().numpy(), limit=10.0, official=True)
         assert bf16_ulps(y, want).max() <= 1
     layer.close()
+
+
+def test_reference_abi_moe_composition(gpu):
+    # The reference engine's MoE step issued through the drop-in ABI exactly as stbl/model.cu:508-592
+    # issues it (official numerics): x quantized once; the routed experts' gate and up in one
+    # stbl_gemv_mxfp4_batch on GGUF blocks, stbl_swiglu_batch with the route weights,
+    # stbl_act_quant_fp8, the downs in a second batch; the FP8 E8M0 shared expert through
+    # stbl_gemv_fp8 (its input re-quantized as the engine's gemv() does, :236-242); then stbl_axpy of
+    # every expert output in top-k order, the shared one, and stbl_round_bf16. Checked against the
+    # oracle's composition and against the fused stbl_amd_moe_experts on the same experts.
+    dim, inter, topk, limit = 512, 256, 3, 10.0
+    experts = [make_expert(ops.FP4, dim, inter, seed=900 + 3 * i, gpu=gpu) for i in range(topk)]
+    shared, sparts = make_expert(ops.FP8_E8M0, dim, inter, seed=990, gpu=gpu)
+    ws = [0.52, 0.31, 0.17]
+    x = data.activation(1, dim, seed=91)
+    f32 = lambda n: torch.zeros(n, dtype=torch.float32, device=gpu)
+
+    def gguf(codes, sc):
+        return torch.from_numpy(oracle.ocp_to_gguf17(codes, sc)).to(gpu)
+
+    mats = [[gguf(p[0], p[1]), gguf(p[2], p[3]), gguf(p[4], p[5])] for _, p in experts]
+    xq = x.float().to(gpu).reshape(-1).clone()
+    ops.stbl_act_quant_fp8(xq)
+    g, u, mid, eo = f32(topk * inter), f32(topk * inter), f32(topk * inter), f32(topk * dim)
+    ops.stbl_gemv_mxfp4_batch([g[j * inter:(j + 1) * inter] for j in range(topk)] +
+                              [u[j * inter:(j + 1) * inter] for j in range(topk)],
+                              [m[0] for m in mats] + [m[1] for m in mats], [xq] * (2 * topk), inter, dim)
+    ops.stbl_swiglu_batch(mid, g, u, ws, limit, inter)
+    ops.stbl_act_quant_fp8(mid)
+    ops.stbl_gemv_mxfp4_batch([eo[j * dim:(j + 1) * dim] for j in range(topk)], [m[2] for m in mats],
+                              [mid[j * inter:(j + 1) * inter] for j in range(topk)], dim, inter)
+    sv = ops.slot_views(shared, ops.FP8_E8M0, dim, inter)
+    sg, su, smid, sout = f32(inter), f32(inter), f32(inter), f32(dim)
+    ops.stbl_gemv_fp8(sg, sv[0].reshape(-1), sv[1].reshape(-1), xq, inter, dim, 1)
+    ops.stbl_gemv_fp8(su, sv[2].reshape(-1), sv[3].reshape(-1), xq, inter, dim, 1)
+    ops.stbl_swiglu(smid, sg, su, 1.0, limit, inter)
+    ops.stbl_act_quant_fp8(smid)
+    ops.stbl_gemv_fp8(sout, sv[4].reshape(-1), sv[5].reshape(-1), smid, dim, inter, 1)
+    y = f32(dim)
+    for j in range(topk):
+        ops.stbl_axpy(y, eo[j * dim:(j + 1) * dim], 1.0, dim)
+    ops.stbl_axpy(y, sout, 1.0, dim)
+    ops.stbl_round_bf16(y)
+    got = np_(y)
+
+    want = oracle.moe_deq([[deq_parts(ops.FP4, p) for _, p in experts]], np.array([ws], np.float32),
+                          deq_parts(ops.FP8_E8M0, sparts), x.float().numpy(), limit=limit, official=True)[0]
+    assert bf16_ulps(got, want).max() <= 1
+    fused = np_(ops.moe_experts(x.to(gpu), [e[0] for e in experts] + [shared], [list(range(topk))], [ws], ops.FP4,
+                                dim, inter, shared=topk, limit=limit, official=True, shared_fmt=ops.FP8_E8M0))[0]
+    assert bf16_ulps(got, fused.astype(np.float64)).max() <= 1
