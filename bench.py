@@ -366,6 +366,83 @@ def compat_batch_workload(torch, rows, k, n, steps, warmup):
             "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS, "weight_sets": sets}
 
 
+def engine_abi_moe_workload(torch, steps, warmup):
+    """One token of the reference engine's MoE step issued through the drop-in ABI as
+    stbl/model.cu:508-592 issues it, at its V4.1 shapes (dim 5120, inter 2304, top-6 GGUF FP4 experts
+    from a >= 512 MB rotation, FP8 E8M0 shared expert, official numerics): act_quant of x, the gate/up
+    batch of 12, swiglu_batch, act_quant, the down batch of 6, the shared expert's three stbl_gemv_fp8
+    with its SwiGLU and act_quant, a zeroed accumulator, 7 axpys and round_bf16. The same step as
+    stbl_amd_moe_experts (moe_v41_allhit_t1) computes it in 3 fused launches."""
+    from stblarge_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    dim, inter, topk, limit = 5120, 2304, 6, 10.0
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    part = lambda rows, k: rows * (k // 32) * 17
+    ebytes = 2 * part(inter, dim) + part(dim, inter)
+    n_exp = max(topk + 1, math.ceil(ROTATE_BYTES / ebytes))
+    experts = []
+    for _ in range(n_exp):
+        gate, up = (torch.randint(0, 256, (part(inter, dim),), dtype=torch.uint8, device=dev, generator=g)
+                    for _ in range(2))
+        down = torch.randint(0, 256, (part(dim, inter),), dtype=torch.uint8, device=dev, generator=g)
+        for t in (gate, up, down):
+            t[::17] = 120
+        experts.append((gate, up, down))
+    sh = [torch.randint(0, 120, (r * k,), dtype=torch.uint8, device=dev, generator=g)
+          for r, k in ((inter, dim), (inter, dim), (dim, inter))]
+    shs = [torch.full((((r + 31) // 32) * (k // 32),), 120, dtype=torch.uint8, device=dev)
+           for r, k in ((inter, dim), (inter, dim), (dim, inter))]
+    x = torch.randn(dim, device=dev, generator=g).to(torch.bfloat16).float()
+    f32 = lambda n: torch.zeros(n, dtype=torch.float32, device=dev)
+    xq, gb, ub, mid, eo = f32(dim), f32(topk * inter), f32(topk * inter), f32(topk * inter), f32(topk * dim)
+    sg, su, smid, sout, y = f32(inter), f32(inter), f32(inter), f32(dim), f32(dim)
+    P = ctypes.c_void_p
+    arr = lambda ts: (P * len(ts))(*[t if isinstance(t, int) else t.data_ptr() for t in ts])
+    gu_y = arr([gb.data_ptr() + 4 * j * inter for j in range(topk)] + [ub.data_ptr() + 4 * j * inter for j in range(topk)])
+    gu_x = arr([xq] * (2 * topk))
+    d_y = arr([eo.data_ptr() + 4 * j * dim for j in range(topk)])
+    d_x = arr([mid.data_ptr() + 4 * j * inter for j in range(topk)])
+    ws = (ctypes.c_float * topk)(*[0.3, 0.2, 0.15, 0.15, 0.1, 0.1])
+    plans = []
+    for i in range(max(1, n_exp // topk)):
+        sel = [experts[(i * topk + j) % n_exp] for j in range(topk)]
+        plans.append((arr([e[0] for e in sel] + [e[1] for e in sel]), arr([e[2] for e in sel])))
+    lib = _lib.load()
+    st = ops._stream
+
+    def launch(i):
+        gu_w, d_w = plans[i]
+        s = st()
+        xq.copy_(x)
+        lib.stbl_act_quant_fp8(P(xq.data_ptr()), dim, s)
+        lib.stbl_gemv_mxfp4_batch(gu_y, gu_w, gu_x, 2 * topk, inter, dim, s)
+        lib.stbl_swiglu_batch(P(mid.data_ptr()), P(gb.data_ptr()), P(ub.data_ptr()), ws, topk, limit, inter, s)
+        lib.stbl_act_quant_fp8(P(mid.data_ptr()), topk * inter, s)
+        lib.stbl_gemv_mxfp4_batch(d_y, d_w, d_x, topk, dim, inter, s)
+        lib.stbl_gemv_fp8(P(sg.data_ptr()), P(sh[0].data_ptr()), P(shs[0].data_ptr()), P(xq.data_ptr()), inter, dim, 1, s)
+        lib.stbl_gemv_fp8(P(su.data_ptr()), P(sh[1].data_ptr()), P(shs[1].data_ptr()), P(xq.data_ptr()), inter, dim, 1, s)
+        lib.stbl_swiglu_batch(P(smid.data_ptr()), P(sg.data_ptr()), P(su.data_ptr()), (ctypes.c_float * 1)(1.0), 1,
+                              limit, inter, s)
+        lib.stbl_act_quant_fp8(P(smid.data_ptr()), inter, s)
+        lib.stbl_gemv_fp8(P(sout.data_ptr()), P(sh[2].data_ptr()), P(shs[2].data_ptr()), P(smid.data_ptr()), dim,
+                          inter, 1, s)
+        y.zero_()
+        for j in range(topk):
+            lib.stbl_axpy(P(y.data_ptr()), P(eo.data_ptr() + 4 * j * dim), 1.0, dim, s)
+        lib.stbl_axpy(P(y.data_ptr()), P(sout.data_ptr()), 1.0, dim, s)
+        lib.stbl_round_bf16(P(y.data_ptr()), dim, s)
+
+    launch(0)
+    _lib.check(None, "engine MoE step through the reference ABI")
+    ms, n = timed_steps(torch, launch, len(plans), steps, warmup)
+    alg = topk * ebytes + sum(t.numel() for t in sh + shs) + 4 * dim * 2
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"workload": "ref_abi_moe_step_v41_t1", "ms_per_step": ms, "steps": n, "tokens_per_s": 1 / (ms * 1e-3),
+            "launches_per_step": 20, "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS}
+
+
 def ref_method_workload(torch, kind, rows, k, group_rows=0, reps=200):
     """The reference ABI's GEMVs timed the way stbl/bench_gemv.py:18-28 times them, for a
     like-for-like comparison with that script's output: the same weight tensor every launch (so it
@@ -694,6 +771,10 @@ def main():
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.2f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
                   flush=True)
+        r = engine_abi_moe_workload(torch, max(200, args.steps // 4), args.warmup)
+        extra[r["workload"]] = r
+        print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.2f} us/step ({r['launches_per_step']} launches), "
+              f"{r['GB_s']:.0f} GB/s", file=sys.stderr, flush=True)
     if args.only in ("all", "refabi"):
         # stbl/bench_gemv.py's own method and rows (:95-107): cache-resident weights, eager launches
         for kind, rows, k, grp in (("mxfp4", 2304, 5120, 0), ("mxfp4", 5120, 2304, 0), ("fp8", 2304, 5120, 0),
