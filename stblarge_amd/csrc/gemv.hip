@@ -311,9 +311,14 @@ template <WFmt F, bool XF32, int M>
 static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int out_mode, hipStream_t st) {
     if constexpr (M > 2) {
         // 3-4 tokens: a lane's x chunk is M times larger, so 4 rows share it (measured at 2048x7168:
-        // 6.5 us against 10.7 us with 1 row per workgroup for FP4, 6.8 against 11.8 for FP8)
+        // 6.5 us against 10.7 us with 1 row per workgroup for FP4, 6.8 against 11.8 for FP8), except
+        // where a row spans one wave: there 2 rows keep twice the workgroups in flight (M = 4: FP4
+        // 7168x2048 7.33 -> 6.81 us, 4096x1024 5.70 -> 5.08; FP8 4096x1024 5.45 -> 4.40)
         if constexpr (XF32) return launch_r<F, XF32, M, 1>(jobs, njobs, rows, k, out_mode, st);
-        else return launch_r<F, XF32, M, 4>(jobs, njobs, rows, k, out_mode, st);
+        else {
+            if (k / WTraits<F>::CH <= 64) return launch_r<F, XF32, M, 2>(jobs, njobs, rows, k, out_mode, st);
+            return launch_r<F, XF32, M, 4>(jobs, njobs, rows, k, out_mode, st);
+        }
     }
     else if constexpr (XF32) {
         // fp32 activations (the reference ABI): a lane's x chunk is 4-8x its weight bytes per row, so
