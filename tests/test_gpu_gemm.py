@@ -1,10 +1,10 @@
 """GPU parity of the multi-token GEMM (scaled f8f6f4 MFMA) against the oracle.
 
 Oracle: act_quant(X, block, ue8m0) (ref/kernel.py:35-45) then Aq . Wdeq^T in double (ref/kernel.py:
-85-102). Bar: fp32 output within 1e-3 normwise (the reference's check() metric); the bf16 output is
-exactly our fp32 output rounded, and within 1e-3 + one bf16 half-step normwise. The MFMA's internal
+85-102). Bar: fp32 output within 1e-3 (max error over max output, the reference's check() metric); the bf16 output is
+exactly our fp32 output rounded, and within 1e-3 + one bf16 half-step by the same metric. The MFMA's internal
 accumulation is not IEEE fp32 round-per-add (about 1e-4 relative on a 128-term step, measured), so
-outputs near zero can be many bf16 steps from the oracle while the normwise error stays ~1e-4; an
+outputs near zero can be many bf16 steps from the oracle while the max-over-max error stays ~1e-4; an
 elementwise ulp bar does not apply here.
 """
 

@@ -1,8 +1,8 @@
 """GPU parity of the quantized GEMVs against the oracle (ref/kernel.py:85-102, stbl/kernels.cu:92-191).
 
-The bar: fp32 outputs within 1e-3 normwise relative error of the oracle's exact-product double sum
-(the GPU sums in a different order, so a few ulp of fp32); bf16 outputs at most one bf16 step from
-bf16(oracle), with flips rare. The weights are seeded N(0, 0.02) quantized by the GPU quantizers,
+The bar: fp32 outputs within 1e-3 (max error over max output, the reference's check() metric) of the
+oracle's exact-product double sum (the GPU sums in a different order, so a few ulp of fp32); bf16
+outputs at most one bf16 step from bf16(oracle), with flips rare. The weights are seeded N(0, 0.02) quantized by the GPU quantizers,
 which test_gpu_quant.py pins bit-exactly to the oracle's.
 """
 

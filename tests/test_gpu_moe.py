@@ -3,7 +3,7 @@
 Oracle: stbl_oracle.c's expert FFN / MoE composition (stbl/model.cu:505-592), router
 (stbl/model.cu:444-451, sigmoid or the engine's sqrt-softplus) and oracle.lru_simulate
 (stbl/model.cu:347-422, 497-507).
-Bar: the unrounded down product within 1e-3 normwise of the oracle; bf16 outputs at most one bf16
+Bar: the unrounded down product within 1e-3 of the oracle (max error over max output); bf16 outputs at most one bf16
 step from the oracle's, flips rare (an intermediate bf16 rounding of g or u may flip when the two
 sums differ in their last fp32 bits). Router ids exact; route weights within a few fp32 ulps (the
 sigmoid's exp is a library routine on both sides).

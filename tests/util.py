@@ -41,12 +41,13 @@ def bf16_ulps(got_bf16, want_f64):
 
 
 def assert_gemv(got_f32, got_bf16, want, tol=1e-3):
-    """fp32 output within `tol` (normwise), bf16 output at most one bf16 step from bf16(want).
+    """fp32 output within `tol` (max error over max output), bf16 output at most one bf16 step from
+    bf16(want).
 
     The step check skips outputs below 2^-16 of the largest: those are sums that cancel to ~1e-5 of
     their terms, whose last bf16 digits fp32 accumulation in any order cannot resolve (a row of 5120
     random FP4 products summing to 5.9e-5 from an absolute sum of 608 came out 3.9e-7 from exact,
-    two bf16 steps). The normwise bound above still covers them."""
+    two bf16 steps). The max-over-max bound above still covers them."""
     e = rel_err(got_f32, want)
     assert e <= tol, f"relative error {e:.3e} > {tol}"
     if got_bf16 is not None:
