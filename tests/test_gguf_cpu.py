@@ -193,3 +193,57 @@ def test_cache_create_gguf_rejects_bad_files(tmp_path):
     gguf.write(p, t)
     assert not lib.stbl_amd_cache_create_gguf(4, str(p).encode(), 0, 1, 2, 1)
     assert "shape differs" in _lib.last_error()[1]
+
+
+_MUTATE = r'''
+import struct, sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from stblarge_amd import gguf
+raw = open(sys.argv[2], "rb").read()
+head = int(sys.argv[3])
+rng = np.random.default_rng(int(sys.argv[4]))
+path = sys.argv[2] + ".m"
+opened = refused = 0
+for it in range(int(sys.argv[5])):
+    b = bytearray(raw)
+    kind = it % 4
+    if kind == 0:  # random bytes in the header
+        for _ in range(rng.integers(1, 8)):
+            b[rng.integers(0, head)] = rng.integers(0, 256)
+    elif kind == 1:  # a count, length, dim or offset field set to an extreme value
+        at = int(rng.integers(0, head - 8)) & ~7
+        b[at:at + 8] = struct.pack("<Q", [0, 1, 2**31, 2**32 - 1, 2**63, 2**64 - 1][int(rng.integers(0, 6))])
+    elif kind == 2:  # truncated anywhere
+        b = b[:rng.integers(0, len(b))]
+    else:  # a header region repeated (lengths now point into the wrong fields)
+        s = int(rng.integers(0, head)); e = int(rng.integers(s, head))
+        b = b[:e] + b[s:e] + b[e:]
+    open(path, "wb").write(bytes(b))
+    try:
+        with gguf.GgufFile(path) as g:
+            g.tensor("a.f32"); g.tensor("blk.0.ffn_gate_exps.weight"); g.u32("general.alignment"); g.uints("test.ids")
+        opened += 1
+    except RuntimeError:
+        refused += 1
+print(opened, refused)
+'''
+
+
+def test_reader_survives_mutated_headers(tmp_path):
+    # 400 corrupted copies of the hand-assembled file: each either opens or is refused with an error;
+    # none may crash the process (run in a child, so a crash fails this test instead of the session)
+    import os
+    import subprocess
+    import sys
+
+    p = tmp_path / "hand.gguf"
+    base, _, _ = _hand_file(p)
+    script = tmp_path / "mutate.py"
+    script.write_text(_MUTATE)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, str(script), root, str(p), str(base), "5", "400"], capture_output=True,
+                       text=True, timeout=300)
+    assert r.returncode == 0, f"reader crashed (exit {r.returncode}): {r.stderr[-2000:]}"
+    opened, refused = map(int, r.stdout.split()[-2:])
+    assert opened + refused == 400 and refused > 0
