@@ -73,3 +73,36 @@ def test_check_raises():
     lib = _lib.load()
     with pytest.raises(_lib.StblError):
         _lib.check(lib.stbl_amd_quant_fp4(None, None, None, 1, 32, None), "quant_fp4")
+
+
+def _zero_args(argtypes):
+    import ctypes as C
+    out = []
+    for t in argtypes:
+        if t in (C.c_int, C.c_int64, C.c_uint64):
+            out.append(0)
+        elif t is C.c_float:
+            out.append(0.0)
+        else:
+            out.append(None)  # any pointer, char*, stream
+    return out
+
+
+_NO_ERROR_ON_ZERO = {"stbl_amd_version", "stbl_amd_last_error", "stbl_amd_expert_layout", "stbl_amd_moe_work_bytes",
+                     "stbl_amd_gemm_work_bytes", "stbl_amd_cache_destroy", "stbl_amd_gguf_close",
+                     "stbl_amd_cache_peek"}
+
+
+@pytest.mark.parametrize("name", sorted(n for n in _lib.SIGNATURES if n not in _NO_ERROR_ON_ZERO))
+def test_every_entry_point_rejects_null_and_zero_arguments(name):
+    # null pointers and zero sizes: each entry point refuses before touching the device, records why
+    # (readable through stbl_amd_last_error) and returns a negative status or NULL; void entry points
+    # of the reference ABI only record it
+    lib = _lib.load()
+    _lib.last_error()  # clear
+    ret, argtypes = _lib.SIGNATURES[name]
+    r = getattr(lib, name)(*_zero_args(argtypes))
+    code, msg = _lib.last_error()
+    if ret is not None and r is not None:
+        assert (r < 0) if isinstance(r, int) else not r, f"{name} returned {r}"
+    assert code != 0 and msg, f"{name} recorded no error"
