@@ -238,3 +238,43 @@ def test_stbl_gemv_bf16(gpu, rows, k, round_out, group_rows):
         assert np.max(np.abs(got - want)) <= np.max(np.abs(want)) * (1e-5 + 2.0 ** -8)
     else:
         assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
+
+
+def test_gemv_from_concurrent_threads_and_streams(gpu):
+    # four host threads, each on its own stream, run FP4 and FP8 GEMVs of their own matrices at once;
+    # every result is bit-identical to the same call made alone (the entry points keep no shared state
+    # beyond a per-device CU count and per-thread error slots)
+    import threading
+
+    rows, k = 2048, 7168
+    jobs = []
+    for i in range(4):
+        c4, s4, d4, e4 = _fp4(gpu, rows, k, seed=40 + i)
+        c8, s8, d8, e8 = _fp8(gpu, rows, k, seed=50 + i)
+        jobs.append((d4, e4, d8, e8, data.activation(2, k, seed=60 + i).to(gpu)))
+    alone = [(ops.gemv_fp4(d4, e4, x), ops.gemv_fp8(d8, e8, x)) for d4, e4, d8, e8, x in jobs]
+    torch.cuda.synchronize()
+    got = [None] * 4
+    errors = []
+
+    def work(i):
+        try:
+            d4, e4, d8, e8, x = jobs[i]
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                out = []
+                for _ in range(20):
+                    out = [ops.gemv_fp4(d4, e4, x), ops.gemv_fp8(d8, e8, x)]
+            s.synchronize()
+            got[i] = out
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    ts = [threading.Thread(target=work, args=(i,)) for i in range(4)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors, errors
+    for (a4, a8), (g4, g8) in zip(alone, got):
+        assert torch.equal(a4, g4) and torch.equal(a8, g8)
