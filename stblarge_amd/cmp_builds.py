@@ -63,6 +63,20 @@ def _cases(dev, seed):
             lib.stbl_gemv_mxfp4(_p(y), _p(w), _p(x), rows, k, st)
             return [y]
         cases.append((f"stbl_gemv_mxfp4 {rows}x{k}", mx))
+    # the engine's expert batches (stbl/model.cu:536-539): 12 gate/up matrices, then 6 down
+    for rows, k, n in ((2304, 5120, 12), (5120, 2304, 6)):
+        ws = [torch.randint(0, 256, (rows, k // 32 * 17), dtype=torch.uint8, device=dev, generator=g) for _ in range(n)]
+        for w in ws:
+            w[:, ::17] = torch.randint(110, 130, (rows, k // 32), dtype=torch.uint8, device=dev, generator=g)
+        xs = [bf(k).float() for _ in range(n)]
+
+        def mxb(lib, ws=ws, xs=xs, rows=rows, k=k, n=n):
+            ys = [torch.empty(rows, device=dev) for _ in range(n)]
+            arr = P * n
+            lib.stbl_gemv_mxfp4_batch(arr(*[y.data_ptr() for y in ys]), arr(*[w.data_ptr() for w in ws]),
+                                      arr(*[x.data_ptr() for x in xs]), n, rows, k, st)
+            return ys
+        cases.append((f"stbl_gemv_mxfp4_batch {n}x {rows}x{k}", mxb))
     for rows, k in ((32768, 1280), (5120, 8192), (2304, 5120)):
         w = torch.randint(0, 256, (rows, k), dtype=torch.uint8, device=dev, generator=g)
         w[(w & 0x7f) == 0x7f] = 0
