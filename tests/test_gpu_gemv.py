@@ -161,9 +161,11 @@ def test_stbl_gemv_mxfp4_batch(gpu, rows, k, n):
 
 
 @pytest.mark.parametrize("fmt", [0, 1])
-def test_gemv_batch(gpu, fmt):
-    # 16 same-shape GEMVs in one launch (stbl_gemv_mxfp4_batch's batching, v2 formats), M = 2
-    rows, k, n, m = 256, 1024, 16, 2
+@pytest.mark.parametrize("rows,k,n", [(256, 1024, 16), (2048, 7168, 3)])
+def test_gemv_batch(gpu, fmt, rows, k, n):
+    # same-shape GEMVs in one launch (stbl_gemv_mxfp4_batch's batching, v2 formats), M = 2: 16 small
+    # matrices (2-row tiles), and 3 large ones (4-row tiles, FP4 scales as dwords from each matrix)
+    m = 2
     q = oracle.quant_fp4 if fmt == 0 else oracle.quant_fp8_b128
     ref = oracle.gemv_fp4 if fmt == 0 else oracle.gemv_fp8_b128
     cs, ss, xs, wants = [], [], [], []
