@@ -391,3 +391,21 @@ def test_reference_abi_moe_composition(gpu):
     fused = np_(ops.moe_experts(x.to(gpu), [e[0] for e in experts] + [shared], [list(range(topk))], [ws], ops.FP4,
                                 dim, inter, shared=topk, limit=limit, official=True, shared_fmt=ops.FP8_E8M0))[0]
     assert bf16_ulps(got, fused.astype(np.float64)).max() <= 1
+
+
+def test_moe_experts_byte_scales_fallback(gpu):
+    # dims whose FP4 scale rows are not a multiple of 4 bytes (160 / 32 = 5, 96 / 32 = 3): the
+    # several-expert launches (4 and 8 rows per workgroup) load scales byte by byte instead of as dwords
+    dim, inter, topk, n = 160, 96, 3, 5
+    experts = [make_expert(ops.FP4, dim, inter, seed=400 + 3 * i, gpu=gpu) for i in range(n)]
+    rng = np.random.default_rng(44)
+    for t in (1, 3):
+        pick = [list(rng.choice(n - 1, size=topk, replace=False)) for _ in range(t)]
+        w = (rng.random((t, topk)) / topk).astype(np.float32)
+        x = data.activation(t, dim, seed=45 + t)
+        y = np_(ops.moe_experts(x.to(gpu), [e[0] for e in experts], pick, w.tolist(), ops.FP4, dim, inter,
+                                shared=n - 1))
+        packed = [np.concatenate([p.ravel() for p in e[1]]) for e in experts]
+        want = oracle.moe_fp4([[packed[i] for i in row] for row in pick], w, packed[n - 1], dim, inter,
+                              x.float().numpy())
+        assert bf16_ulps(y, want).max() <= 1
