@@ -37,8 +37,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="all",
-                    help="fp4 (headline only) | gemv | batch | ffn | gemm | moe | moeallhit | refabi | file | "
-                         "filestack | all")
+                    help="fp4 (headline and its floors) | gemv | batch | ffn | gemm | moe | moeallhit | refabi | "
+                         "file | filestack | floor | all")
     ap.add_argument("--moe-steps", type=int, default=200)
     ap.add_argument("--moe-warmup", type=int, default=1000)
     ap.add_argument("--eager", action="store_true", help="also time launches issued one by one from Python")
@@ -63,7 +63,9 @@ def timed_steps(torch, launch, copies, steps, warmup, use_graph=True):
             with torch.cuda.graph(graph, stream=stream):
                 for i in range(copies):
                     launch(i)
-            reps = max(1, round(steps / copies))
+            # at least 10 replays of the rotation are timed, whatever `steps` asks (the launches
+            # actually timed are returned and reported)
+            reps = max(10, round(steps / copies))
             wreps = max(1, round(warmup / copies))
             for _ in range(wreps):
                 graph.replay()
@@ -658,6 +660,40 @@ def file_stack_workload(torch, guess_quality, n_layers=4, n_experts=24, topk=6, 
             "demand_GB_read": info["bytes_read"] / 1e9, "prefetch": pst, "direct": bool(info["direct"])}
 
 
+def read_floor_workload(torch, nbytes, steps, warmup):
+    """The bare streaming read of nbytes in one launch (stbl_amd_read_floor), timed exactly as the
+    GEMV rows are: graph replays of launches that each read a different slice of a >= 512 MB buffer
+    (so the 256 MB Infinity Cache cannot serve repeats), events on the launch stream."""
+    from stblarge_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    span = (nbytes + 4095) // 4096 * 4096
+    copies = max(2, math.ceil(ROTATE_BYTES / span))
+    buf = torch.randint(0, 256, (copies * span,), dtype=torch.uint8, device=dev)
+    sink = torch.empty(int(_lib.load().stbl_amd_read_floor_sink_words(nbytes)), dtype=torch.int32, device=dev)
+    lib = _lib.load()
+
+    def launch(i):
+        _lib.check(lib.stbl_amd_read_floor(ctypes.c_void_p(buf.data_ptr() + i * span), nbytes, ops._ptr(sink),
+                                           ops._stream()), "read_floor")
+
+    ms, n = timed_steps(torch, launch, copies, steps, warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del buf
+    return {"workload": f"read_floor_{nbytes}B", "bytes": nbytes, "ms_per_step": ms, "steps": n, "GB_s": gbs,
+            "frac_hbm_peak": gbs / PEAK_HBM_GBS}
+
+
+def attach_floor(row, floors):
+    """Adds the row's fraction of the bare-read floor for its byte count (the same bytes in one
+    launch, timed the same way) next to its fraction of peak."""
+    f = floors.get(int(row["alg_bytes"]))
+    if f:
+        row["read_floor_GB_s"] = f["GB_s"]
+        row["frac_of_read_floor"] = row["GB_s"] / f["GB_s"]
+    return row
+
+
 def measured_traffic():
     """HBM bytes per launch of the headline kernel from the committed rocprofv3 counter summary
     (profiles/gemv_fp4_2048x7168_traffic.md, line `traffic_bytes_per_launch: N`), or None."""
@@ -671,12 +707,54 @@ def measured_traffic():
     return None
 
 
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
 def cpu_baseline(seconds):
-    """The oracle's scalar C GEMV (oracle/stbl_oracle.c orc_gemv_fp4) on the headline workload's
-    shape, one thread, repeated for about `seconds`."""
-    import numpy as np
+    """ref/kernel.py's own CPU method for the headline workload (fp4_gemm, ref/kernel.py:94-102,
+    restated in oracle.fp4_gemm_torch): per call the FP4 codes and E8M0 scales are dequantized into
+    an fp32 [2048 x 7168] matrix and x @ W^T runs in fp32 on every core this process may use, with a
+    bf16 result. Repeated for about `seconds`; algorithmic bytes per call as for the GPU row."""
     import torch
 
+    import oracle
+    from stblarge_amd import data
+
+    rows, k = 2048, 7168
+    cores = len(os.sched_getaffinity(0))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    w = data.weight(rows, k, seed=1)
+    codes, scales = oracle.quant_fp4(w.numpy())
+    codes, scales = torch.from_numpy(codes), torch.from_numpy(scales)
+    x = data.activation(1, k, seed=2)
+    alg = data.algorithmic_bytes_fp4(rows, k, 1)
+    for _ in range(3):  # warm
+        oracle.fp4_gemm_torch(x, codes, scales)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.fp4_gemm_torch(x, codes, scales)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    torch.set_num_threads(prev)
+    return {"value": alg * reps / el / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{reps} x fp4 GEMV 2048x7168 m=1 in {el:.1f} s by ref/kernel.py's method (torch CPU: dequant to "
+                      f"fp32, x @ W^T, bf16 out; oracle.fp4_gemm_torch) on {cores} threads of {_cpu_model()} "
+                      f"(os.cpu_count() {os.cpu_count()}); {el / reps * 1e3:.2f} ms per GEMV"}
+
+
+def cpu_scalar_oracle(seconds):
+    """The oracle's scalar C GEMV (oracle/stbl_oracle.c orc_gemv_fp4, one thread, fp64 accumulation)
+    on the headline shape, repeated for about `seconds`: a second CPU row."""
     import oracle
     from stblarge_amd import data
 
@@ -693,18 +771,9 @@ def cpu_baseline(seconds):
         el = time.perf_counter() - t0
         if el >= seconds:
             break
-    del torch
-    model = "unknown CPU"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": alg * reps / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} x fp4 GEMV 2048x7168 m=1 (oracle orc_gemv_fp4, scalar C, fp64 accumulate) in {el:.1f} s "
-                      f"on one core of {model}"}
+    return {"workload": "cpu_scalar_oracle_fp4_gemv_2048x7168", "GB_s": alg * reps / el / 1e9, "cores": 1,
+            "ms_per_gemv": el / reps * 1e3,
+            "sample": f"{reps} x orc_gemv_fp4 (scalar C, fp64 accumulate) in {el:.1f} s on one core of {_cpu_model()}"}
 
 
 def main():
@@ -814,13 +883,34 @@ def main():
         r = gemv_workload(torch, "fp4", 2048, 7168, 1, args.steps, args.warmup, use_graph=False)
         extra["fp4_gemv_2048x7168_m1_eager"] = r
         print(f"# eager launches: {r['ms_per_step'] * 1e3:.3f} us/step", file=sys.stderr, flush=True)
+    if args.only in ("all", "fp4", "gemv", "batch", "ffn", "floor"):
+        # bare-read floors at the single-launch rows' byte counts: FP4 / FP8 GEMV, FP4 / FP8 expert
+        # FFN, 16 FP4 / FP8 GEMVs per launch
+        floors = {}
+        for nbytes in (7817216, 14702080, 23425024, 44079616, 125075456, 235233280):
+            r = read_floor_workload(torch, nbytes, args.steps, args.warmup)
+            floors[nbytes] = r
+            extra[r["workload"]] = r
+            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s "
+                  f"({100 * r['frac_hbm_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
+        for row in [head] + list(extra.values()):
+            if "alg_bytes" in row and not row["workload"].startswith("read_floor"):
+                attach_floor(row, floors)
+        if "frac_of_read_floor" in head:
+            print(f"# headline: {100 * head['frac_of_read_floor']:.1f}% of the bare read of its bytes",
+                  file=sys.stderr, flush=True)
     if args.copy_calib:
         a = torch.empty(64 << 20, dtype=torch.uint8, device="cuda:0")
         b = torch.empty_like(a)
         for _ in range(5):
             b.copy_(a)
         torch.cuda.synchronize()
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args.cpu_seconds)
+        extra["cpu_scalar_oracle"] = cpu_scalar_oracle(min(args.cpu_seconds, 5.0))
+        print(f"# cpu baseline: {cpu['value']:.2f} GB/s ({cpu['sample']}); scalar oracle "
+              f"{extra['cpu_scalar_oracle']['GB_s']:.2f} GB/s", file=sys.stderr, flush=True)
     gbs = head["GB_s"]
     line = {
         "metric": METRIC,
@@ -838,7 +928,8 @@ def main():
         "config": {"workload": head["workload"], "rows": 2048, "k": 7168, "m": 1,
                    "weight_copies": head["weight_copies"], "rotation_MB": round(head["weight_copies"] * 7.8, 1)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic()},
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
+                     "frac_of_read_floor": head.get("frac_of_read_floor")},
         "cpu_baseline": cpu,
         "extra": extra,
     }

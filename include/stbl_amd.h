@@ -174,6 +174,17 @@ int stbl_amd_moe_experts(int fmt, void *y, const void *x, int t, int dim, int in
                          int n_slots, const int *pick, const float *weights, int topk, int shared, int shared_fmt,
                          float limit, int official, int y_f32, void *work, hipStream_t st);
 
+/* stbl_amd_moe_experts split in two calls around an expert cache's refill wait, as the reference
+ * queues its cached experts and the shared expert before reading the misses and runs the missed
+ * experts after (stbl/model.cu:541-549, 588). slot_ready: HOST array of n_slots flags (the `ready`
+ * output of stbl_amd_cache_lookup_begin; 1 for a resident shared slot). phase 1 runs the experts of
+ * ready slots, phase 2 the others and the ordered combine; both calls take the same arguments and
+ * work, and their result is bit-identical to stbl_amd_moe_experts. phase 0 = stbl_amd_moe_experts. */
+int stbl_amd_moe_experts_phase(int fmt, void *y, const void *x, int t, int dim, int inter, const void *const *slots,
+                               int n_slots, const int *pick, const float *weights, int topk, int shared,
+                               int shared_fmt, float limit, int official, int y_f32, const int *slot_ready, int phase,
+                               void *work, hipStream_t st);
+
 /* Scratch bytes for stbl_amd_moe_experts on t tokens. */
 uint64_t stbl_amd_moe_work_bytes(int t, int topk, int dim, int inter);
 
@@ -268,6 +279,28 @@ void stbl_amd_cache_destroy(void *cache);
 int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **slot_ptrs, int *hit,
                           hipStream_t compute);
 
+/* stbl_amd_cache_lookup in two calls (stbl/model.cu:497-553, the reference's expert() lookups, then
+ * read_pieces after the cached experts' kernels are queued). _begin maps every id as the lookup
+ * does and queues pool refills on the copy stream; ready (HOST, optional, n flags) is 1 where
+ * `compute` may read the slot at once and 0 where it must wait for _end (a refill, a file read, a
+ * prefetch landed or still being read). _end reads the file misses (blocking the host), waits for
+ * routed prefetches still being read, and makes `compute` wait for every copy and repack. Every
+ * _begin must be followed by _end before the next lookup or prefetch on the cache. _begin returns
+ * the number of misses or a negative hipError_t; _end returns 0 or a negative hipError_t (then the
+ * experts not read stay unmapped and their slots must not be read). */
+int stbl_amd_cache_lookup_begin(void *cache, const int *ids, int n, int layer, void **slot_ptrs, int *hit, int *ready,
+                                hipStream_t compute);
+int stbl_amd_cache_lookup_end(void *cache, hipStream_t compute);
+
+/* Notes the guesses for `layer` (HOST ids, best first: the next layer's router scored on this
+ * layer's input, the reference's STBL_LOOKAHEAD, stbl/model.cu:432-435, 461-474) and whether each is
+ * uncached now; the lookup of `layer` then updates the lookahead counters. */
+int stbl_amd_cache_note_guesses(void *cache, const int *ids, int n, int layer);
+
+/* out[0..3] = guesses uncached when noted, of which routed; routed experts not mapped at their
+ * lookup, of which guessed (stbl_lookahead, stbl/model.cu:452-460, 1107-1109). */
+int stbl_amd_cache_lookahead(void *cache, uint64_t *out);
+
 /* Marks the slots of the last lookup as used by the work queued so far on `compute`; a later refill
  * of one of them waits for that work. */
 int stbl_amd_cache_mark_used(void *cache, hipStream_t compute);
@@ -303,6 +336,15 @@ int stbl_amd_gguf_f32(void *g, const char *key, float *v);
 /* A u32 or u64 array (stbl/gguf.h:31 uints): up to cap values into out (may be NULL); returns the
  * array's length, or -hipErrorNotFound when the key is absent or holds another type. */
 int64_t stbl_amd_gguf_uints(void *g, const char *key, uint64_t *out, int64_t cap);
+
+/* ---- v2: measurement ------------------------------------------------------------------------------------ */
+
+/* A bare streaming read of `bytes` (a multiple of 16) from 16-byte aligned device memory in one
+ * launch: the floor for one-launch kernels that read as many bytes. sink: device buffer of
+ * stbl_amd_read_floor_sink_words(bytes) 32-bit words (one per wave). No reference counterpart (the
+ * reference calibrates with a 64 MiB device copy, stbl/bench_gemv.py:58-61). */
+int stbl_amd_read_floor(const void *src, uint64_t bytes, void *sink, hipStream_t st);
+uint64_t stbl_amd_read_floor_sink_words(uint64_t bytes);
 
 /* ---- library ------------------------------------------------------------------------------------------ */
 

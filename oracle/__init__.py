@@ -344,6 +344,33 @@ def moe_deq(experts, weights, shared, x, limit=0.0, official=False):
     return y
 
 
+# ---- ref/kernel.py's own CPU method (torch), the CPU baseline of the measurements -------------------
+
+_FP4_LUT = None
+
+
+def fp4_gemm_torch(x, codes, scales):
+    """fp4_gemm of ref/kernel.py:94-102 as the reference runs it on the CPU: every call dequantizes
+    the whole weight into one fp32 matrix (each code's e2m1 value, low nibble first, times
+    2^(scale - 127) per 32 along K) and multiplies x [m][k] (bf16 values) by its transpose in fp32
+    with torch's CPU matmul on torch's thread pool; the result is rounded to bf16. codes uint8
+    [n][k/2], scales uint8 [n][k/32] (torch tensors). Used as the timed CPU baseline; its bits
+    depend on torch's summation order, so parity checks use the C restatement instead."""
+    import torch
+
+    global _FP4_LUT
+    if _FP4_LUT is None:
+        mags = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+        _FP4_LUT = torch.tensor(mags + [-v for v in mags], dtype=torch.float32)
+    n, k = codes.shape[0], codes.shape[1] * 2
+    w = torch.empty((n, k // 2, 2), dtype=torch.float32)
+    w[..., 0] = _FP4_LUT[(codes & 15).long()]
+    w[..., 1] = _FP4_LUT[(codes >> 4).long()]
+    scale = torch.ldexp(torch.ones(1), scales.to(torch.int32) - 127)
+    w = (w.view(n, k // 32, 32) * scale.view(n, k // 32, 1)).view(n, k)
+    return (x.float().view(-1, k) @ w.t()).to(torch.bfloat16)
+
+
 # ---- expert LRU bookkeeping (stbl/model.cu:347-422, 497-507) ---------------------------------------
 
 def lru_simulate(steps, slots):

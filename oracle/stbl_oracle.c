@@ -335,7 +335,8 @@ float orc_route_score(float l, int score_fn) {
 
 /* logits [t][e]. score = orc_route_score(l); top-k by score + bias (bias may be NULL), ties to the
  * lower id; weight_i = score_i / (sum of the top-k scores in top-k order + 1e-20) * route_scale
- * (stbl/model.cu:444-451, 528-530). */
+ * (stbl/model.cu:444-451, 528-530). A NaN key ranks below every number (the reference's host sort
+ * leaves NaN undefined; this is the rule the device router follows). */
 void orc_route(const float *logits, const float *bias, int t, int e, int topk, float route_scale, int score_fn,
                float *scores, int *ids, float *weights) {
     for (int i = 0; i < t; i++) {
@@ -349,7 +350,8 @@ void orc_route(const float *logits, const float *bias, int t, int e, int topk, f
                 int used = 0;
                 for (int q = 0; q < p; q++) used |= id[q] == j;
                 if (used) continue;
-                const float v = sc[j] + (bias ? bias[j] : 0.f);
+                float v = sc[j] + (bias ? bias[j] : 0.f);
+                if (v != v) v = -INFINITY; /* a NaN key ranks last (then the lower id wins) */
                 if (best < 0 || v > bv) best = j, bv = v;
             }
             id[p] = best;

@@ -49,6 +49,7 @@ SIGNATURES = {
     "stbl_amd_expert_layout": (U64, [I, I, I, PU64]),
     "stbl_amd_expert_ffn": (I, [I, P, P, P, I, I, I, F, F, I, I, P, P]),
     "stbl_amd_moe_experts": (I, [I, P, P, I, I, I, PP, I, PI, PF, I, I, I, F, I, I, P, P]),
+    "stbl_amd_moe_experts_phase": (I, [I, P, P, I, I, I, PP, I, PI, PF, I, I, I, F, I, I, PI, I, P, P]),
     "stbl_amd_moe_work_bytes": (U64, [I, I, I, I]),
     "stbl_amd_route": (I, [P, P, I, I, I, F, I, P, P, P, P]),
     "stbl_amd_gemm": (I, [I, P, P, P, P, I, I, I, I, I, P, P]),
@@ -70,10 +71,16 @@ SIGNATURES = {
     "stbl_amd_gguf_f32": (I, [P, ctypes.c_char_p, PF]),
     "stbl_amd_gguf_uints": (ctypes.c_int64, [P, ctypes.c_char_p, PU64, ctypes.c_int64]),
     "stbl_amd_cache_lookup": (I, [P, PI, I, I, PP, PI, P]),
+    "stbl_amd_cache_lookup_begin": (I, [P, PI, I, I, PP, PI, PI, P]),
+    "stbl_amd_cache_lookup_end": (I, [P, P]),
+    "stbl_amd_cache_note_guesses": (I, [P, PI, I, I]),
+    "stbl_amd_cache_lookahead": (I, [P, PU64]),
     "stbl_amd_cache_mark_used": (I, [P, P]),
     "stbl_amd_cache_stats": (I, [P, PU64]),
     "stbl_amd_cache_peek": (P, [P, I, I]),
     "stbl_amd_cache_fail_refill_after": (I, [P, I]),
+    "stbl_amd_read_floor": (I, [P, U64, P, P]),
+    "stbl_amd_read_floor_sink_words": (U64, [U64]),
     "stbl_amd_last_error": (I, [ctypes.c_char_p, I]),
     "stbl_amd_version": (I, []),
 }

@@ -12,7 +12,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libstbl_amd.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["abi.hip", "quant.hip", "gemv.hip", "moe.hip", "gemm.hip", "expert_cache.hip", "gguf.hip"]
+SOURCES = ["abi.hip", "quant.hip", "gemv.hip", "moe.hip", "gemm.hip", "expert_cache.hip", "gguf.hip", "calib.hip"]
 
 FLAGS = [
     "--offload-arch=gfx950",

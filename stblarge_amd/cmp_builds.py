@@ -7,7 +7,9 @@ moves work between lanes, waves or workgroups must leave every output bit unchan
                                                          # built from a temporary worktree
 
 Both builds must report the same stbl_amd_version() (the same ABI). Runs on one GPU in seconds; the
-inputs are seeded, random and bf16-valued where the path needs it. Prints each differing case and
+inputs are seeded, random and bf16-valued where the path needs it. Outputs start as NaN (ids as -1),
+and a case that either build rejects (a recorded stbl_amd_last_error, or a v2 status other than 0)
+counts as a difference, so two rejected calls never compare equal. Prints each differing case and
 exits 1 if any output differs.
 """
 
@@ -42,6 +44,13 @@ def _load(path):
     return lib
 
 
+def _out(shape, dev, dtype=torch.float32):
+    """An output buffer filled with a sentinel (NaN, or -1 for integers) before the call."""
+    if dtype.is_floating_point:
+        return torch.full(shape if isinstance(shape, tuple) else (shape,), float("nan"), dtype=dtype, device=dev)
+    return torch.full(shape if isinstance(shape, tuple) else (shape,), -1, dtype=dtype, device=dev)
+
+
 def _cases(dev, seed):
     """(name, function(lib) -> list of output tensors) for one seed."""
     g = torch.Generator(device=dev)
@@ -59,7 +68,7 @@ def _cases(dev, seed):
         x = bf(k).float()
 
         def mx(lib, w=w, x=x, rows=rows, k=k):
-            y = torch.empty(rows, device=dev)
+            y = _out(rows, dev)
             lib.stbl_gemv_mxfp4(_p(y), _p(w), _p(x), rows, k, st)
             return [y]
         cases.append((f"stbl_gemv_mxfp4 {rows}x{k}", mx))
@@ -71,7 +80,7 @@ def _cases(dev, seed):
         xs = [bf(k).float() for _ in range(n)]
 
         def mxb(lib, ws=ws, xs=xs, rows=rows, k=k, n=n):
-            ys = [torch.empty(rows, device=dev) for _ in range(n)]
+            ys = [_out(rows, dev) for _ in range(n)]
             arr = P * n
             lib.stbl_gemv_mxfp4_batch(arr(*[y.data_ptr() for y in ys]), arr(*[w.data_ptr() for w in ws]),
                                       arr(*[x.data_ptr() for x in xs]), n, rows, k, st)
@@ -84,7 +93,7 @@ def _cases(dev, seed):
         x = bf(k).float()
 
         def f8(lib, w=w, sc=sc, x=x, rows=rows, k=k):
-            y = torch.empty(rows, device=dev)
+            y = _out(rows, dev)
             lib.stbl_gemv_fp8(_p(y), _p(w), _p(sc), _p(x), rows, k, seed % 2, st)
             return [y]
         cases.append((f"stbl_gemv_fp8 {rows}x{k}", f8))
@@ -92,7 +101,7 @@ def _cases(dev, seed):
     xb = bf(2 * 5120).float()
 
     def b16(lib):
-        y, z = torch.empty(4096, device=dev), torch.empty(4096, device=dev)
+        y, z = _out(4096, dev), _out(4096, dev)
         lib.stbl_gemv_bf16(_p(y), _p(wb), _p(xb), 4096, 5120, 1, 0, st)
         lib.stbl_gemv_bf16(_p(z), _p(wb), _p(xb), 4096, 5120, 0, 2048, st)
         return [y, z]
@@ -101,7 +110,7 @@ def _cases(dev, seed):
     xf = torch.randn(5120, device=dev, generator=g)
 
     def f32(lib):
-        y = torch.empty(256, device=dev)
+        y = _out(256, dev)
         lib.stbl_gemv_f32(_p(y), _p(wf), _p(xf), 256, 5120, 0, st)
         return [y]
     cases.append(("stbl_gemv_f32 256x5120", f32))
@@ -114,7 +123,7 @@ def _cases(dev, seed):
             x = bf((m, k))
 
             def v2(lib, fmt=fmt, codes=codes, scales=scales, x=x, m=m, rows=rows, k=k):
-                y = torch.empty((m, rows), device=dev)
+                y = _out((m, rows), dev)
                 fn = lib.stbl_amd_gemv_fp4 if fmt == ops.FP4 else lib.stbl_amd_gemv_fp8
                 assert fn(_p(y), _p(codes), _p(scales), _p(x), m, rows, k, 1, st) == 0
                 return [y]
@@ -123,7 +132,7 @@ def _cases(dev, seed):
     xs = [bf((1, 2048)) for _ in range(16)]
 
     def batch(lib):
-        ys = [torch.empty(7168, device=dev) for _ in range(16)]
+        ys = [_out(7168, dev) for _ in range(16)]
         arr = ctypes.c_void_p * 16
         assert lib.stbl_amd_gemv_fp4_batch(arr(*[y.data_ptr() for y in ys]), arr(*[codes.data_ptr()] * 16),
                                            arr(*[scales.data_ptr()] * 16), arr(*[x.data_ptr() for x in xs]),
@@ -144,7 +153,7 @@ def _cases(dev, seed):
             pick = [[(j + 2 * i) % 7 for j in range(6)] for i in range(t)]
             wts = [[0.3, 0.2, 0.15, 0.15, 0.1, 0.1]] * t
             slots = experts + [shared]
-            y = torch.empty((t, dim), dtype=torch.bfloat16, device=dev)
+            y = _out((t, dim), dev, torch.bfloat16)
             work = torch.empty(ops.moe_work_bytes(t, 6, dim, inter), dtype=torch.uint8, device=dev)
             arr = (ctypes.c_void_p * len(slots))(*[s.data_ptr() for s in slots])
             pk = (ctypes.c_int * (6 * t))(*[v for row in pick for v in row])
@@ -156,8 +165,8 @@ def _cases(dev, seed):
     logits = torch.randn((4, 256), device=dev, generator=g) * 3
 
     def route(lib):
-        ids = torch.empty((4, 8), dtype=torch.int32, device=dev)
-        w = torch.empty((4, 8), device=dev)
+        ids = _out((4, 8), dev, torch.int32)
+        w = _out((4, 8), dev)
         assert lib.stbl_amd_route(_p(logits), None, 4, 256, 8, 2.5, 1, _p(ids), _p(w), None, st) == 0
         return [ids, w]
     cases.append(("route sqrt-softplus", route))
@@ -167,7 +176,7 @@ def _cases(dev, seed):
     xg = bf((64, 7168))
 
     def gemm(lib):
-        y = torch.empty((64, 2048), device=dev)
+        y = _out((64, 2048), dev)
         work = torch.empty(int(lib.stbl_amd_gemm_work_bytes(64, 2048, 7168)), dtype=torch.uint8, device=dev)
         assert lib.stbl_amd_gemm(ops.FP4, _p(y), _p(gc), _p(gs), _p(xg), 64, 2048, 7168, 32, 1, _p(work), st) == 0
         return [y]
@@ -175,17 +184,35 @@ def _cases(dev, seed):
     return cases
 
 
-def compare(new_path, old_path, seeds=3):
-    """Runs every case on both builds; returns the list of (case, differing values)."""
-    new, old = _load(new_path), _load(old_path)
+def _run(fn, lib):
+    """The case's outputs, or None when the build rejected it (a recorded failure or a non-zero v2
+    status, which the cases assert)."""
+    lib.stbl_amd_last_error(None, 0)  # clear
+    try:
+        outs = fn(lib)
+    except AssertionError:
+        return None
+    torch.cuda.synchronize()
+    return None if lib.stbl_amd_last_error(None, 0) else outs
+
+
+def compare(new, old, seeds=3):
+    """Runs every case on both builds (paths of built libraries, or loaded handles); returns the list
+    of (case, differing bytes or "rejected by ...")."""
+    new = _load(new) if isinstance(new, str) else new
+    old = _load(old) if isinstance(old, str) else old
     if new.stbl_amd_version() != old.stbl_amd_version():
         raise SystemExit(f"ABI versions differ: {new.stbl_amd_version()} vs {old.stbl_amd_version()}")
     dev = torch.device("cuda", torch.cuda.current_device())
     bad = []
     for seed in range(seeds):
         for name, fn in _cases(dev, seed):
-            a, b = fn(new), fn(old)
-            torch.cuda.synchronize()
+            a, b = _run(fn, new), _run(fn, old)
+            if a is None or b is None:
+                who = " and ".join(w for w, r in (("the new build", a), ("the old build", b)) if r is None)
+                bad.append((f"{name} seed {seed}", f"rejected by {who}"))
+                print(f"{name} seed {seed}: rejected by {who}", flush=True)
+                continue
             d = sum(int((x.view(torch.uint8) != y.view(torch.uint8)).sum()) for x, y in zip(a, b))
             if d:
                 bad.append((f"{name} seed {seed}", d))

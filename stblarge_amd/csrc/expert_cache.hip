@@ -117,6 +117,10 @@ struct Prefetcher {
     uint64_t stat[5] = {};
 };
 
+struct PendingRead {
+    int expert, slot;
+};
+
 struct ExpertCache {
     int device = 0;
     int slots = 0;
@@ -140,6 +144,23 @@ struct ExpertCache {
     int fail_in = -1;  // test hook: the refill after this many more fails (host side, nothing copied)
     FileTier *file = nullptr;
     Prefetcher *pf = nullptr;
+    // A lookup between stbl_amd_cache_lookup_begin and _end: its file misses (mapped, not yet read),
+    // routed prefetch jobs still being read when it began, and whether the copy stream holds work
+    // the compute stream must be ordered after.
+    struct Open {
+        bool open = false, order = false;
+        int layer = 0;
+        std::vector<PendingRead> pend;
+        std::vector<uint64_t> reading;
+    } op;
+    // Per layer, the guesses noted for it before the lookups that may evict them, and whether each
+    // was uncached then; the lookahead counters (the reference's stbl_lookahead, stbl/model.cu:452-460).
+    struct Guess {
+        std::vector<int> ids;
+        std::vector<char> cold;
+    };
+    std::unordered_map<int, Guess> guesses;
+    uint64_t la[4] = {};
 };
 
 // GGUF MXFP4 blocks (byte 0: E8M0 scale; byte 1+i: element i in the low nibble, element 16+i in the
@@ -318,10 +339,6 @@ static hipError_t read_pieces(ExpertCache &c, const std::vector<Piece> &ps, std:
     return hipSuccess;
 }
 
-struct PendingRead {
-    int expert, slot;
-};
-
 // Serves the file misses of one lookup: reads them in batches of kStageExperts, then repacks each
 // into its slot on the copy stream after the slot's last use. Returns how many were served (a prefix
 // of `pend`); on failure `err` says why.
@@ -477,26 +494,24 @@ static hipError_t pf_settle(ExpertCache &c, int layer, const int *ids, int n) {
     return e;
 }
 
-// A routed expert that a prefetch job holds: 0 when its bytes are (or will be, in stream order) in
-// the slot; 1 when the caller must read it on demand (the job had not started, or failed); <0 error.
+// A routed expert that a prefetch job holds (stbl/model.cu:478-496, 550-553): 0 when it landed (its
+// repack is then ordered on the copy stream); 1 when it is still being read (the lookup's end waits
+// for it, as the reference waits after queueing the cached experts' kernels); 2 when the caller
+// must read it on demand (the job had not started, or failed); <0 on a runtime error.
 static int pf_claim(ExpertCache &c, std::unordered_map<uint64_t, std::shared_ptr<PfJob>>::iterator jt) {
     std::shared_ptr<PfJob> j = jt->second;
     int st = PF_QUEUED;
-    bool waited = false;
-    if (!j->state.compare_exchange_strong(st, PF_TAKEN))
-        while (st == PF_READING) {  // stbl/model.cu:550-553: wait for the reading job
-            waited = true;
-            std::this_thread::yield();
-            st = j->state.load();
+    if (!j->state.compare_exchange_strong(st, PF_TAKEN)) {
+        if (st == PF_READING) return 1;
+        if (st == PF_LANDED) {
+            c.pf->stat[1]++;
+            return pf_retire_landed(c, jt) == hipSuccess ? 0 : -1;
         }
-    if (st == PF_LANDED) {
-        c.pf->stat[waited ? 2 : 1]++;
-        return pf_retire_landed(c, jt) == hipSuccess ? 0 : -1;
     }
     c.pf->stat[4]++;  // not started (now taken) or failed
     pf_release(c, j);
     c.pf->jobs.erase(jt);
-    return 1;
+    return 2;
 }
 
 // The least recently used entry that may be evicted, skipping prefetch jobs still queued or reading
@@ -541,6 +556,44 @@ static ExpertCache *new_cache(int slots, uint64_t slot_bytes, int n_experts, int
         return nullptr;
     }
     return c;
+}
+
+// The open lookup's file misses from `from` on leave the map again (their slots are free; they
+// count as neither misses nor refills), so the next lookup misses them again.
+static void unmap_pending(ExpertCache &c, size_t from) {
+    auto &pend = c.op.pend;
+    for (size_t j = from; j < pend.size(); j++) {
+        auto it = c.where.find((uint64_t)c.op.layer << 32 | (uint32_t)pend[j].expert);
+        c.lru.erase(it->second.second);
+        c.where.erase(it);
+        c.free_slots.push_back(pend[j].slot);
+        c.misses--;
+        c.refill_bytes -= c.slot_bytes;
+    }
+    pend.resize(from);
+}
+
+// Makes `compute` wait for the work queued so far on the copy stream.
+static hipError_t order_compute(ExpertCache &c, hipStream_t compute) {
+    hipError_t e = hipEventRecord(c.ready, c.copy);
+    if (e == hipSuccess) e = hipStreamWaitEvent(compute, c.ready, 0);
+    return e;
+}
+
+// Lookahead counters at the lookup of the guessed layer (stbl/model.cu:452-460): the guesses that
+// were uncached when noted and how many of them are routed; the routed experts not mapped now
+// (counted before the lookup maps them) and how many of them were guessed.
+static void count_lookahead(ExpertCache &c, const int *ids, int n, int layer) {
+    auto g = c.guesses.find(layer);
+    if (g == c.guesses.end()) return;
+    const std::vector<int> &guess = g->second.ids;
+    auto routed = [&](int e) { return std::find(ids, ids + n, e) != ids + n; };
+    for (size_t i = 0; i < guess.size(); i++)
+        if (g->second.cold[i]) c.la[0]++, c.la[1] += routed(guess[i]);
+    for (int i = 0; i < n; i++)
+        if (!c.where.count((uint64_t)layer << 32 | (uint32_t)ids[i]))
+            c.la[2]++, c.la[3] += std::find(guess.begin(), guess.end(), ids[i]) != guess.end();
+    c.guesses.erase(g);
 }
 
 }  // namespace stbl
@@ -664,35 +717,43 @@ int stbl_amd_cache_file_info(void *cache, uint64_t *out) {
 
 void stbl_amd_cache_destroy(void *cache) { destroy((ExpertCache *)cache); }
 
-// Looks up n expert ids (HOST array) of one layer, in order. slot_ptrs (HOST, n entries) receives
-// each expert's slot; hit (HOST, optional) 1/0 per id. Misses are copied from the host pool on the
-// copy stream and `compute` is made to wait for them. Returns the number of misses, or a negative
-// hipError_t (then nothing of this lookup is mapped that was not before, apart from completed
-// refills, and the caller must not use slot_ptrs).
-int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **slot_ptrs, int *hit,
-                          hipStream_t compute) {
+// Looks up n expert ids (HOST array) of one layer, in order, and maps every miss to a slot.
+// slot_ptrs (HOST, n entries) receives each expert's slot; hit (HOST, optional) 1/0 per id; ready
+// (HOST, optional) 1 where `compute` may read the slot at once, 0 where it must first pass
+// stbl_amd_cache_lookup_end (a refill, a landed or still-reading prefetch). Pool misses are queued on
+// the copy stream here; file misses are read by _end. Every begin must be followed by an end before
+// the next lookup or prefetch of the cache: in between, the caller may queue kernels that read the
+// ready slots, which then run while the misses are copied or read (stbl/model.cu:541-549, 588).
+// Returns the number of misses, or a negative hipError_t (then nothing of this lookup is mapped that
+// was not before, apart from completed refills; the lookup is not open and slot_ptrs must not be used).
+int stbl_amd_cache_lookup_begin(void *cache, const int *ids, int n, int layer, void **slot_ptrs, int *hit, int *ready,
+                                hipStream_t compute) {
     ExpertCache *c = (ExpertCache *)cache;
     if (!c || !ids || !slot_ptrs || n < 0 || layer < 0 || layer >= c->n_layers)
         return abi_fail(hipErrorInvalidValue, "cache_lookup: bad arguments");
+    if (c->op.open) return abi_fail(hipErrorInvalidValue, "cache_lookup: the previous lookup was not ended");
     for (int i = 0; i < n; i++)
         if (ids[i] < 0 || ids[i] >= c->n_experts) return abi_fail(hipErrorInvalidValue, "cache_lookup: expert id %d out of range", ids[i]);
     c->lookups++;
+    count_lookahead(*c, ids, n, layer);
     auto key = [&](int e) { return (uint64_t)layer << 32 | (uint32_t)e; };
+    ExpertCache::Open &op = c->op;
+    op.order = false;
+    op.layer = layer;
+    op.pend.clear();
+    op.reading.clear();
     // A lookup that fails after queueing refills still orders `compute` after them: the refilled
     // experts stay mapped, and a later lookup that hits them queues no wait of its own.
-    bool order = false;
-    auto order_compute = [&]() {
-        hipError_t e = hipEventRecord(c->ready, c->copy);
-        if (e == hipSuccess) e = hipStreamWaitEvent(compute, c->ready, 0);
-        return e;
+    auto fail = [&](hipError_t e, const std::string &msg) {
+        unmap_pending(*c, 0);
+        op.reading.clear();
+        if (op.order) (void)order_compute(*c, compute);
+        return abi_fail(e, "cache_lookup: %s", msg.c_str());
     };
     if (c->pf) {
         const hipError_t e = pf_settle(*c, layer, ids, n);
-        order = true;  // retired prefetches made the copy stream wait
-        if (e != hipSuccess) {
-            (void)order_compute();
-            return abi_status(e, "cache_lookup: settling prefetches");
-        }
+        op.order = true;  // retired prefetches made the copy stream wait
+        if (e != hipSuccess) return fail(e, std::string("settling prefetches: ") + hipGetErrorString(e));
     }
     // 1. touch every cached expert of this lookup first
     for (int i = 0; i < n; i++) {
@@ -701,22 +762,6 @@ int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **
     }
     c->touched.clear();
     int nmiss = 0;
-    std::vector<PendingRead> pend;  // file tier: misses mapped, not yet read
-    auto unmap = [&](size_t from) {  // pending misses from `from` on stay unmapped
-        for (size_t j = from; j < pend.size(); j++) {
-            auto it = c->where.find(key(pend[j].expert));
-            c->lru.erase(it->second.second);
-            c->where.erase(it);
-            c->free_slots.push_back(pend[j].slot);
-            c->misses--;
-            c->refill_bytes -= c->slot_bytes;
-        }
-        pend.resize(from);
-    };
-    auto fail = [&](hipError_t e, const char *fmt, int a, const char *b) {
-        if (order) (void)order_compute();
-        return abi_fail(e, fmt, a, b);
-    };
     for (int i = 0; i < n; i++) {
         const uint64_t k = key(ids[i]);
         auto it = c->where.find(k);
@@ -724,23 +769,23 @@ int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **
         if (it != c->where.end()) {
             c->lru.splice(c->lru.begin(), c->lru, it->second.second);
             s = it->second.first;
-            int claim = 0;
+            int claim = -3;  // a plain entry
             if (c->pf) {
                 auto jt = c->pf->jobs.find(k);
                 if (jt != c->pf->jobs.end()) claim = pf_claim(*c, jt);
             }
-            if (claim < 0) {
-                unmap(0);
-                return fail(hipErrorUnknown, "cache_lookup: expert %d: waiting for its prefetch failed%s", ids[i], "");
-            }
-            if (claim == 0) {
+            if (claim == -1) return fail(hipErrorUnknown, "expert " + std::to_string(ids[i]) + ": retiring its prefetch failed");
+            if (claim != 2) {
                 slot_ptrs[i] = c->mem + (uint64_t)s * c->slot_bytes;
                 if (hit) hit[i] = 1;
+                if (ready) ready[i] = claim == -3;
+                if (claim == 0) op.order = true;
+                if (claim == 1) op.reading.push_back(k);
                 c->hits++;
                 c->touched.push_back(s);
                 continue;
             }
-            pend.push_back({ids[i], s});  // a prefetch that had not started or failed: read it now
+            op.pend.push_back({ids[i], s});  // a prefetch that had not started or failed: read it on demand
         } else {
             // 2. miss: a free slot, or the least recently used entry not needed by this lookup
             s = take_slot(*c);
@@ -750,15 +795,10 @@ int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **
                         if (key(ids[j]) == key_) return true;
                     return false;
                 });
-            if (s == -2) {
-                unmap(0);
-                return fail(hipErrorUnknown, "cache_lookup: expert %d: retiring a prefetch failed%s", ids[i], "");
-            }
-            if (s < 0) {
-                unmap(0);
-                return fail(hipErrorOutOfMemory, "cache_lookup: every slot is held by this lookup or a prefetch (%d slots)%s",
-                            c->slots, "");
-            }
+            if (s == -2) return fail(hipErrorUnknown, "expert " + std::to_string(ids[i]) + ": retiring a prefetch failed");
+            if (s < 0)
+                return fail(hipErrorOutOfMemory,
+                            "every slot is held by this lookup or a prefetch (" + std::to_string(c->slots) + " slots)");
             if (!c->file) {
                 const uint8_t *src = c->host + ((uint64_t)layer * c->n_experts + ids[i]) * c->host_stride;
                 hipError_t e = hipSuccess;
@@ -770,40 +810,121 @@ int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **
                 }
                 if (e != hipSuccess) {
                     c->free_slots.push_back(s);  // slot stays unmapped: the next lookup misses again
-                    return fail(e, "cache_lookup: refill of expert %d failed: %s", ids[i], hipGetErrorString(e));
+                    return fail(e, "refill of expert " + std::to_string(ids[i]) + " failed: " + hipGetErrorString(e));
                 }
-                order = true;
+                op.order = true;
             } else {
-                pend.push_back({ids[i], s});
+                op.pend.push_back({ids[i], s});
             }
             c->lru.push_front(k);
             c->where[k] = {s, c->lru.begin()};
         }
         slot_ptrs[i] = c->mem + (uint64_t)s * c->slot_bytes;
         if (hit) hit[i] = 0;
+        if (ready) ready[i] = 0;
         c->misses++;
         c->refill_bytes += c->slot_bytes;
         c->touched.push_back(s);
         nmiss++;
     }
-    if (!pend.empty()) {
+    op.open = true;
+    return nmiss;
+}
+
+// Ends the open lookup (a no-op when none is open): reads its file misses (the host thread waits
+// for the reads; the kernels queued meanwhile run on), waits for routed prefetches still being
+// read (one that failed is read on demand), and makes `compute` wait for every copy and repack of
+// the lookup. Returns 0 or a negative hipError_t; on failure the experts not yet read stay unmapped
+// and the caller must not queue kernels on the slots begin reported not ready.
+int stbl_amd_cache_lookup_end(void *cache, hipStream_t compute) {
+    ExpertCache *c = (ExpertCache *)cache;
+    if (!c) return abi_fail(hipErrorInvalidValue, "cache_lookup_end: null cache");
+    ExpertCache::Open &op = c->op;
+    if (!op.open) return 0;
+    op.open = false;
+    auto serve = [&]() -> int {
+        if (op.pend.empty()) return 0;
         hipError_t e;
         std::string err;
-        const size_t served = serve_file_misses(*c, layer, pend, e, err);
-        order |= served > 0;
-        if (served < pend.size()) {
-            const int first = pend[served].expert;
-            unmap(served);
-            if (order) (void)order_compute();
-            return abi_fail(e == hipSuccess ? hipErrorUnknown : e, "cache_lookup: reading expert %d of layer %d failed: %s",
-                            first, layer, err.c_str());
+        const size_t served = serve_file_misses(*c, op.layer, op.pend, e, err);
+        op.order |= served > 0;
+        if (served == op.pend.size()) {
+            op.pend.clear();
+            return 0;
+        }
+        const int first = op.pend[served].expert;
+        unmap_pending(*c, served);
+        if (op.order) (void)order_compute(*c, compute);
+        return abi_fail(e == hipSuccess ? hipErrorUnknown : e, "cache_lookup: reading expert %d of layer %d failed: %s",
+                        first, op.layer, err.c_str());
+    };
+    // 1. demand reads (stbl/model.cu:550)
+    if (int r = serve()) return r;
+    // 2. routed prefetches that were being read (stbl/model.cu:551-553)
+    for (uint64_t k : op.reading) {
+        auto jt = c->pf->jobs.find(k);
+        if (jt == c->pf->jobs.end()) continue;
+        const std::shared_ptr<PfJob> j = jt->second;
+        int st;
+        while ((st = j->state.load()) == PF_READING) std::this_thread::yield();
+        if (st == PF_LANDED) {
+            c->pf->stat[2]++;
+            op.order = true;
+            if (pf_retire_landed(*c, jt) != hipSuccess) {
+                (void)order_compute(*c, compute);
+                return abi_fail(hipErrorUnknown, "cache_lookup: retiring the prefetch of expert %d failed", j->expert);
+            }
+        } else {  // it failed: read it on demand, as a miss
+            c->pf->stat[4]++;
+            pf_release(*c, j);
+            c->pf->jobs.erase(jt);
+            op.pend.push_back({j->expert, j->slot});
+            c->hits--, c->misses++, c->refill_bytes += c->slot_bytes;
         }
     }
-    if (order) {
-        const hipError_t e = order_compute();
+    op.reading.clear();
+    if (int r = serve()) return r;
+    if (op.order) {
+        const hipError_t e = order_compute(*c, compute);
         if (e != hipSuccess) return abi_status(e, "cache_lookup: ordering the compute stream after the refills");
     }
-    return nmiss;
+    return 0;
+}
+
+// Looks up n expert ids of one layer and makes `compute` wait for every refill: begin, then end.
+// Returns the number of misses, or a negative hipError_t (then nothing of this lookup is mapped that
+// was not before, apart from completed refills, and the caller must not use slot_ptrs).
+int stbl_amd_cache_lookup(void *cache, const int *ids, int n, int layer, void **slot_ptrs, int *hit,
+                          hipStream_t compute) {
+    const int nmiss = stbl_amd_cache_lookup_begin(cache, ids, n, layer, slot_ptrs, hit, nullptr, compute);
+    if (nmiss < 0) return nmiss;
+    const int r = stbl_amd_cache_lookup_end(cache, compute);
+    return r < 0 ? r : nmiss;
+}
+
+// Notes the guesses for `layer` (best first; the reference's STBL_LOOKAHEAD guesses: the next
+// layer's router on this layer's input, stbl/model.cu:461-474) before the lookups that could evict
+// them, with whether each is uncached now. The next lookup of `layer` then updates the lookahead
+// counters with them. A later note for the same layer replaces an unused one.
+int stbl_amd_cache_note_guesses(void *cache, const int *ids, int n, int layer) {
+    ExpertCache *c = (ExpertCache *)cache;
+    if (!c || (!ids && n > 0) || n < 0 || layer < 0 || layer >= c->n_layers)
+        return abi_fail(hipErrorInvalidValue, "cache_note_guesses: bad arguments");
+    ExpertCache::Guess &g = c->guesses[layer];
+    g.ids.assign(ids, ids + n);
+    g.cold.assign(n, 0);
+    for (int i = 0; i < n; i++) g.cold[i] = !c->where.count((uint64_t)layer << 32 | (uint32_t)ids[i]);
+    return 0;
+}
+
+// out[0..3] = guesses that were uncached when noted, of those how many the lookup of their layer
+// routed; routed experts that were not mapped at their lookup, of those how many were guessed (the
+// reference's stbl_lookahead counters, stbl/model.cu:452-460, 1107-1109).
+int stbl_amd_cache_lookahead(void *cache, uint64_t *out) {
+    ExpertCache *c = (ExpertCache *)cache;
+    if (!c || !out) return abi_fail(hipErrorInvalidValue, "cache_lookahead: bad arguments");
+    for (int i = 0; i < 4; i++) out[i] = c->la[i];
+    return 0;
 }
 
 // Starts `readers` (1..16) background prefetch readers on a file-backed cache, with staging for
@@ -851,6 +972,7 @@ int stbl_amd_cache_prefetch(void *cache, const int *ids, int n, int layer) {
     ExpertCache *c = (ExpertCache *)cache;
     if (!c || !c->pf || !ids || n < 0 || layer < 0 || layer >= c->n_layers)
         return abi_fail(hipErrorInvalidValue, "cache_prefetch: bad arguments or prefetch not enabled");
+    if (c->op.open) return abi_fail(hipErrorInvalidValue, "cache_prefetch: a lookup is open (end it first)");
     for (int i = 0; i < n; i++)
         if (ids[i] < 0 || ids[i] >= c->n_experts) return abi_fail(hipErrorInvalidValue, "cache_prefetch: expert id %d out of range", ids[i]);
     Prefetcher &P = *c->pf;

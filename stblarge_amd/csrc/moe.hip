@@ -307,7 +307,8 @@ __global__ __launch_bounds__(256) void k_sqrt_softplus(float *__restrict__ s, in
 // configuration's router) or sqrt(softplus(logit)) with softplus(l) = l above 20, else
 // log1p(exp(l)) (score_fn 1, stbl/kernels.cu:436-442); the top-k of score + bias (ties to the lower
 // expert id) by k rounds of a workgroup argmax; weight_i = score_i / (sum of the top-k scores in
-// top-k order + 1e-20) * route_scale.
+// top-k order + 1e-20) * route_scale. A NaN key ranks below every number (so a token with fewer than
+// k numeric keys takes the lowest unused ids next), and its weight comes out NaN.
 __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits, const float *__restrict__ bias,
                                                int n_exp, int topk, float route_scale, int score_fn,
                                                int *__restrict__ ids, float *__restrict__ weights,
@@ -331,7 +332,8 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
             bool used = false;
             for (int q = 0; q < p; q++) used |= chosen[q] == e;
             if (used) continue;
-            const float v = sc[e] + (bias ? bias[e] : 0.f);
+            float v = sc[e] + (bias ? bias[e] : 0.f);
+            v = v != v ? -INFINITY : v;  // a NaN key ranks last; among equal keys the lower id wins
             if (v > best || (v == best && e < besti)) best = v, besti = e;
         }
 #pragma unroll
@@ -506,19 +508,28 @@ int stbl_amd_expert_ffn(int fmt, void *y, const void *slot, const void *x, int m
     return abi_status(e, "expert_ffn launch");
 }
 
-// Routed MoE over cached expert slots. slots: HOST array of n_slots device pointers (one per
-// distinct expert used by this call). pick: HOST [t][topk] indices into slots, weights: HOST
-// [t][topk] route weights, shared: index into slots of the always-on expert (weight 1) or -1, whose
-// slot holds format shared_fmt (-1: the routed experts' format; the reference's shared expert is
-// FP8 with E8M0 32x32 scales, stbl/model.cu:544-547, next to FP4 routed experts).
+// Routed MoE over cached expert slots, in up to two phases. slots: HOST array of n_slots device
+// pointers (one per distinct expert used by this call). pick: HOST [t][topk] indices into slots,
+// weights: HOST [t][topk] route weights, shared: index into slots of the always-on expert (weight
+// 1) or -1, whose slot holds format shared_fmt (-1: the routed experts' format; the reference's
+// shared expert is FP8 with E8M0 32x32 scales, stbl/model.cu:544-547, next to FP4 routed experts).
 // work: device scratch of at least stbl_amd_moe_work_bytes(t, topk, dim, inter) bytes.
-int stbl_amd_moe_experts(int fmt, void *y, const void *x, int t, int dim, int inter, const void *const *slots,
-                         int n_slots, const int *pick, const float *weights, int topk, int shared, int shared_fmt,
-                         float limit, int official, int y_f32, void *work, hipStream_t st) {
+// phase 0 runs every expert and the combine. With slot_ready (HOST, n_slots flags), phase 1 runs
+// the experts whose slots are ready and phase 2 the others and then the combine, so a caller can
+// queue phase 1 before an expert cache's refills are waited for and phase 2 after
+// (stbl/model.cu:541-549, 588). Both phases must get the same arguments and work; every expert's
+// output has its own rows of work, and the combine adds them in top-k order, so the result is the
+// same bits as phase 0.
+static int moe_experts_impl(int fmt, void *y, const void *x, int t, int dim, int inter, const void *const *slots,
+                            int n_slots, const int *pick, const float *weights, int topk, int shared, int shared_fmt,
+                            float limit, int official, int y_f32, const int *slot_ready, int phase, void *work,
+                            hipStream_t st) {
     if (shared_fmt < 0) shared_fmt = fmt;
     if (!fmt_ok(fmt) || !fmt_ok(shared_fmt))
         return abi_fail(hipErrorInvalidValue, "moe_experts: unknown format %d / %d", fmt, shared_fmt);
     if (!y || !x || !slots || !pick || !weights || !work) return abi_fail(hipErrorInvalidValue, "moe_experts: null pointer");
+    if (phase < 0 || phase > 2 || (phase > 0 && !slot_ready))
+        return abi_fail(hipErrorInvalidValue, "moe_experts: phase must be 0, or 1 or 2 with slot_ready (phase=%d)", phase);
     if (!dims_ok(fmt, dim, inter) || !dims_ok(shared_fmt, dim, inter))
         return abi_fail(hipErrorInvalidValue, "moe_experts: unsupported dims %d x %d", dim, inter);
     if (t < 1 || t > kMoeMaxT || topk < 1 || topk + 1 > kMoeMaxPick || n_slots < 1 || shared >= n_slots)
@@ -526,41 +537,64 @@ int stbl_amd_moe_experts(int fmt, void *y, const void *x, int t, int dim, int in
     if (!aligned16(x) || !aligned16(work)) return abi_fail(hipErrorInvalidValue, "moe_experts: x and work must be 16-byte aligned");
     for (int i = 0; i < n_slots; i++)
         if (!slots[i] || ((uintptr_t)slots[i] & 255)) return abi_fail(hipErrorInvalidValue, "moe_experts: slot %d null or not 256-byte aligned", i);
-    // jobs: one per (slot, group of <= 4 tokens); pair rows numbered in job order. A shared expert of
-    // another format runs in launches of its own (sjobs).
-    static thread_local MoeJob jobs[kMoeMaxT * kMoeMaxPick], sjobs[kMoeMaxT];
+    const int npick = topk + (shared >= 0 ? 1 : 0);
+    for (int tt = 0; tt < t; tt++)
+        for (int p = 0; p < topk; p++)
+            if (pick[tt * topk + p] < 0 || pick[tt * topk + p] >= n_slots)
+                return abi_fail(hipErrorInvalidValue, "moe_experts: pick out of range");
+    // jobs: one per (slot, group of <= 4 tokens); pair rows numbered in job order over all slots,
+    // so both phases number them alike. A shared expert of another format runs in launches of its
+    // own (sjobs). Each array holds every (token, pick) pair, duplicates included.
+    static thread_local MoeJob jobs[kMoeMaxT * kMoeMaxPick], sjobs[kMoeMaxT * kMoeMaxPick];
     PickTable table = {};
     int njobs = 0, nsjobs = 0, npairs = 0;
-    const int npick = topk + (shared >= 0 ? 1 : 0);
     for (int s = 0; s < n_slots; s++) {
+        const bool run = phase == 0 || (phase == 1) == (slot_ready[s] != 0);
         MoeJob *J = nullptr;
         for (int tt = 0; tt < t; tt++)
             for (int p = 0; p < npick; p++) {
                 const int sl = p < topk ? pick[tt * topk + p] : shared;
-                if (sl < 0 || sl >= n_slots) return abi_fail(hipErrorInvalidValue, "moe_experts: pick out of range");
                 if (sl != s) continue;
-                if (!J || J->m == kMoeMaxTok) {
-                    J = s == shared && shared_fmt != fmt ? &sjobs[nsjobs++] : &jobs[njobs++];
-                    *J = MoeJob{};
-                    J->slot = (const uint8_t *)slots[s];
+                table.pair[tt][p] = npairs;
+                if (run) {
+                    if (!J || J->m == kMoeMaxTok) {
+                        J = s == shared && shared_fmt != fmt ? &sjobs[nsjobs++] : &jobs[njobs++];
+                        *J = MoeJob{};
+                        J->slot = (const uint8_t *)slots[s];
+                    }
+                    J->tok[J->m] = tt;
+                    J->pair[J->m] = npairs;
+                    J->w[J->m] = p < topk ? weights[tt * topk + p] : 1.f;
+                    J->m++;
                 }
-                J->tok[J->m] = tt;
-                J->pair[J->m] = npairs;
-                J->w[J->m] = p < topk ? weights[tt * topk + p] : 1.f;
-                J->m++;
-                table.pair[tt][p] = npairs++;
+                npairs++;
             }
     }
     uint16_t *h = (uint16_t *)work;
-    uint16_t *o = h + (size_t)npairs * inter;
+    uint16_t *o = h + (size_t)t * npick * inter;
     hipError_t e = run_fmt(fmt, jobs, njobs, dim, inter, (const uint16_t *)x, h, o, limit, official, 0, st);
     if (e == hipSuccess && nsjobs > 0)
         e = run_fmt(shared_fmt, sjobs, nsjobs, dim, inter, (const uint16_t *)x, h, o, limit, official, 0, st);
-    if (e == hipSuccess) {
+    if (e == hipSuccess && phase != 1) {
         hipLaunchKernelGGL(k_moe_combine, dim3(ceil_div(dim, 256), t), dim3(256), 0, st, table, npick, o, y, dim, y_f32);
         e = hipGetLastError();
     }
     return abi_status(e, "moe_experts launch");
+}
+
+int stbl_amd_moe_experts(int fmt, void *y, const void *x, int t, int dim, int inter, const void *const *slots,
+                         int n_slots, const int *pick, const float *weights, int topk, int shared, int shared_fmt,
+                         float limit, int official, int y_f32, void *work, hipStream_t st) {
+    return moe_experts_impl(fmt, y, x, t, dim, inter, slots, n_slots, pick, weights, topk, shared, shared_fmt, limit,
+                            official, y_f32, nullptr, 0, work, st);
+}
+
+int stbl_amd_moe_experts_phase(int fmt, void *y, const void *x, int t, int dim, int inter, const void *const *slots,
+                               int n_slots, const int *pick, const float *weights, int topk, int shared,
+                               int shared_fmt, float limit, int official, int y_f32, const int *slot_ready, int phase,
+                               void *work, hipStream_t st) {
+    return moe_experts_impl(fmt, y, x, t, dim, inter, slots, n_slots, pick, weights, topk, shared, shared_fmt, limit,
+                            official, y_f32, slot_ready, phase, work, st);
 }
 
 // Scratch bytes stbl_amd_moe_experts needs for t tokens.

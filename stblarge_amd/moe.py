@@ -7,6 +7,7 @@ Mirrors the reference engine's moe() (stbl/model.cu:426-594) for one layer:
 All device work is in libstbl_amd.so; this module only sequences it and keeps the host-side state.
 """
 
+import contextlib
 import ctypes
 
 import torch
@@ -86,6 +87,38 @@ class ExpertCache:
             _lib.check(nmiss, "cache_lookup")
         return [int(p) for p in ptrs], [bool(h) for h in hit], nmiss
 
+    def lookup_begin(self, ids, layer=0, stream=None):
+        """First half of lookup (stbl_amd_cache_lookup_begin): maps every id and queues pool refills;
+        returns (ptrs, hits, ready, misses), ready[i] telling whether the slot may be read before
+        lookup_end. lookup_end must follow before the next lookup or prefetch."""
+        n = len(ids)
+        arr = (ctypes.c_int * max(n, 1))(*[int(i) for i in ids])
+        ptrs = (ctypes.c_void_p * max(n, 1))()
+        hit = (ctypes.c_int * max(n, 1))()
+        rdy = (ctypes.c_int * max(n, 1))()
+        nmiss = _lib.load().stbl_amd_cache_lookup_begin(self.handle, arr, n, layer, ptrs, hit, rdy, ops._stream(stream))
+        if nmiss < 0:
+            _lib.check(nmiss, "cache_lookup_begin")
+        return [int(p) for p in ptrs[:n]], [bool(h) for h in hit[:n]], [bool(r) for r in rdy[:n]], nmiss
+
+    def lookup_end(self, stream=None):
+        """Second half of lookup: file reads, routed prefetches still being read, and the compute
+        stream's wait for every refill (stbl_amd_cache_lookup_end)."""
+        _lib.check(_lib.load().stbl_amd_cache_lookup_end(self.handle, ops._stream(stream)), "cache_lookup_end")
+
+    def note_guesses(self, ids, layer):
+        """Records guesses for `layer` before the lookups that could evict them (lookahead counters)."""
+        n = len(ids)
+        arr = (ctypes.c_int * max(n, 1))(*[int(i) for i in ids])
+        _lib.check(_lib.load().stbl_amd_cache_note_guesses(self.handle, arr, n, layer), "cache_note_guesses")
+
+    def lookahead(self):
+        """The reference's stbl_lookahead counters (stbl/model.cu:452-460)."""
+        out = (ctypes.c_uint64 * 4)()
+        _lib.check(_lib.load().stbl_amd_cache_lookahead(self.handle, out), "cache_lookahead")
+        keys = ("cold_guesses", "cold_guesses_routed", "misses", "misses_guessed")
+        return dict(zip(keys, [int(v) for v in out]))
+
     def mark_used(self, stream=None):
         _lib.check(_lib.load().stbl_amd_cache_mark_used(self.handle, ops._stream(stream)), "cache_mark_used")
 
@@ -143,12 +176,24 @@ class MoELayer:
         self.work = torch.empty(ops.moe_work_bytes(max_tokens, topk, dim, inter), dtype=torch.uint8, device=dev)
         self.max_tokens = max_tokens
         self.last_route = None  # (ids, weights) of the last step, as lists (stbl_last_route)
+        self.last_lookup = None  # (distinct expert ids in lookup order, hit flags) of the last step
 
     def route(self, logits):
         ids, w = ops.route(logits, self.topk, self.bias, self.route_scale, score_fn=self.score_fn)
         return ids.cpu().tolist(), w.cpu().tolist()  # host sync, as the reference's to_host
 
-    def forward(self, x, logits, route=None, stream=None):
+    def forward(self, x, logits, route=None, stream=None, after_reads=None):
+        """y = the layer's output for x. Every device call goes on `stream` (default: the current
+        stream). As in the reference (stbl/model.cu:541-549, 588), the experts already in HBM and
+        the shared expert are queued first, then the cache's misses are waited for (file reads
+        block the host meanwhile), then the missed experts and the ordered combine run; the result
+        is the same bits as one call over all experts. after_reads() runs between the two (the
+        reference issues its prefetches there, stbl/model.cu:555-586)."""
+        ctx = torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
+        with ctx:
+            return self._forward(x, logits, route, after_reads)
+
+    def _forward(self, x, logits, route, after_reads):
         t = x.shape[0]
         if t > self.max_tokens:
             raise ValueError(f"at most {self.max_tokens} tokens per step")
@@ -159,18 +204,33 @@ class MoELayer:
             for e in row:
                 if e not in uniq:
                     uniq.append(e)
-        ptrs, _, _ = self.cache.lookup(uniq, layer=self.layer, stream=stream)
+        ptrs, hits, ready, _ = self.cache.lookup_begin(uniq, layer=self.layer)
+        self.last_lookup = (uniq, hits)
         slot_of = {e: i for i, e in enumerate(uniq)}
         slots = list(ptrs)
         shared = -1
         if self.shared is not None:
             shared = len(slots)
             slots.append(self.shared.data_ptr())
+            ready = ready + [True]
         pick = [[slot_of[e] for e in row] for row in ids]
-        y = ops.moe_experts(x, slots, pick, w, self.fmt, self.dim, self.inter, shared=shared, limit=self.limit,
-                            official=self.official, work=self.work, shared_fmt=self.shared_fmt)
-        self.cache.mark_used(stream)
-        return y
+        y = torch.empty((t, self.dim), dtype=torch.bfloat16, device=x.device)
+        kw = dict(shared=shared, limit=self.limit, official=self.official, work=self.work, out=y,
+                  shared_fmt=self.shared_fmt)
+        try:
+            if all(ready):
+                self.cache.lookup_end()
+                if after_reads:
+                    after_reads()
+                return ops.moe_experts(x, slots, pick, w, self.fmt, self.dim, self.inter, **kw)
+            if any(ready):
+                ops.moe_experts(x, slots, pick, w, self.fmt, self.dim, self.inter, slot_ready=ready, phase=1, **kw)
+            self.cache.lookup_end()
+            if after_reads:
+                after_reads()
+            return ops.moe_experts(x, slots, pick, w, self.fmt, self.dim, self.inter, slot_ready=ready, phase=2, **kw)
+        finally:
+            self.cache.mark_used()  # after every kernel queued on the slots, whatever failed
 
     def close(self):
         self.cache.close()
@@ -178,24 +238,33 @@ class MoELayer:
 
 class MoEStack:
     """Decode through routed MoE layers whose experts share one cache, with the reference engine's
-    stale-router prefetch (stbl/model.cu:426-475, 555-586): after layer l, layer l+1's router is run
-    on layer l's input, its top `prefetch` experts are queued for background reads, and layer l+1's
+    stale-router guesses (stbl/model.cu:426-475, 555-586). Before layer l's lookup, layer l+1's
+    router is scored on layer l's input: its top `lookahead` experts per token are noted with the
+    cache for the lookahead counters (STBL_LOOKAHEAD), and with prefetch > 0 the top `prefetch` are
+    queued for background reads once layer l's own reads are done (STBL_PREFETCH); layer l+1's
     lookup then finds them landed, waits for them, reads them itself or cancels the unrouted ones.
+    prefetch2 > 0 (with prefetch) also queues the top `prefetch2` of layer l+2's router on the same
+    input, behind layer l+1's (STBL_PREFETCH2). As in the reference, lookahead is at least prefetch.
 
     routers[l]: fp32 [n_experts, dim] router weights of layer l; the logits are stbl_gemv_f32 of the
     layer's input, as in the engine (stbl/model.cu:430). Between layers the hidden state takes the
     layer's output as a residual update (h = bf16(h + y)); the layers between MoE blocks (attention,
-    norms) are outside this path. step(h) returns the final hidden state, bf16 [t, dim]."""
+    norms) are outside this path. step(h) returns the final hidden state, bf16 [t, dim].
+    trace (when trace=True): per layer, ("guess", layer, ids) when guesses are noted and ("lookup",
+    layer, distinct routed ids in lookup order), in the order they reach the cache."""
 
     def __init__(self, cache, fmt, dim, inter, n_experts, topk, routers, biases=None, shared_slots=None, prefetch=0,
                  score_fn=ops.SCORE_SIGMOID, route_scale=1.0, limit=0.0, official=False, shared_fmt=None,
-                 max_tokens=4):
+                 max_tokens=4, prefetch2=0, lookahead=0, trace=False):
         n_layers = len(routers)
         biases = biases or [None] * n_layers
         shared_slots = shared_slots or [None] * n_layers
         self.cache, self.routers, self.biases = cache, routers, biases
         self.dim, self.n_experts, self.topk, self.prefetch = dim, n_experts, topk, prefetch
+        self.prefetch2 = prefetch2 if prefetch else 0
+        self.ahead = max(lookahead, prefetch)
         self.score_fn, self.route_scale = score_fn, route_scale
+        self.trace = [] if trace else None
         self.layers = [MoELayer(fmt, dim, inter, None, n_experts, topk, cache.slots, shared_slot=shared_slots[l],
                                 bias=biases[l], route_scale=route_scale, limit=limit, official=official,
                                 max_tokens=max_tokens, score_fn=score_fn, shared_fmt=shared_fmt, cache=cache, layer=l)
@@ -210,17 +279,39 @@ class MoEStack:
             ops.stbl_gemv_f32(out[i], self.routers[layer], hf[i], self.n_experts, self.dim)
         return out
 
+    def _guess(self, layer, hf, m):
+        """Per token, the top m experts of `layer`'s router on hf (best first)."""
+        ids, _ = ops.route(self._logits(layer, hf), min(m, self.n_experts), self.biases[layer], self.route_scale,
+                           score_fn=self.score_fn)
+        return ids.cpu().tolist()
+
+    @staticmethod
+    def _union(rows, m):
+        return list(dict.fromkeys(e for row in rows for e in row[:m]))
+
     def step(self, h, stream=None):
         n_layers = len(self.layers)
-        for l, layer in enumerate(self.layers):
-            hf = h.float()
-            y = layer.forward(h, self._logits(l, hf), stream=stream)
-            if self.prefetch and l + 1 < n_layers:
-                ids, _ = ops.route(self._logits(l + 1, hf), min(self.prefetch, self.n_experts), self.biases[l + 1],
-                                   self.route_scale, score_fn=self.score_fn)
-                guesses = list(dict.fromkeys(e for row in ids.cpu().tolist() for e in row))
-                self.cache.prefetch(guesses, l + 1)
-            h = (hf + y.float()).to(torch.bfloat16)
+        ctx = torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
+        with ctx:
+            for l, layer in enumerate(self.layers):
+                hf = h.float()
+                rows1 = self._guess(l + 1, hf, self.ahead) if self.ahead and l + 1 < n_layers else None
+                rows2 = self._guess(l + 2, hf, self.prefetch2) if self.prefetch2 and l + 2 < n_layers else None
+                if rows1 is not None:
+                    guesses = self._union(rows1, self.ahead)
+                    self.cache.note_guesses(guesses, l + 1)
+                    if self.trace is not None:
+                        self.trace.append(("guess", l + 1, guesses))
+
+                def issue(rows1=rows1, rows2=rows2, l=l):
+                    if self.prefetch and rows1 is not None:
+                        self.cache.prefetch(self._union(rows1, self.prefetch), l + 1)
+                    if rows2 is not None:
+                        self.cache.prefetch(self._union(rows2, self.prefetch2), l + 2)
+                y = layer.forward(h, self._logits(l, hf), after_reads=issue)
+                if self.trace is not None:
+                    self.trace.append(("lookup", l, list(layer.last_lookup[0])))
+                h = (hf + y.float()).to(torch.bfloat16)
         return h
 
     def close(self):

@@ -395,10 +395,12 @@ def moe_work_bytes(t, topk, dim, inter):
 
 
 def moe_experts(x, slots, pick, weights, fmt, dim, inter, shared=-1, limit=0.0, official=False, out_f32=False,
-                work=None, out=None, shared_fmt=-1):
+                work=None, out=None, shared_fmt=-1, stream=None, slot_ready=None, phase=0):
     """Expert part of a routed MoE layer. slots: list of device uint8 slot tensors (or raw device
     addresses); pick: [t][topk] indices into slots; weights: [t][topk] floats; shared: slot index of
-    the always-on expert or -1; shared_fmt: its format when it differs from the routed experts'."""
+    the always-on expert or -1; shared_fmt: its format when it differs from the routed experts'.
+    phase 1 / 2 with slot_ready (one flag per slot): the experts of ready slots, then the others and
+    the combine (stbl_amd_moe_experts_phase); both calls need the same out and work."""
     _need(x, torch.bfloat16, "x")
     x2 = _rows2(x)
     t = x2.shape[0]
@@ -412,16 +414,25 @@ def moe_experts(x, slots, pick, weights, fmt, dim, inter, shared=-1, limit=0.0, 
         work = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
     y = out if out is not None else torch.empty((t, dim), dtype=torch.float32 if out_f32 else torch.bfloat16,
                                                 device=x.device)
-    _lib.check(_lib.load().stbl_amd_moe_experts(fmt, _ptr(y), _ptr(x2), t, dim, inter, arr, len(addrs), pk, wt, topk,
-                                                shared, int(shared_fmt), float(limit), int(official), int(out_f32),
-                                                _ptr(work), _stream()), "moe_experts")
+    if phase == 0:
+        _lib.check(_lib.load().stbl_amd_moe_experts(fmt, _ptr(y), _ptr(x2), t, dim, inter, arr, len(addrs), pk, wt,
+                                                    topk, shared, int(shared_fmt), float(limit), int(official),
+                                                    int(out_f32), _ptr(work), _stream(stream)), "moe_experts")
+        return y
+    if slot_ready is None or len(slot_ready) != len(addrs):
+        raise ValueError("moe_experts: phases 1 and 2 need one slot_ready flag per slot")
+    rd = (ctypes.c_int * len(addrs))(*[1 if r else 0 for r in slot_ready])
+    _lib.check(_lib.load().stbl_amd_moe_experts_phase(fmt, _ptr(y), _ptr(x2), t, dim, inter, arr, len(addrs), pk, wt,
+                                                      topk, shared, int(shared_fmt), float(limit), int(official),
+                                                      int(out_f32), rd, int(phase), _ptr(work), _stream(stream)),
+               f"moe_experts phase {phase}")
     return y
 
 
 SCORE_SIGMOID, SCORE_SQRT_SOFTPLUS = 0, 1
 
 
-def route(logits, topk, bias=None, route_scale=1.0, want_scores=False, score_fn=SCORE_SIGMOID):
+def route(logits, topk, bias=None, route_scale=1.0, want_scores=False, score_fn=SCORE_SIGMOID, stream=None):
     """Device router: (ids int32 [t, topk], weights fp32 [t, topk][, scores fp32 [t, E]]). score_fn:
     SCORE_SIGMOID (the configuration's) or SCORE_SQRT_SOFTPLUS (the reference engine's)."""
     _need(logits, torch.float32, "logits", 2)
@@ -432,7 +443,7 @@ def route(logits, topk, bias=None, route_scale=1.0, want_scores=False, score_fn=
     if bias is not None:
         _need(bias, torch.float32, "bias", 1)
     _lib.check(_lib.load().stbl_amd_route(_ptr(logits), _ptr(bias), t, e, topk, float(route_scale), int(score_fn),
-                                          _ptr(ids), _ptr(w), _ptr(sc), _stream()), "route")
+                                          _ptr(ids), _ptr(w), _ptr(sc), _stream(stream)), "route")
     return (ids, w, sc) if want_scores else (ids, w)
 
 

@@ -90,7 +90,7 @@ def _zero_args(argtypes):
 
 _NO_ERROR_ON_ZERO = {"stbl_amd_version", "stbl_amd_last_error", "stbl_amd_expert_layout", "stbl_amd_moe_work_bytes",
                      "stbl_amd_gemm_work_bytes", "stbl_amd_cache_destroy", "stbl_amd_gguf_close",
-                     "stbl_amd_cache_peek"}
+                     "stbl_amd_cache_peek", "stbl_amd_read_floor_sink_words"}
 
 
 @pytest.mark.parametrize("name", sorted(n for n in _lib.SIGNATURES if n not in _NO_ERROR_ON_ZERO))
@@ -106,3 +106,30 @@ def test_every_entry_point_rejects_null_and_zero_arguments(name):
     if ret is not None and r is not None:
         assert (r < 0) if isinstance(r, int) else not r, f"{name} returned {r}"
     assert code != 0 and msg, f"{name} recorded no error"
+
+
+def test_moe_experts_host_jobs_at_the_largest_step():
+    # The host side of stbl_amd_moe_experts builds its job tables before any launch: 16 tokens x
+    # top-16 whose every pick is the shared slot of another format (272 pairs, 68 shared-format
+    # jobs) must fit them. Without a GPU the call then fails at the launch with "no device"; on a
+    # machine with a GPU this would launch on fake pointers, so it is skipped there.
+    import torch
+
+    if torch.cuda.device_count() > 0:
+        pytest.skip("needs a machine without a GPU (fake device pointers)")
+    lib = _lib.load()
+    _lib.last_error()
+    P = ctypes.c_void_p
+    t, topk = 16, 16
+    slots = (P * 2)(0x10000, 0x20000)
+    pk = (ctypes.c_int * (t * topk))(*([1] * (t * topk)))
+    wt = (ctypes.c_float * (t * topk))(*([0.1] * (t * topk)))
+    st = lib.stbl_amd_moe_experts(0, P(0x30000), P(0x40000), t, 256, 128, slots, 2, pk, wt, topk, 1, 2, 0.0, 0, 0,
+                                  P(0x50000), None)
+    code, msg = _lib.last_error()
+    assert st < 0 and "moe_experts launch" in msg, (st, msg)
+    # phases 1 and 2 need the ready flags; phase 3 does not exist
+    for phase, ready in ((1, None), (3, (ctypes.c_int * 2)(1, 0))):
+        st = lib.stbl_amd_moe_experts_phase(0, P(0x30000), P(0x40000), t, 256, 128, slots, 2, pk, wt, topk, 1, 2, 0.0,
+                                            0, 0, ready, phase, P(0x50000), None)
+        assert st < 0 and "phase" in _lib.last_error()[1]

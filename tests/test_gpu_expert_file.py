@@ -13,6 +13,7 @@ under the repository, so the aligned-read path runs too.
 import os
 import pathlib
 import shutil
+from collections import OrderedDict
 
 import numpy as np
 import pytest
@@ -288,3 +289,63 @@ def test_moe_stack_stale_router_prefetch(gpu, tmp_path):
     assert plain.cache.stats()["hits"] + plain.cache.stats()["misses"] == ahead.cache.stats()["hits"] + ahead.cache.stats()["misses"]
     plain.close()
     ahead.close()
+
+
+def _replay_lookahead(trace, slots):
+    """Host replay of the lookahead counters (stbl/model.cu:452-460) over a stack's trace, on the
+    plain LRU of a cache without prefetch: keys (layer, expert); a guess's cold flags are taken when
+    it is noted; the next lookup of its layer counts it, before its own misses are mapped."""
+    lru, la, noted = OrderedDict(), [0, 0, 0, 0], {}
+    for kind, layer, ids in trace:
+        if kind == "guess":
+            noted[layer] = (ids, [(layer, e) not in lru for e in ids])
+            continue
+        if layer in noted:
+            guess, cold = noted.pop(layer)
+            la[0] += sum(cold)
+            la[1] += sum(1 for e, c in zip(guess, cold) if c and e in ids)
+            miss = [e for e in ids if (layer, e) not in lru]
+            la[2] += len(miss)
+            la[3] += sum(1 for e in miss if e in guess)
+        for e in ids:
+            if (layer, e) in lru:
+                lru.move_to_end((layer, e))
+        for e in ids:
+            k = (layer, e)
+            if k in lru:
+                lru.move_to_end(k)
+            else:
+                if len(lru) >= slots:
+                    lru.popitem(last=False)
+                lru[k] = True
+    return la
+
+
+def test_moe_stack_prefetch2_and_lookahead(gpu, tmp_path):
+    # four layers: guesses for the next layer are noted for the lookahead counters (STBL_LOOKAHEAD)
+    # and, with prefetch, read in the background, with prefetch2 also the layer after next's
+    # (STBL_PREFETCH2, stbl/model.cu:437-442, 573-583). Outputs are bit-identical to the stack that
+    # only counts; its counters equal a host replay of its guesses and lookups.
+    dim, inter, n, topk, slots, n_layers = 256, 128, 16, 3, 12, 4
+    path = tmp_path / "ahead2.gguf"
+    expert_file(path, dim, inter, n_layers, n, seed=61, make=quantized_parts)
+    routers = [data.normal((n, dim), 0.05, seed=80 + l).to(gpu) for l in range(n_layers)]
+    shared = direct_slot(quantized_parts(dim, inter, 89), dim, inter, gpu).to(gpu)
+    mk = lambda **kw: MoEStack(ExpertCache.from_gguf(slots, path, n_layers=n_layers, readers=2), ops.FP4, dim, inter, n,
+                               topk, routers, shared_slots=[shared] * n_layers, **kw)
+    counting = mk(lookahead=5, trace=True)
+    ahead2 = mk(prefetch=5, prefetch2=3)
+    for token in range(8):
+        h = data.activation(1 + token % 2, dim, seed=900 + token).to(gpu)
+        a, b = counting.step(h), ahead2.step(h)
+        assert torch.equal(a, b), f"token {token}"
+    la = counting.cache.lookahead()
+    assert list(la.values()) == _replay_lookahead(counting.trace, slots)
+    assert la["cold_guesses"] > 0 and la["misses"] > 0 and la["misses_guessed"] > 0
+    la2 = ahead2.cache.lookahead()
+    assert la2["cold_guesses"] >= la2["cold_guesses_routed"] and la2["misses"] >= la2["misses_guessed"]
+    st = ahead2.cache.prefetch_stats()
+    assert st["issued"] > 0 and st["routed_landed"] + st["routed_reading"] > 0
+    assert counting.cache.stats()["lookups"] == ahead2.cache.stats()["lookups"] == 8 * n_layers
+    counting.close()
+    ahead2.close()

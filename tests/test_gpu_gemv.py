@@ -102,10 +102,11 @@ def test_gemv_fp4_zero_and_extreme_inputs(gpu):
 @pytest.mark.parametrize("rows,k,round_out", [(1000, 1280, 1), (2048, 7168, 0), (64, 96, 1),
                                                # the attention-side shapes of stbl/bench_gemv.py:103-107
                                                (32768, 1280, 1), (5120, 8192, 1), (1280, 5120, 0), (512, 5120, 1),
-                                               (16388, 1280, 1)])
+                                               (16388, 1280, 1), (999, 1280, 1)])
 def test_stbl_gemv_fp8_e8m0(gpu, rows, k, round_out):
     # stbl/test_kernels.py:82-98 input idiom: e4m3 weights, E8M0 scales 2^U[-14,-7] per 32x32;
-    # 16388 x 1280 takes 8-row tiles, the last one half full
+    # 16388 x 1280 takes 8-row tiles, the last one half full; 999 x 1280 2-row tiles, the last one
+    # half full; 64 x 96 1-row tiles
     rng = np.random.default_rng(rows)
     w = np.clip(rng.standard_normal((rows, k)) * 100, -448, 448).astype(np.float32)
     codes = oracle.e4m3_encode(w)
@@ -126,9 +127,11 @@ def test_stbl_gemv_fp8_e8m0(gpu, rows, k, round_out):
         assert_gemv(got, None, want)
 
 
-@pytest.mark.parametrize("rows,k", [(512, 2560), (2048, 7168), (7168, 2048)])
+@pytest.mark.parametrize("rows,k", [(512, 2560), (2048, 7168), (7168, 2048), (64, 256), (999, 2560)])
 def test_stbl_gemv_mxfp4_gguf(gpu, rows, k):
-    # stbl/test_kernels.py:101-117: random codes, scale bytes 118..125, repacked to GGUF blocks
+    # stbl/test_kernels.py:101-117: random codes, scale bytes 118..125, repacked to GGUF blocks;
+    # small matrices whose 4-row tiles would leave CUs idle take 1-row (64 x 256) or 2-row tiles
+    # (999 x 2560, the last tile half full)
     rng = np.random.default_rng(k)
     codes = rng.integers(0, 256, (rows, k // 2), dtype=np.uint8)
     sc = rng.integers(118, 126, (rows, k // 32), dtype=np.uint8)
@@ -141,10 +144,12 @@ def test_stbl_gemv_mxfp4_gguf(gpu, rows, k):
     assert_gemv(got, got, want, tol=2.0 ** -8)
 
 
-@pytest.mark.parametrize("rows,k,n", [(256, 1024, 16), (2304, 5120, 12), (5120, 2304, 6), (2300, 5120, 16)])
+@pytest.mark.parametrize("rows,k,n", [(256, 1024, 16), (2304, 5120, 12), (5120, 2304, 6), (2300, 5120, 16),
+                                      (40, 512, 3)])
 def test_stbl_gemv_mxfp4_batch(gpu, rows, k, n):
     # small; the reference engine's V4.1 expert batches (12 gate/up, 6 down matrices), which take 16-
-    # and 8-row tiles; and 16-row tiles with the last one 12 rows full
+    # and 8-row tiles; 16-row tiles with the last one 12 rows full; three 40 x 512 matrices in
+    # 1-row tiles
     rng = np.random.default_rng(3)
     ys, ws, xs, wants = [], [], [], []
     for j in range(n):

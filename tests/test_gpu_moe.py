@@ -170,6 +170,33 @@ def test_expert_ffn_fp8_e8m0(gpu, dim, inter, official):
         assert_gemv(y32[t], y16[t], raw)
 
 
+def test_moe_experts_routed_picks_of_the_shared_slot_and_phases(gpu):
+    # 16 tokens x top-16 whose picks repeat the shared slot (FP8 E8M0, the routed experts FP4): the
+    # shared format's jobs, up to one per 4 of the 272 (token, pick) pairs, run in launches of their
+    # own. Checked against the oracle, and the two-phase call (slots 1 and 3 "ready") against one call.
+    dim, inter, topk, t = 256, 128, 16, 16
+    routed = [make_expert(ops.FP4, dim, inter, seed=820 + 3 * i, gpu=gpu) for i in range(3)]
+    shared = make_expert(ops.FP8_E8M0, dim, inter, seed=850, gpu=gpu)
+    slots = [r[0] for r in routed] + [shared[0]]
+    rng = np.random.default_rng(85)
+    pick = [[int(v) for v in rng.choice([0, 1, 2, 3, 3, 3], size=topk)] for _ in range(t)]
+    w = (rng.random((t, topk)) / topk).astype(np.float32)
+    x = data.activation(t, dim, seed=86)
+    kw = dict(shared=3, shared_fmt=ops.FP8_E8M0, limit=10.0)
+    y = ops.moe_experts(x.to(gpu), slots, pick, w.tolist(), ops.FP4, dim, inter, **kw)
+    mats = [deq_parts(ops.FP4, r[1]) for r in routed] + [deq_parts(ops.FP8_E8M0, shared[1])]
+    want = oracle.moe_deq([[mats[i] for i in row] for row in pick], w, mats[3], x.float().numpy(), limit=10.0)
+    u = bf16_ulps(np_(y), want)
+    assert u.max() <= 1 and u.mean() < 0.02, (u.max(), u.mean())
+    ready = [False, True, False, True]
+    work = torch.empty(ops.moe_work_bytes(t, topk, dim, inter), dtype=torch.uint8, device=gpu)
+    y2 = torch.full((t, dim), float("nan"), dtype=torch.bfloat16, device=gpu)
+    for phase in (1, 2):
+        ops.moe_experts(x.to(gpu), slots, pick, w.tolist(), ops.FP4, dim, inter, work=work, out=y2, slot_ready=ready,
+                        phase=phase, **kw)
+    assert torch.equal(y, y2)
+
+
 @pytest.mark.parametrize("t", [1, 4])
 def test_moe_v41_semantics(gpu, t):
     # the reference engine's MoE at V4.1 shapes (stbl/bench_gemv.py:15): dim 5120, inter 2304, top-6,
@@ -270,6 +297,54 @@ def test_cache_lru_matches_oracle(gpu):
     assert st["hits"] + st["misses"] == 800 and st["in_use"] == slots
     assert st["refill_bytes"] == st["misses"] * sb
     cache.close()
+
+
+def test_cache_lookup_begin_end(gpu):
+    # the lookup in two calls: begin maps and queues the refills and says which slots may be read at
+    # once (pool tier: the hits), end makes the compute stream wait for the refills
+    n, slots, sb = 12, 4, 4096
+    cache = ExpertCache(slots, sb, pinned_pool(n, sb), n)
+    ptrs, hits, ready, nmiss = cache.lookup_begin([0, 1])
+    assert hits == [False, False] and ready == [False, False] and nmiss == 2
+    with pytest.raises(Exception, match="not ended"):
+        cache.lookup_begin([2])
+    cache.lookup_end()
+    cache.lookup_end()  # nothing open: a no-op
+    cache.mark_used()
+    ptrs, hits, ready, nmiss = cache.lookup_begin([1, 2, 0])
+    assert hits == [True, False, True] and ready == hits and nmiss == 1
+    cache.lookup_end()
+    cache.mark_used()
+    torch.cuda.synchronize()
+    for e, p in zip([1, 2, 0], ptrs):
+        assert read_device(p, 8).tolist()[:4] == [e, 255 - e, 7, 9]
+    # lookahead counters (stbl/model.cu:452-460): guesses 3 and 5 are uncached when noted, 0 cached
+    cache.note_guesses([3, 0, 5], layer=0)
+    cache.lookup([5, 6, 0])  # 5: a cold guess, routed, a miss; 6: an unguessed miss; 0: a hit
+    cache.mark_used()
+    assert cache.lookahead() == {"cold_guesses": 2, "cold_guesses_routed": 1, "misses": 2, "misses_guessed": 1}
+    cache.lookup([7])  # no guesses noted for this lookup: nothing counted
+    cache.mark_used()
+    assert cache.lookahead()["misses"] == 2
+    cache.close()
+
+
+def test_route_nan_logits(gpu):
+    # NaN keys rank below every number (the oracle's rule): a token with fewer than k numeric keys
+    # takes the lowest unused ids next, and NaN scores make its weights NaN
+    t, e, topk = 3, 64, 8
+    logits = data.zipf_logits(t, e, seed=19)
+    logits[0, [3, 7, 11]] = float("nan")
+    logits[1, :] = float("nan")
+    logits[1, [30, 5, 17, 22, 9]] = torch.tensor([2.0, -1.0, 0.5, 0.5, 3.0])
+    logits[2, :] = float("nan")
+    ids, w = ops.route(logits.to(gpu), topk)
+    _, oids, ow = oracle.route(logits.numpy(), topk)
+    assert np_(ids).tolist() == oids.tolist()
+    assert np_(ids)[2].tolist() == list(range(topk))
+    got = np_(w)
+    assert np.array_equal(np.isnan(got), np.isnan(ow)) and np.all(np.isnan(got[1:]))
+    assert np.allclose(got[0], ow[0], rtol=8 * 2.0 ** -24, atol=0)
 
 
 def test_cache_refill_failure_leaves_slot_unmapped(gpu):

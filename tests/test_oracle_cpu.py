@@ -318,6 +318,27 @@ def test_route_sqrt_softplus_brute_force():
         assert np.array_equal(w[i], ww.astype(np.float32))
 
 
+def test_route_nan_keys_rank_last():
+    # NaN logits (a NaN hidden state) give NaN keys: they rank below every number, so a token with
+    # fewer numeric keys than k takes the lowest unused ids next (ties to the lower id); weights
+    # that sum a NaN score come out NaN. Checked by brute force over (key or -inf, id).
+    rng = np.random.default_rng(25)
+    t, e, k = 3, 40, 8
+    logits = rng.standard_normal((t, e)).astype(np.float32)
+    logits[0, [3, 7, 11]] = np.nan           # three NaN keys among numeric ones
+    logits[1, :] = np.nan
+    logits[1, [30, 5, 17, 22, 9]] = [2.0, -1.0, 0.5, 0.5, 3.0]  # five numeric keys, one tie
+    logits[2, :] = np.nan                    # no numeric key at all
+    sc, ids, w = oracle.route(logits, k)
+    for i in range(t):
+        key = [(-np.float64(sc[i, j]) if not np.isnan(sc[i, j]) else np.inf, j) for j in range(e)]
+        assert ids[i].tolist() == [j for _, j in sorted(key)[:k]]
+    assert ids[1].tolist() == [9, 30, 17, 22, 5, 0, 1, 2]
+    assert ids[2].tolist() == list(range(k))
+    assert np.all(np.isfinite(w[0]))  # its 8 best keys are numeric
+    assert np.all(np.isnan(w[1])) and np.all(np.isnan(w[2]))
+
+
 def test_quant_fp8_e8m0_b32_properties():
     rng = np.random.default_rng(22)
     rows, k = 70, 96  # a partial last row block
@@ -353,14 +374,17 @@ def _fp4_slot(rng, dim, inter):
     return np.concatenate(parts), mats
 
 
-def _ffn_numpy(mats, x, w, official):
+def _ffn_numpy(mats, x, w, official, limit=0.0):
     """stbl/model.cu:536-539 composition with dense float64 products: g, u rounded to bf16, SwiGLU
-    with the route weight, optional act_quant of the input and of the SwiGLU output, bf16 output."""
+    with the route weight (g capped at limit, u clamped to +-limit when limit > 0,
+    stbl/kernels.cu:444-459), optional act_quant of the input and of the SwiGLU output, bf16 output."""
     wg, wu, wd = mats
     if official:
         x = oracle.act_quant(x[None], 32, True)[2][0]
     g = oracle.bf16_round((wg.astype(np.float64) @ x.astype(np.float64)).astype(np.float32))
     u = oracle.bf16_round((wu.astype(np.float64) @ x.astype(np.float64)).astype(np.float32))
+    if limit > 0:
+        g, u = np.minimum(g, np.float32(limit)), np.clip(u, -np.float32(limit), np.float32(limit))
     gt = torch.from_numpy(g)
     h = ((gt / (1 + torch.exp(-gt))) * torch.from_numpy(u) * w).to(torch.bfloat16).float().numpy()
     if official:
@@ -421,6 +445,89 @@ def test_moe_deq_equals_fp4_path():
     b = oracle.moe_deq([[slots[e][1] for e in row] for row in picks], wts, slots[3][1], x, 2.0, True)
     assert np.all(np.abs(a - b) <= np.abs(a) * 2.0 ** -7 + 1e-30)
     assert np.mean(a == b) > 0.99
+
+
+def _fp8_parts(rng, dim, inter):
+    """(gate, up, down) as (e4m3 codes, fp32 128x128 scales) from the oracle's quantizer, and their
+    dequantized matrices. Each 128x128 block gets its own magnitude, so every block scale matters."""
+    parts, mats = [], []
+    for rows, k in ((inter, dim), (inter, dim), (dim, inter)):
+        w = rng.standard_normal((rows, k)).astype(np.float32) * np.float32(0.02)
+        gain = rng.uniform(0.25, 4.0, ((rows + 127) // 128, (k + 127) // 128)).astype(np.float32)
+        w *= np.repeat(np.repeat(gain, 128, 0), 128, 1)[:rows, :k]
+        c, s = oracle.quant_fp8_b128(w)
+        parts.append((c, s))
+        mats.append(oracle.dequant_fp8_b128(c, s))
+    return parts, mats
+
+
+@pytest.mark.parametrize("official,limit", [(False, 0.0), (True, 0.0), (False, 0.25), (True, 0.25)])
+def test_expert_ffn_fp8_composition(official, limit):
+    # orc_expert_ffn_fp8 (FP8 weights with 128x128 fp32 block scales) against the dense float64
+    # composition of stbl/model.cu:536-539 on its dequantized matrices, and against the
+    # format-independent composition; limit 0.25 caps g and clamps u in most rows
+    rng = np.random.default_rng(31)
+    dim, inter = 384, 256
+    parts, mats = _fp8_parts(rng, dim, inter)
+    x = oracle.bf16_round(rng.standard_normal(dim).astype(np.float32))
+    got = oracle.expert_ffn_fp8(*parts, dim, inter, x, 0.7, limit, official)
+    want = _ffn_numpy(mats, x, 0.7, official, limit)
+    close = lambda a, b: np.abs(a - b) <= np.abs(b) * 2.0 ** -7 + 1e-30
+    assert np.all(close(got, want))
+    assert np.mean(got == want) > 0.9
+    deq = oracle.expert_ffn_deq(*mats, x, 0.7, limit, official)
+    assert np.all(close(got, deq))
+    assert np.mean(got == deq) > 0.99
+    # a planted mistake, gate and up passed swapped, fails that bar
+    bad = oracle.expert_ffn_fp8(parts[1], parts[0], parts[2], dim, inter, x, 0.7, limit, official)
+    assert np.mean(close(bad, want)) < 0.5
+
+
+@pytest.mark.parametrize("official,limit", [(False, 0.0), (True, 0.0), (False, 0.25)])
+def test_expert_ffn_fp8_intermediate_exact(official, limit):
+    # A down matrix that dequantizes to the identity (e4m3 code 0x38 = 1.0 on the diagonal, block
+    # scales 1) makes the raw output the SwiGLU intermediate itself, so it is checked bit for bit:
+    # g and u each rounded to bf16, the SwiGLU of stbl/kernels.cu:444-459 with the route weight
+    # (pinned on its own), and in official mode act_quant(h, 32) (stbl/model.cu:538)
+    rng = np.random.default_rng(32)
+    dim = inter = 256
+    parts, mats = _fp8_parts(rng, dim, inter)
+    eye = np.zeros((dim, inter), np.uint8)
+    np.fill_diagonal(eye, 0x38)
+    parts[2] = (eye, np.ones((2, 2), np.float32))
+    assert np.array_equal(oracle.dequant_fp8_b128(*parts[2]), np.eye(dim, dtype=np.float32))
+    x = oracle.bf16_round(rng.standard_normal(dim).astype(np.float32) * 2)
+    _, h = oracle.expert_ffn_fp8(*parts, dim, inter, x, 0.7, limit, official, raw=True)
+    h = h.astype(np.float32)
+    xin = oracle.act_quant(x[None], 32, True)[2][0] if official else x
+    gsum, usum = (m.astype(np.float64) @ xin.astype(np.float64) for m in mats[:2])
+    g, u = (oracle.bf16_round(v.astype(np.float32)) for v in (gsum, usum))
+
+    def swiglu_h(g, u, w):
+        out = oracle.swiglu(g, u, w, limit)
+        return oracle.act_quant(out[None], 32, True)[2][0] if official else out
+
+    assert np.array_equal(h, swiglu_h(g, u, 0.7))
+    if not official:  # (act_quant's 3-bit mantissa would hide the smaller mistakes)
+        # each planted mistake changes the intermediate: g not rounded to bf16, gate and up
+        # swapped, the route weight dropped
+        assert np.mean(h != swiglu_h(gsum.astype(np.float32), u, 0.7)) > 0.05
+        assert np.mean(h != swiglu_h(u, g, 0.7)) > 0.5
+        assert np.mean(h != swiglu_h(g, u, 1.0)) > 0.5
+
+
+def test_fp4_gemm_torch_matches_the_c_restatement():
+    # the timed CPU baseline (ref/kernel.py:94-102's torch method) against the pinned C GEMV:
+    # the same exact products in another summation order, rounded to bf16
+    rng = np.random.default_rng(26)
+    n, k = 96, 512
+    codes = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    sc = rng.integers(118, 130, (n, k // 32), dtype=np.uint8)
+    x = oracle.bf16_round(rng.standard_normal((2, k)).astype(np.float32))
+    got = oracle.fp4_gemm_torch(torch.from_numpy(x), torch.from_numpy(codes), torch.from_numpy(sc)).float().numpy()
+    want = oracle.gemv_fp4(codes, sc, x)
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-30)
+    assert np.mean(got == oracle.bf16_round(want.astype(np.float32))) > 0.95
 
 
 # ---- expert LRU bookkeeping ------------------------------------------------------------------------------

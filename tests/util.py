@@ -59,6 +59,21 @@ def assert_gemv(got_f32, got_bf16, want, tol=1e-3):
     return e
 
 
+def assert_moe_sum(got_bf16, want, term_abs_sum):
+    """A routed MoE output y = bf16(sum_i o_i) against the oracle's, where each expert output o_i is
+    a bf16-rounded FFN that may sit one bf16 step from the oracle's (the fp32 sums inside take
+    another order). Every element is held to |y - want| <= 2^-7 (sum_i |o_i| + |want|): one step
+    of each term plus one of the result (a bf16 step of v is at most 2^-7 |v|). Where terms cancel
+    that allows several steps of a small y, so flips (outputs not equal to the oracle's) must also
+    stay rare."""
+    got = np.asarray(got_bf16, np.float64)
+    want = np.asarray(want, np.float64)
+    bound = 2.0 ** -7 * (np.asarray(term_abs_sum, np.float64) + np.abs(want))
+    assert np.all(np.abs(got - want) <= bound), f"{int(np.sum(np.abs(got - want) > bound))} outputs past the bound"
+    u = bf16_ulps(got, want)
+    assert np.mean(u > 0) < 0.02, f"{np.mean(u > 0):.4f} of outputs flipped"
+
+
 def read_device(addr, n):
     """n bytes at device address addr (a slot handed out by an expert cache) as a uint8 tensor,
     through the HIP runtime torch already loaded (the one libstbl_amd.so binds to)."""
