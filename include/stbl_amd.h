@@ -185,6 +185,17 @@ int stbl_amd_moe_experts_phase(int fmt, void *y, const void *x, int t, int dim, 
                                int shared_fmt, float limit, int official, int y_f32, const int *slot_ready, int phase,
                                void *work, hipStream_t st);
 
+/* stbl_amd_moe_experts without the work argument: it allocates nothing (no hipMalloc, no library
+ * allocation) and uses a static device array of the library's, 8 MiB per GPU, held until the
+ * process ends. No counterpart in the reference; it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops). Refuses (negative hipError_t) a step
+ * whose stbl_amd_moe_work_bytes(t, topk, dim, inter) exceeds 8 MiB (every step of the C4 and V4.1
+ * shapes up to 16 tokens x top-16 fits). Nothing in the scratch must start at zero. Calls that
+ * overlap in time on one GPU share that GPU's scratch and race; serialize them (one stream). */
+int stbl_amd_moe_experts_noalloc(int fmt, void *y, const void *x, int t, int dim, int inter, const void *const *slots,
+                                 int n_slots, const int *pick, const float *weights, int topk, int shared,
+                                 int shared_fmt, float limit, int official, int y_f32, hipStream_t st);
+
 /* Scratch bytes for stbl_amd_moe_experts on t tokens. */
 uint64_t stbl_amd_moe_work_bytes(int t, int topk, int dim, int inter);
 

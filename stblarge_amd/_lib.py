@@ -50,6 +50,7 @@ SIGNATURES = {
     "stbl_amd_expert_ffn": (I, [I, P, P, P, I, I, I, F, F, I, I, P, P]),
     "stbl_amd_moe_experts": (I, [I, P, P, I, I, I, PP, I, PI, PF, I, I, I, F, I, I, P, P]),
     "stbl_amd_moe_experts_phase": (I, [I, P, P, I, I, I, PP, I, PI, PF, I, I, I, F, I, I, PI, I, P, P]),
+    "stbl_amd_moe_experts_noalloc": (I, [I, P, P, I, I, I, PP, I, PI, PF, I, I, I, F, I, I, P]),
     "stbl_amd_moe_work_bytes": (U64, [I, I, I, I]),
     "stbl_amd_route": (I, [P, P, I, I, I, F, I, P, P, P, P]),
     "stbl_amd_gemm": (I, [I, P, P, P, P, I, I, I, I, I, P, P]),

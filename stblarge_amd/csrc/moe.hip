@@ -18,6 +18,8 @@
 // lane's own chunk of the activation, so it costs no launch and no memory traffic.
 // The router is k_route: sigmoid scores, top-k by score + bias with ties to the lower id, weights
 // renormalized in top-k order (stbl/model.cu:444-451, :528-530 with sigmoid for sqrt-softplus).
+#include <mutex>
+
 #include "abi_util.hpp"
 #include "expert_layout.hpp"
 #include "gemv_core.hpp"
@@ -597,10 +599,65 @@ int stbl_amd_moe_experts_phase(int fmt, void *y, const void *x, int t, int dim, 
                             official, y_f32, slot_ready, phase, work, st);
 }
 
+// ---- the MoE step without a caller workspace --------------------------------------------------------
+
+// Device scratch of stbl_amd_moe_experts_noalloc: the SwiGLU intermediates and expert outputs of one
+// call (what `work` holds for stbl_amd_moe_experts), at most kMoeScratchBytes. Each GPU the library
+// runs on holds its own copy until the process ends; every call on a GPU uses that GPU's copy.
+constexpr uint64_t kMoeScratchBytes = 8ull << 20;
+static __device__ __align__(256) uint8_t scratch[kMoeScratchBytes];
+
+// The current device's address of `scratch`, looked up once per device (the array's name in host
+// code is not a device address). nullptr on failure, recorded for stbl_amd_last_error.
+static void *scratch_address() {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void *addr[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        abi_status(e, "moe_experts_noalloc: hipGetDevice");
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        abi_fail(hipErrorInvalidDevice, "moe_experts_noalloc: device %d beyond %d", dev, kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    if (!addr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            abi_status(e != hipSuccess ? e : hipErrorInvalidSymbol, "moe_experts_noalloc: hipGetSymbolAddress(scratch)");
+            return nullptr;
+        }
+        addr[dev] = p;
+    }
+    return addr[dev];
+}
+
 // Scratch bytes stbl_amd_moe_experts needs for t tokens.
 uint64_t stbl_amd_moe_work_bytes(int t, int topk, int dim, int inter) {
     const uint64_t pairs = (uint64_t)t * (topk + 1);
     return align256(pairs * inter * 2) + align256(pairs * dim * 2);
+}
+
+// stbl_amd_moe_experts with the library's static device scratch instead of `work`: no allocation
+// of any kind, for callers that cannot allocate. Refuses steps whose scratch would exceed
+// kMoeScratchBytes. Calls that overlap on one GPU share its scratch and race.
+int stbl_amd_moe_experts_noalloc(int fmt, void *y, const void *x, int t, int dim, int inter, const void *const *slots,
+                                 int n_slots, const int *pick, const float *weights, int topk, int shared,
+                                 int shared_fmt, float limit, int official, int y_f32, hipStream_t st) {
+    if (t < 1 || t > kMoeMaxT || topk < 1 || topk + 1 > kMoeMaxPick || dim < 1 || inter < 1)
+        return abi_fail(hipErrorInvalidValue, "moe_experts_noalloc: need 1 <= t <= 16, 1 <= topk <= 16, dims > 0");
+    const uint64_t need = stbl_amd_moe_work_bytes(t, topk, dim, inter);
+    if (need > kMoeScratchBytes)
+        return abi_fail(hipErrorInvalidValue, "moe_experts_noalloc: the step needs %llu bytes of scratch, more than the %llu it has",
+                        (unsigned long long)need, (unsigned long long)kMoeScratchBytes);
+    void *work = scratch_address();
+    if (!work) return -(int)hipErrorInvalidSymbol;
+    return moe_experts_impl(fmt, y, x, t, dim, inter, slots, n_slots, pick, weights, topk, shared, shared_fmt, limit,
+                            official, y_f32, nullptr, 0, work, st);
 }
 
 // stbl/kernels.h:34: s[i] = sqrt(softplus(s[i])) in place, the engine's router scores.
