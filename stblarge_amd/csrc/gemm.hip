@@ -20,6 +20,8 @@
 // (column r of B); e4m3 operands hold K bytes [16g, 16g+16) and [64+16g, 64+16g+16) of the 128-K
 // step, e2m1 operands K elements [32g, 32g+32) (low nibble first); the lane's E8M0 scale covers K
 // block [32g, 32g+32); D lane l holds rows 4g..4g+3 of column r.
+#include <algorithm>
+
 #include "abi_util.hpp"
 #include "common.hpp"
 
@@ -28,9 +30,6 @@ namespace stbl {
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kGemmMaxM = 64;
-constexpr int kGemmWaveSteps = 2;                  // 128-K steps per wave
-constexpr int kGemmWgSteps = 4 * kGemmWaveSteps;   // per workgroup (one slice of K)
-constexpr int kGemmTileVecs = 16 * 64;  // f32x4 per 64 x 64 tile, in the order k_gemm's threads hold them
 constexpr int kGemmMaxN = 1 << 20;
 
 // ---- activation quantization --------------------------------------------------------------------
@@ -70,38 +69,40 @@ __global__ __launch_bounds__(256) void k_act_quant_e4m3(const uint16_t *__restri
 
 // ---- GEMM ---------------------------------------------------------------------------------------
 
-// One workgroup owns a 64 x 64 output tile (4 m-tiles x 4 n-tiles of 16 x 16) and a slice of up to
-// 4 SW 128-K steps (SW = kGemmWaveSteps); wave w takes SW consecutive steps of the slice and
-// accumulates all 16 tiles in registers, loading its activations and weights straight from global
-// memory (no operand is shared between waves, so nothing is staged through LDS). All loads of a
-// wave are issued before its first MFMA, from addresses clamped into the buffers; a step past the
-// slice gets zero operands instead of a branch. The 4 waves' tiles are summed through LDS in wave
-// order. With one slice the workgroup writes Y; otherwise it writes its slice's partial tile and
-// k_gemm_reduce adds the slices in order. (Summing the slices in the last workgroup to finish needs
-// an agent-scope release/acquire per workgroup, which writes back and invalidates the XCD's L2 each
-// time: measured at about 4x the whole GEMM, so the kernel boundary is the synchronization point.)
-// Workgroup b takes tile b % ntiles and slice b / ntiles: with ntiles % 8 == 0 every slice of a tile
-// runs on one XCD (workgroups go round-robin over the 8 XCDs), which shares its activation reads.
-// A rows are lda bytes apart.
-template <bool FP4W, int SW>
-__global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ wc, const void *__restrict__ ws,
-                                              const uint8_t *__restrict__ aq, const uint8_t *__restrict__ as_,
-                                              f32x4 *__restrict__ part, void *__restrict__ y, int y_f32, int M,
-                                              int N, int K, int lda, int act_shift, int ntiles, int slices,
-                                              int steps_wg) {
-    __shared__ f32x4 red[4 * kGemmTileVecs];
+// One workgroup owns a 64 x 16 NT output tile (4 m-tiles x NT n-tiles of 16 x 16) and a slice of up
+// to NW * SW 128-K steps; wave w takes SW consecutive steps of the slice and accumulates its NT * 4
+// tiles in registers, loading its activations and weights straight from global memory (no operand is
+// shared between waves, so nothing is staged through LDS). All loads of a wave are issued before its
+// first MFMA, from addresses clamped into the buffers; a step past the slice gets zero operands
+// instead of a branch. The waves' tiles are summed through LDS in wave order. With one slice the
+// workgroup writes Y; otherwise it writes its slice's partial tile and k_gemm_reduce adds the slices
+// in order. (Summing the slices in the last workgroup to finish needs an agent-scope release/acquire
+// per workgroup, which writes back and invalidates the XCD's L2 each time: measured at about 4x the
+// whole GEMM, so the kernel boundary is the synchronization point.) Workgroup b takes tile b % ntiles
+// and slice b / ntiles: with ntiles % 8 == 0 every slice of a tile runs on one XCD (workgroups go
+// round-robin over the 8 XCDs), which shares its activation reads. A rows are lda bytes apart.
+// Partial tiles and the LDS sum hold f32x4 q = t * 64 + lane with t = m-tile * NT + n-tile.
+template <bool FP4W, int NT, int NW, int SW>
+__global__ __launch_bounds__(NW * 64) void k_gemm(const uint8_t *__restrict__ wc, const void *__restrict__ ws,
+                                                  const uint8_t *__restrict__ aq, const uint8_t *__restrict__ as_,
+                                                  f32x4 *__restrict__ part, void *__restrict__ y, int y_f32, int M,
+                                                  int N, int K, int lda, int act_shift, int ntiles, int slices,
+                                                  int steps_wg) {
+    constexpr int kTileVecs = 4 * NT * 64;
+    constexpr int kThreads = NW * 64;
+    __shared__ f32x4 red[NW * kTileVecs];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
     const int tile = blockIdx.x % ntiles, slice = blockIdx.x / ntiles;
-    const int n0 = tile * 64, KS = K >> 7;
-    const int wsteps = (steps_wg + 3) >> 2;
+    const int n0 = tile * 16 * NT, KS = K >> 7;
+    const int wsteps = (steps_wg + NW - 1) / NW;
     const int s0 = slice * steps_wg + wave * wsteps;
     const int nst = max(0, min(wsteps, min(KS, (slice + 1) * steps_wg) - s0));  // wave-uniform
 
     // 1. loads: lane (r, g) holds, per step, rows 16 mt + r of A and columns n0 + 16 nt + r of W
     u32x4 av[SW][4][2];
     uint32_t asc[SW][4];
-    u32x4 bv[SW][4][FP4W ? 1 : 2];
-    uint32_t bsc[SW][4];
+    u32x4 bv[SW][NT][FP4W ? 1 : 2];
+    uint32_t bsc[SW][NT];
     float wsc[SW];
 #pragma unroll
     for (int s = 0; s < SW; s++) {
@@ -115,7 +116,7 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ wc, co
             asc[s][mt] = as_[(size_t)m * (K >> act_shift) + ((kb + 32 * g) >> act_shift)];
         }
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++) {
+        for (int nt = 0; nt < NT; nt++) {
             const int n = min(n0 + 16 * nt + r, N - 1);
             if constexpr (FP4W) {
                 bv[s][nt][0] = *(const u32x4 *)(wc + (size_t)n * (K >> 1) + (kb >> 1) + 16 * g);
@@ -128,19 +129,19 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ wc, co
         }
         if constexpr (!FP4W) wsc[s] = ((const float *)ws)[(size_t)(n0 >> 7) * KS + (kb >> 7)];
     }
-    // 2. MFMAs, 16 independent accumulators per step
-    f32x4 acc[4][4];
+    // 2. MFMAs, 4 NT independent accumulators per step
+    f32x4 acc[4][NT];
 #pragma unroll
     for (int mt = 0; mt < 4; mt++)
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int nt = 0; nt < NT; nt++) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     const u32x4 z4 = {0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < SW; s++) {
         const bool live = s < nst;
-        i32x8 b[4];
+        i32x8 b[NT];
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++) {
+        for (int nt = 0; nt < NT; nt++) {
             const u32x4 b0 = live ? bv[s][nt][0] : z4;
             if constexpr (FP4W) {
                 b[nt] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], 0, 0, 0, 0};
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ wc, co
             const u32x4 a0 = live ? av[s][mt][0] : z4, a1 = live ? av[s][mt][1] : z4;
             const i32x8 a = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
 #pragma unroll
-            for (int nt = 0; nt < 4; nt++) {
+            for (int nt = 0; nt < NT; nt++) {
                 if constexpr (FP4W) {
                     acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b[nt], acc[mt][nt], 0, 4, 0,
                                                                                    (int)asc[s][mt], 0, (int)bsc[s][nt]);
@@ -168,44 +169,46 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ wc, co
             }
         }
     }
-    // 3. the workgroup's sum, in wave order; thread (wave, lane) keeps m-tile j, n-tile `wave`
+    // 3. the workgroup's sum, in wave order; thread tid takes q = tid + kThreads j
 #pragma unroll
-    for (int t = 0; t < 16; t++) red[(wave * 16 + t) * 64 + lane] = acc[t >> 2][t & 3];
+    for (int t = 0; t < 4 * NT; t++) red[(wave * 4 * NT + t) * 64 + lane] = acc[t / NT][t % NT];
     __syncthreads();
-    f32x4 v[4];
+    constexpr int kPer = (kTileVecs + kThreads - 1) / kThreads;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int q = tid + 256 * j;
-        v[j] = ((red[q] + red[kGemmTileVecs + q]) + red[2 * kGemmTileVecs + q]) + red[3 * kGemmTileVecs + q];
-    }
-    if (slices > 1) {
-        f32x4 *tp = part + ((size_t)tile * slices + slice) * kGemmTileVecs;
+    for (int j = 0; j < kPer; j++) {
+        const int q = tid + kThreads * j;
+        if (q >= kTileVecs) break;
+        f32x4 v = red[q];
 #pragma unroll
-        for (int j = 0; j < 4; j++) tp[tid + 256 * j] = v[j];
-        return;
-    }
-    // Y: element e of v[j] is row 16 j + 4 g + e, column n0 + 16 wave + r
-    const int n = n0 + 16 * wave + r;
-    if (n >= N) return;
-#pragma unroll
-    for (int j = 0; j < 4; j++)
+        for (int w = 1; w < NW; w++) v += red[w * kTileVecs + q];
+        if (slices > 1) {
+            part[((size_t)tile * slices + slice) * kTileVecs + q] = v;
+            continue;
+        }
+        // Y: element e of v is row 16 mt + 4 g' + e, column n0 + 16 nt + r' of the lane q % 64
+        const int t = q >> 6, ql = q & 63, mt = t / NT, nt = t % NT;
+        const int n = n0 + 16 * nt + (ql & 15);
+        if (n >= N) continue;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int m = 16 * j + 4 * g + e;
+            const int m = 16 * mt + 4 * (ql >> 4) + e;
             if (m >= M) continue;
-            if (y_f32) ((float *)y)[(size_t)m * N + n] = v[j][e];
-            else ((uint16_t *)y)[(size_t)m * N + n] = f32_to_bf16_bits(v[j][e]);
+            if (y_f32) ((float *)y)[(size_t)m * N + n] = v[e];
+            else ((uint16_t *)y)[(size_t)m * N + n] = f32_to_bf16_bits(v[e]);
         }
+    }
 }
 
 // Y = the slices' partial tiles added in slice order; thread i takes f32x4 i of every tile (the
-// layout k_gemm's threads stored them in), so partial reads are contiguous per slice.
+// layout k_gemm stored them in), so partial reads are contiguous per slice.
+template <int NT>
 __global__ __launch_bounds__(256) void k_gemm_reduce(const f32x4 *__restrict__ part, int slices, int ntiles,
                                                      void *__restrict__ y, int y_f32, int M, int N) {
+    constexpr int kTileVecs = 4 * NT * 64;
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= ntiles * kGemmTileVecs) return;
-    const int tile = i / kGemmTileVecs, q = i % kGemmTileVecs;
-    const f32x4 *tp = part + (size_t)tile * slices * kGemmTileVecs + q;
+    if (i >= ntiles * kTileVecs) return;
+    const int tile = i / kTileVecs, q = i % kTileVecs;
+    const f32x4 *tp = part + (size_t)tile * slices * kTileVecs + q;
     // slices are loaded up to 8 at a time, all loads issued before the first add (a plain loop waits
     // for each load in turn), and added in slice order
     constexpr int kBatch = 8;
@@ -214,67 +217,84 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const f32x4 *__restrict__ p
         f32x4 v[kBatch];
 #pragma unroll
         for (int i = 0; i < kBatch; i++)
-            if (sl0 + i < slices) v[i] = tp[(size_t)(sl0 + i) * kGemmTileVecs];
+            if (sl0 + i < slices) v[i] = tp[(size_t)(sl0 + i) * kTileVecs];
 #pragma unroll
         for (int i = 0; i < kBatch; i++)
             if (sl0 + i < slices) s += v[i];
     }
-    // q = tid + 256 j of the producing workgroup: m-tile j, n-tile tid / 64, lane tid % 64
-    const int j = q >> 8, t = q & 255, r = t & 15, g = (t >> 4) & 3, w = t >> 6;
-    const int n = tile * 64 + 16 * w + r;
+    const int t = q >> 6, ql = q & 63, mt = t / NT, nt = t % NT;
+    const int n = tile * 16 * NT + 16 * nt + (ql & 15);
     if (n >= N) return;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-        const int m = 16 * j + 4 * g + e;
+        const int m = 16 * mt + 4 * (ql >> 4) + e;
         if (m >= M) continue;
         if (y_f32) ((float *)y)[(size_t)m * N + n] = s[e];
         else ((uint16_t *)y)[(size_t)m * N + n] = f32_to_bf16_bits(s[e]);
     }
 }
 
-// Split of K: slices of 8 steps (2 per wave), fewer steps per slice when that leaves under 192
-// workgroups. (Unsplit tiles with 4 steps per wave, which need no partials, measured slower at
-// 7168 x 2048: 112 workgroups leave half the CUs idle.)
+// Tile shape and split of K, chosen per shape (each choice measured fastest for its shape):
+//   variant 1, 64 x 32 tiles and 16 waves of one step each, when one slice covers K (<= 16 steps)
+//     and the tiles alone give >= 192 workgroups (7168 x 2048: no partials and no second launch,
+//     11.6 -> 9.3 us against variant 0);
+//   variant 0 otherwise, 64 x 64 tiles and 8 waves of one step each, K split into slices of <= 8
+//     steps, as many as it takes to give >= 200 workgroups (2048 x 7168: 7 slices, 224 workgroups;
+//     against the earlier 4 waves of 2 steps, FP4 11.9 -> 11.6 us, FP8 12.7 -> 11.8 us).
 struct GemmPlan {
-    int ntiles, slices, steps;
+    int variant, nt, ntiles, slices, steps;
 };
 
 static GemmPlan gemm_plan(int n, int k) {
     GemmPlan p;
-    p.ntiles = (n + 63) / 64;
     const int ks = k / 128;
-    int st = kGemmWgSteps;
-    while (st > 1 && p.ntiles * ((ks + st - 1) / st) < 192) st--;
-    p.steps = st, p.slices = (ks + st - 1) / st;
+    if (ks <= 16 && (n + 31) / 32 >= 192) {
+        p.variant = 1, p.nt = 2, p.ntiles = (n + 31) / 32, p.slices = 1, p.steps = ks;
+        return p;
+    }
+    p.variant = 0, p.nt = 4, p.ntiles = (n + 63) / 64;
+    const int slices = std::max((ks + 7) / 8, std::min(ks, (200 + p.ntiles - 1) / p.ntiles));
+    p.steps = (ks + slices - 1) / slices;
+    p.slices = (ks + p.steps - 1) / p.steps;
     return p;
 }
 
 static uint64_t a256(uint64_t v) { return (v + 255) & ~(uint64_t)255; }
 
 static uint64_t part_bytes(const GemmPlan &p) {
-    return p.slices > 1 ? (uint64_t)p.ntiles * p.slices * kGemmTileVecs * 16 : 0;
+    return p.slices > 1 ? (uint64_t)p.ntiles * p.slices * (4 * p.nt * 64) * 16 : 0;
 }
 
-// Requires p.steps <= kGemmWgSteps and p.slices * p.steps covering k / 128; A rows lda bytes apart.
+template <int NT, int NW>
+static hipError_t launch_gemm_t(const GemmPlan &p, int fmt, void *y, const void *codes, const void *scales,
+                                const uint8_t *aq, int lda, const uint8_t *as_, int m, int n, int k, int shift,
+                                int y_f32, f32x4 *part, hipStream_t st) {
+    const dim3 grid(p.ntiles * p.slices);
+    if (fmt == 0)
+        hipLaunchKernelGGL((k_gemm<true, NT, NW, 1>), grid, dim3(NW * 64), 0, st, (const uint8_t *)codes, scales, aq,
+                           as_, part, y, y_f32, m, n, k, lda, shift, p.ntiles, p.slices, p.steps);
+    else
+        hipLaunchKernelGGL((k_gemm<false, NT, NW, 1>), grid, dim3(NW * 64), 0, st, (const uint8_t *)codes, scales, aq,
+                           as_, part, y, y_f32, m, n, k, lda, shift, p.ntiles, p.slices, p.steps);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && p.slices > 1) {
+        hipLaunchKernelGGL(k_gemm_reduce<NT>, dim3(p.ntiles * (4 * NT * 64) / 256), dim3(256), 0, st, part, p.slices,
+                           p.ntiles, y, y_f32, m, n);
+        e = hipGetLastError();
+    }
+    return e;
+}
+
+// Requires p.steps <= the variant's steps per workgroup and p.slices * p.steps covering k / 128; A rows
+// lda bytes apart.
 static hipError_t launch_gemm_plan(const GemmPlan &p, int fmt, void *y, const void *codes, const void *scales,
                                    const uint8_t *aq, int lda, const uint8_t *as_, int m, int n, int k, int act_block,
                                    int y_f32, void *work, hipStream_t st) {
     f32x4 *part = (f32x4 *)work;
     const int shift = act_block == 32 ? 5 : 7;
-    const dim3 grid(p.ntiles * p.slices);
-    if (fmt == 0)
-        hipLaunchKernelGGL((k_gemm<true, kGemmWaveSteps>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales, aq,
-                           as_, part, y, y_f32, m, n, k, lda, shift, p.ntiles, p.slices, p.steps);
-    else
-        hipLaunchKernelGGL((k_gemm<false, kGemmWaveSteps>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales, aq,
-                           as_, part, y, y_f32, m, n, k, lda, shift, p.ntiles, p.slices, p.steps);
-    hipError_t e = hipGetLastError();
-    if (e == hipSuccess && p.slices > 1) {
-        hipLaunchKernelGGL(k_gemm_reduce, dim3(p.ntiles * kGemmTileVecs / 256), dim3(256), 0, st, part, p.slices,
-                           p.ntiles, y, y_f32, m, n);
-        e = hipGetLastError();
-    }
-    return e;
+    if (p.variant == 0)
+        return launch_gemm_t<4, 8>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
+    return launch_gemm_t<2, 16>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
 }
 
 static hipError_t launch_gemm(int fmt, void *y, const void *codes, const void *scales, const uint8_t *aq,
