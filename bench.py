@@ -122,7 +122,7 @@ def gemv_workload(torch, fmt, rows, k, m, steps, warmup, use_graph=True):
             "graph": use_graph}
 
 
-def gemv_batch_workload(torch, fmt, rows, k, steps, warmup, nb=16):
+def gemv_batch_workload(torch, fmt, rows, k, steps, warmup, nb=16, use_graph=True):
     """Sustained GEMV bandwidth: nb same-shape GEMVs per launch (the reference's kMxBatch batching,
     stbl/kernels.h:18-20), every launch on nb different weight matrices from a >= 512 MB rotation."""
     from stblarge_amd import data, ops
@@ -142,7 +142,7 @@ def gemv_batch_workload(torch, fmt, rows, k, steps, warmup, nb=16):
     def launch(i):
         ops.gemv_batch(cs[i], ss[i], xs, f, outs=ys)
 
-    ms, n = timed_steps(torch, launch, groups, max(20, steps // nb), max(4, warmup // nb))
+    ms, n = timed_steps(torch, launch, groups, max(20, steps // nb), max(4, warmup // nb), use_graph)
     per = data.algorithmic_bytes_fp4(rows, k, 1) if fmt == "fp4" else data.algorithmic_bytes_fp8(rows, k, 1)
     alg = nb * per
     gbs = alg / (ms * 1e-3) / 1e9
@@ -150,7 +150,7 @@ def gemv_batch_workload(torch, fmt, rows, k, steps, warmup, nb=16):
             "launches": n, "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS}
 
 
-def ffn_workload(torch, fmt, steps, warmup):
+def ffn_workload(torch, fmt, steps, warmup, use_graph=True):
     """C3: one expert FFN (gate/up + SwiGLU, down) at dim 7168, inter 2048, one token."""
     from stblarge_amd import data, ops
 
@@ -172,7 +172,7 @@ def ffn_workload(torch, fmt, steps, warmup):
         _lib.check(lib.stbl_amd_expert_ffn(fmt, ops._ptr(y), ops._ptr(slots[i]), ops._ptr(x), 1, dim, inter, 1.0, 0.0,
                                            0, 0, ops._ptr(work), st), "expert_ffn")
 
-    ms, n = timed_steps(torch, launch, copies, steps, warmup)
+    ms, n = timed_steps(torch, launch, copies, steps, warmup, use_graph)
     nbytes, offs = ops.expert_layout(fmt, dim, inter)
     wbytes = sum(ops._mat_bytes(fmt, r, k) for r, k in ((inter, dim), (inter, dim), (dim, inter)))
     alg = wbytes + 2 * dim + 2 * dim
@@ -224,7 +224,7 @@ def moe_workload(torch, tokens, steps, warmup_steps):
             "refill_GB_s": (st1["refill_bytes"] - st0["refill_bytes"]) / el / 1e9}
 
 
-def moe_allhit_workload(torch, tokens, steps, warmup, v41=False):
+def moe_allhit_workload(torch, tokens, steps, warmup, v41=False, use_graph=True):
     """C4's expert kernels alone with every expert resident (the kernel bound of the layer): per
     step, each token's 8 routed experts are drawn from 64 resident slots (1.5 GB, so weights come
     from HBM) plus the shared expert; algorithmic bytes = every distinct expert's weights once.
@@ -266,7 +266,7 @@ def moe_allhit_workload(torch, tokens, steps, warmup, v41=False):
         ops.moe_experts(x, sl, pick, w, fmt, dim, inter, shared=len(sl) - 1, work=work, out=y, shared_fmt=sfmt,
                         official=v41, limit=10.0 if v41 else 0.0)
 
-    ms, n = timed_steps(torch, launch, len(plans), steps, warmup)
+    ms, n = timed_steps(torch, launch, len(plans), steps, warmup, use_graph)
     alg = np.mean([p[2] for p in plans]) * wbytes + sbytes + 4 * dim * tokens
     gbs = alg / (ms * 1e-3) / 1e9
     name = f"moe_v41_allhit_t{tokens}_fp4_top6_fp8e8m0_shared" if v41 else f"moe_experts_allhit_t{tokens}_fp4"
@@ -496,7 +496,7 @@ def ref_method_workload(torch, kind, rows, k, group_rows=0, reps=200):
     return {"workload": name, "us": us, "GB_s": nbytes / us / 1e3, "bytes": nbytes, "reps": reps}
 
 
-def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168, prequant=False):
+def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168, prequant=False, use_graph=True):
     """C5: multi-token expert GEMM, M = 64 tokens, W [2048 x 7168] FP4 or FP8 (scaled f8f6f4 MFMA).
     prequant: the activations are quantized outside the timed region and the GEMM proper is timed
     (stbl_amd_gemm_q, fp8_gemm(a, a_s, b, b_s)'s form); otherwise act_quant + GEMM (stbl_amd_gemm)."""
@@ -524,7 +524,7 @@ def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168, prequant=Fals
             _lib.check(lib.stbl_amd_gemm(fmt, ops._ptr(y), ops._ptr(cs[i]), ops._ptr(ss[i]), ops._ptr(x), m, n, k,
                                          128, 0, ops._ptr(work), ops._stream()), "gemm")
 
-    ms, nsteps = timed_steps(torch, launch, copies, steps, warmup)
+    ms, nsteps = timed_steps(torch, launch, copies, steps, warmup, use_graph)
     alg = wbytes + (m * k + m * k // 128 if prequant else 2 * m * k) + 2 * m * n
     flops = 2.0 * m * n * k
     name = "fp4" if fmt == ops.FP4 else "fp8"
@@ -804,7 +804,7 @@ def main():
                   flush=True)
     if args.only in ("all", "gemv", "batch"):
         for fmt, rows, k in (("fp4", 7168, 2048), ("fp4", 2048, 7168), ("fp8", 7168, 2048), ("fp8", 2048, 7168)):
-            r = gemv_batch_workload(torch, fmt, rows, k, args.steps, args.warmup)
+            r = gemv_batch_workload(torch, fmt, rows, k, args.steps, args.warmup, use_graph=not args.no_graph)
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_launch'] * 1e3:.2f} us/launch of 16, {r['GB_s']:.0f} GB/s "
                   f"({100 * r['frac_hbm_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
@@ -812,7 +812,7 @@ def main():
         from stblarge_amd import ops
 
         for fmt in (ops.FP4, ops.FP8):
-            r = ffn_workload(torch, fmt, max(200, args.steps // 4), args.warmup)
+            r = ffn_workload(torch, fmt, max(200, args.steps // 4), args.warmup, use_graph=not args.no_graph)
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
                   flush=True)
@@ -821,7 +821,8 @@ def main():
 
         for fmt, pq, n, k in [(ops.FP4, True, 2048, 7168), (ops.FP8, True, 2048, 7168), (ops.FP4, False, 2048, 7168),
                               (ops.FP8, False, 2048, 7168), (ops.FP4, True, 7168, 2048)]:
-            r = gemm_workload(torch, fmt, max(200, args.steps // 4), args.warmup, n=n, k=k, prequant=pq)
+            r = gemm_workload(torch, fmt, max(200, args.steps // 4), args.warmup, n=n, k=k, prequant=pq,
+                              use_graph=not args.no_graph)
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s, "
                   f"{r['TFLOP_s']:.0f} TFLOP/s ({100 * r['frac_mfma_peak']:.1f}% MFMA)", file=sys.stderr, flush=True)
@@ -855,7 +856,7 @@ def main():
             print(f"# {r['workload']}: {r['us']:.2f} us, {r['GB_s']:.1f} GB/s", file=sys.stderr, flush=True)
     if args.only in ("all", "moe", "moeallhit"):
         for t, v41 in ((1, False), (4, False), (1, True), (4, True)):
-            r = moe_allhit_workload(torch, t, max(100, args.steps // 10), 32, v41=v41)
+            r = moe_allhit_workload(torch, t, max(100, args.steps // 10), 32, v41=v41, use_graph=not args.no_graph)
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s, "
                   f"{r['GB_s']:.0f} GB/s", file=sys.stderr, flush=True)

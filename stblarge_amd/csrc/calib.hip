@@ -4,7 +4,8 @@
 // stbl/bench_gemv.py:58-61).
 //
 // Every thread issues kReadLoads 16-byte non-temporal loads, one per pass over the workgroup's span, all
-// before its first use (the loads of a wave cover consecutive kilobytes, as the GEMV weight loads
+// before its first use (2 loads x 512 threads was the fastest of the shapes measured: 1-16 loads per
+// thread, 64-1024 threads, row-contiguous waves; 3.06 us for 7.8 MB, 19.7 us for 125 MB) (the loads of a wave cover consecutive kilobytes, as the GEMV weight loads
 // do), folds them with XOR, the wave folds its lanes' words, and lane 0 writes one word per wave, so
 // no load can be dropped. Bytes past the range are not read (the last unit clamps its address and
 // drops its value).
@@ -13,8 +14,8 @@
 
 namespace stbl {
 
-constexpr int kReadLoads = 4;
-constexpr int kReadThreads = 256;
+constexpr int kReadLoads = 2;
+constexpr int kReadThreads = 512;
 
 __global__ __launch_bounds__(kReadThreads) void k_read_floor(const u32x4 *__restrict__ src, uint64_t units,
                                                              uint32_t *__restrict__ sink) {
