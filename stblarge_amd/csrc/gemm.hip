@@ -69,38 +69,38 @@ __global__ __launch_bounds__(256) void k_act_quant_e4m3(const uint16_t *__restri
 
 // ---- GEMM ---------------------------------------------------------------------------------------
 
-// One workgroup owns a 64 x 16 NT output tile (4 m-tiles x NT n-tiles of 16 x 16) and a slice of up
-// to NW * SW 128-K steps; wave w takes SW consecutive steps of the slice and accumulates its NT * 4
-// tiles in registers, loading its activations and weights straight from global memory (no operand is
-// shared between waves, so nothing is staged through LDS). All loads of a wave are issued before its
-// first MFMA, from addresses clamped into the buffers; a step past the slice gets zero operands
-// instead of a branch. The waves' tiles are summed through LDS in wave order. With one slice the
-// workgroup writes Y; otherwise it writes its slice's partial tile and k_gemm_reduce adds the slices
-// in order. (Summing the slices in the last workgroup to finish needs an agent-scope release/acquire
-// per workgroup, which writes back and invalidates the XCD's L2 each time: measured at about 4x the
-// whole GEMM, so the kernel boundary is the synchronization point.) Workgroup b takes tile b % ntiles
-// and slice b / ntiles: with ntiles % 8 == 0 every slice of a tile runs on one XCD (workgroups go
-// round-robin over the 8 XCDs), which shares its activation reads. A rows are lda bytes apart.
-// Partial tiles and the LDS sum hold f32x4 q = t * 64 + lane with t = m-tile * NT + n-tile.
-template <bool FP4W, int NT, int NW, int SW>
+// One workgroup owns a 16 MT x 16 NT output tile (MT m-tiles x NT n-tiles of 16 x 16, rows m0 ..) and
+// a slice of up to NW * SW 128-K steps; wave w takes SW consecutive steps of the slice and accumulates
+// its MT * NT tiles in registers, loading its activations and weights straight from global memory
+// (no operand is shared between waves, so nothing is staged through LDS). All loads of a wave are
+// issued before its first MFMA, from addresses clamped into the buffers; a step past the slice gets
+// zero operands instead of a branch. The waves' tiles are summed through LDS in wave order. With one
+// slice the workgroup writes Y; otherwise it writes its slice's partial tile and k_gemm_reduce adds
+// the slices in order. (Summing the slices in the last workgroup to finish needs an agent-scope
+// release/acquire per workgroup, which writes back and invalidates the XCD's L2 each time: measured
+// at about 4x the whole GEMM, so the kernel boundary is the synchronization point.) The workgroup
+// order is gemm_plan's. A rows are lda bytes apart. Partial tiles and the LDS sum hold f32x4
+// q = t * 64 + lane with t = m-tile * NT + n-tile.
+template <bool FP4W, int MT, int NT, int NW, int SW>
 __global__ __launch_bounds__(NW * 64) void k_gemm(const uint8_t *__restrict__ wc, const void *__restrict__ ws,
                                                   const uint8_t *__restrict__ aq, const uint8_t *__restrict__ as_,
                                                   f32x4 *__restrict__ part, void *__restrict__ y, int y_f32, int M,
-                                                  int N, int K, int lda, int act_shift, int ntiles, int slices,
-                                                  int steps_wg) {
-    constexpr int kTileVecs = 4 * NT * 64;
+                                                  int N, int K, int lda, int act_shift, int ntiles, int mgroups,
+                                                  int slices, int steps_wg) {
+    constexpr int kTileVecs = MT * NT * 64;
     constexpr int kThreads = NW * 64;
     __shared__ f32x4 red[NW * kTileVecs];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
-    const int tile = blockIdx.x % ntiles, slice = blockIdx.x / ntiles;
+    const int u = blockIdx.x % (ntiles * mgroups), slice = blockIdx.x / (ntiles * mgroups);
+    const int tile = u % ntiles, m0 = (u / ntiles) * 16 * MT;
     const int n0 = tile * 16 * NT, KS = K >> 7;
     const int wsteps = (steps_wg + NW - 1) / NW;
     const int s0 = slice * steps_wg + wave * wsteps;
     const int nst = max(0, min(wsteps, min(KS, (slice + 1) * steps_wg) - s0));  // wave-uniform
 
     // 1. loads: lane (r, g) holds, per step, rows 16 mt + r of A and columns n0 + 16 nt + r of W
-    u32x4 av[SW][4][2];
-    uint32_t asc[SW][4];
+    u32x4 av[SW][MT][2];
+    uint32_t asc[SW][MT];
     u32x4 bv[SW][NT][FP4W ? 1 : 2];
     uint32_t bsc[SW][NT];
     float wsc[SW];
@@ -108,8 +108,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemm(const uint8_t *__restrict__ wc
     for (int s = 0; s < SW; s++) {
         const size_t kb = (size_t)(s < nst ? s0 + s : 0) * 128;
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++) {
-            const int m = min(16 * mt + r, M - 1);
+        for (int mt = 0; mt < MT; mt++) {
+            const int m = min(m0 + 16 * mt + r, M - 1);
             const uint8_t *row = aq + (size_t)m * lda + kb;
             av[s][mt][0] = *(const u32x4 *)(row + 16 * g);
             av[s][mt][1] = *(const u32x4 *)(row + 64 + 16 * g);
@@ -130,9 +130,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemm(const uint8_t *__restrict__ wc
         if constexpr (!FP4W) wsc[s] = ((const float *)ws)[(size_t)(n0 >> 7) * KS + (kb >> 7)];
     }
     // 2. MFMAs, 4 NT independent accumulators per step
-    f32x4 acc[4][NT];
+    f32x4 acc[MT][NT];
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+    for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     const u32x4 z4 = {0, 0, 0, 0};
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm(const uint8_t *__restrict__ wc
             }
         }
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++) {
+        for (int mt = 0; mt < MT; mt++) {
             const u32x4 a0 = live ? av[s][mt][0] : z4, a1 = live ? av[s][mt][1] : z4;
             const i32x8 a = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
 #pragma unroll
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm(const uint8_t *__restrict__ wc
     }
     // 3. the workgroup's sum, in wave order; thread tid takes q = tid + kThreads j
 #pragma unroll
-    for (int t = 0; t < 4 * NT; t++) red[(wave * 4 * NT + t) * 64 + lane] = acc[t / NT][t % NT];
+    for (int t = 0; t < MT * NT; t++) red[(wave * MT * NT + t) * 64 + lane] = acc[t / NT][t % NT];
     __syncthreads();
     constexpr int kPer = (kTileVecs + kThreads - 1) / kThreads;
 #pragma unroll
@@ -181,8 +181,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemm(const uint8_t *__restrict__ wc
         f32x4 v = red[q];
 #pragma unroll
         for (int w = 1; w < NW; w++) v += red[w * kTileVecs + q];
-        if (slices > 1) {
-            part[((size_t)tile * slices + slice) * kTileVecs + q] = v;
+        if (slices > 1) {  // (split K only with mgroups == 1: u is the tile)
+            part[((size_t)u * slices + slice) * kTileVecs + q] = v;
             continue;
         }
         // Y: element e of v is row 16 mt + 4 g' + e, column n0 + 16 nt + r' of the lane q % 64
@@ -191,7 +191,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm(const uint8_t *__restrict__ wc
         if (n >= N) continue;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int m = 16 * mt + 4 * (ql >> 4) + e;
+            const int m = m0 + 16 * mt + 4 * (ql >> 4) + e;
             if (m >= M) continue;
             if (y_f32) ((float *)y)[(size_t)m * N + n] = v[e];
             else ((uint16_t *)y)[(size_t)m * N + n] = f32_to_bf16_bits(v[e]);
@@ -235,24 +235,35 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const f32x4 *__restrict__ p
 }
 
 // Tile shape and split of K, chosen per shape (each choice measured fastest for its shape):
-//   variant 1, 64 x 32 tiles and 16 waves of one step each, when one slice covers K (<= 16 steps)
-//     and the tiles alone give >= 192 workgroups (7168 x 2048: no partials and no second launch,
+//   variant 2, 32 x 64 tiles (two workgroups per 64 columns when m > 32) and 16 waves of one step
+//     each, when one slice covers K (<= 16 steps) and the tiles give >= 192 workgroups: per
+//     workgroup 32 rows of activations and 64 columns of weights instead of 64 and 32 (7168 x 2048);
+//   variant 1, 64 x 32 tiles and 16 waves of one step each, when one slice covers K and the tiles
+//     alone give >= 192 workgroups (m <= 32 at 7168 x 2048: no partials and no second launch,
 //     11.6 -> 9.3 us against variant 0);
 //   variant 0 otherwise, 64 x 64 tiles and 8 waves of one step each, K split into slices of <= 8
 //     steps, as many as it takes to give >= 200 workgroups (2048 x 7168: 7 slices, 224 workgroups;
 //     against the earlier 4 waves of 2 steps, FP4 11.9 -> 11.6 us, FP8 12.7 -> 11.8 us).
+// Workgroup b takes column tile u % ntiles and row group u / ntiles, u = b % (ntiles * mgroups), and
+// slice b / (ntiles * mgroups): with ntiles % 8 == 0 the row groups and slices of a column tile run
+// on one XCD.
 struct GemmPlan {
-    int variant, nt, ntiles, slices, steps;
+    int variant, mt, nt, ntiles, mgroups, slices, steps;
 };
 
-static GemmPlan gemm_plan(int n, int k) {
+static GemmPlan gemm_plan(int m, int n, int k) {
     GemmPlan p;
     const int ks = k / 128;
-    if (ks <= 16 && (n + 31) / 32 >= 192) {
-        p.variant = 1, p.nt = 2, p.ntiles = (n + 31) / 32, p.slices = 1, p.steps = ks;
+    p.mgroups = 1;
+    if (ks <= 16 && m > 32 && 2 * ((n + 63) / 64) >= 192) {
+        p.variant = 2, p.mt = 2, p.nt = 4, p.ntiles = (n + 63) / 64, p.mgroups = 2, p.slices = 1, p.steps = ks;
         return p;
     }
-    p.variant = 0, p.nt = 4, p.ntiles = (n + 63) / 64;
+    if (ks <= 16 && (n + 31) / 32 >= 192) {
+        p.variant = 1, p.mt = 4, p.nt = 2, p.ntiles = (n + 31) / 32, p.slices = 1, p.steps = ks;
+        return p;
+    }
+    p.variant = 0, p.mt = 4, p.nt = 4, p.ntiles = (n + 63) / 64;
     const int slices = std::max((ks + 7) / 8, std::min(ks, (200 + p.ntiles - 1) / p.ntiles));
     p.steps = (ks + slices - 1) / slices;
     p.slices = (ks + p.steps - 1) / p.steps;
@@ -262,20 +273,21 @@ static GemmPlan gemm_plan(int n, int k) {
 static uint64_t a256(uint64_t v) { return (v + 255) & ~(uint64_t)255; }
 
 static uint64_t part_bytes(const GemmPlan &p) {
-    return p.slices > 1 ? (uint64_t)p.ntiles * p.slices * (4 * p.nt * 64) * 16 : 0;
+    return p.slices > 1 ? (uint64_t)p.ntiles * p.slices * (p.mt * p.nt * 64) * 16 : 0;
 }
 
-template <int NT, int NW>
+template <int MT, int NT, int NW>
 static hipError_t launch_gemm_t(const GemmPlan &p, int fmt, void *y, const void *codes, const void *scales,
                                 const uint8_t *aq, int lda, const uint8_t *as_, int m, int n, int k, int shift,
                                 int y_f32, f32x4 *part, hipStream_t st) {
-    const dim3 grid(p.ntiles * p.slices);
+    static_assert(MT == 4 || NW == 16, "split K (the reduce kernel) takes 64-row tiles only");
+    const dim3 grid(p.ntiles * p.mgroups * p.slices);
     if (fmt == 0)
-        hipLaunchKernelGGL((k_gemm<true, NT, NW, 1>), grid, dim3(NW * 64), 0, st, (const uint8_t *)codes, scales, aq,
-                           as_, part, y, y_f32, m, n, k, lda, shift, p.ntiles, p.slices, p.steps);
+        hipLaunchKernelGGL((k_gemm<true, MT, NT, NW, 1>), grid, dim3(NW * 64), 0, st, (const uint8_t *)codes, scales, aq,
+                           as_, part, y, y_f32, m, n, k, lda, shift, p.ntiles, p.mgroups, p.slices, p.steps);
     else
-        hipLaunchKernelGGL((k_gemm<false, NT, NW, 1>), grid, dim3(NW * 64), 0, st, (const uint8_t *)codes, scales, aq,
-                           as_, part, y, y_f32, m, n, k, lda, shift, p.ntiles, p.slices, p.steps);
+        hipLaunchKernelGGL((k_gemm<false, MT, NT, NW, 1>), grid, dim3(NW * 64), 0, st, (const uint8_t *)codes, scales, aq,
+                           as_, part, y, y_f32, m, n, k, lda, shift, p.ntiles, p.mgroups, p.slices, p.steps);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && p.slices > 1) {
         hipLaunchKernelGGL(k_gemm_reduce<NT>, dim3(p.ntiles * (4 * NT * 64) / 256), dim3(256), 0, st, part, p.slices,
@@ -285,22 +297,24 @@ static hipError_t launch_gemm_t(const GemmPlan &p, int fmt, void *y, const void 
     return e;
 }
 
-// Requires p.steps <= the variant's steps per workgroup and p.slices * p.steps covering k / 128; A rows
-// lda bytes apart.
+// Requires p.steps <= the variant's steps per workgroup and p.slices * p.steps covering k / 128, and
+// split K (slices > 1) only in variant 0; A rows lda bytes apart.
 static hipError_t launch_gemm_plan(const GemmPlan &p, int fmt, void *y, const void *codes, const void *scales,
                                    const uint8_t *aq, int lda, const uint8_t *as_, int m, int n, int k, int act_block,
                                    int y_f32, void *work, hipStream_t st) {
     f32x4 *part = (f32x4 *)work;
     const int shift = act_block == 32 ? 5 : 7;
     if (p.variant == 0)
-        return launch_gemm_t<4, 8>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
-    return launch_gemm_t<2, 16>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
+        return launch_gemm_t<4, 4, 8>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
+    if (p.variant == 1)
+        return launch_gemm_t<4, 2, 16>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
+    return launch_gemm_t<2, 4, 16>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
 }
 
 static hipError_t launch_gemm(int fmt, void *y, const void *codes, const void *scales, const uint8_t *aq,
                               const uint8_t *as_, int m, int n, int k, int act_block, int y_f32, void *work,
                               hipStream_t st) {
-    return launch_gemm_plan(gemm_plan(n, k), fmt, y, codes, scales, aq, k, as_, m, n, k, act_block, y_f32, work, st);
+    return launch_gemm_plan(gemm_plan(m, n, k), fmt, y, codes, scales, aq, k, as_, m, n, k, act_block, y_f32, work, st);
 }
 
 static int check_gemm(const char *name, int fmt, const void *y, const void *codes, const void *scales, int m, int n,
@@ -323,7 +337,7 @@ extern "C" {
 
 uint64_t stbl_amd_gemm_work_bytes(int m, int n, int k) {
     if (m < 1 || n < 1 || k < 128) return 256;
-    return a256(part_bytes(gemm_plan(n, k))) + a256((uint64_t)m * k) + a256((uint64_t)m * (k / 32)) + 256;
+    return a256(part_bytes(gemm_plan(m, n, k))) + a256((uint64_t)m * k) + a256((uint64_t)m * (k / 32)) + 256;
 }
 
 int stbl_amd_gemm_q(int fmt, void *y, const void *codes, const void *scales, const void *aq, const void *as, int m,
@@ -339,7 +353,7 @@ int stbl_amd_gemm(int fmt, void *y, const void *codes, const void *scales, const
                   int act_block, int y_f32, void *work, hipStream_t st) {
     if (int e = check_gemm("gemm", fmt, y, codes, scales, m, n, k, act_block, work)) return e;
     if (!x || !aligned16(x)) return abi_fail(hipErrorInvalidValue, "gemm: x must be 16-byte aligned");
-    uint8_t *aq = (uint8_t *)work + a256(part_bytes(gemm_plan(n, k)));
+    uint8_t *aq = (uint8_t *)work + a256(part_bytes(gemm_plan(m, n, k)));
     uint8_t *as_ = aq + a256((uint64_t)m * k);
     const int n8 = m * k / 8;
     hipLaunchKernelGGL(k_act_quant_e4m3, dim3((n8 + 255) / 256), dim3(256), 0, st, (const uint16_t *)x, n8, act_block, aq, as_);
