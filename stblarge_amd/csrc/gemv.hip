@@ -29,7 +29,7 @@ template <WFmt F, bool XF32, int M, int R, bool DW>
 __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, int out_mode) {
     using T = WTraits<F>;
     constexpr int CH = T::CH;
-    static_assert(32 % R == 0, "a row tile must sit inside one scale block");
+    static_assert(F == WFmt::FP4_GGUF || 32 % R == 0, "a row tile must sit inside one scale block");
     const GemvJob J = jobs.j[blockIdx.y];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     const int nch = k / CH, c = wave * 64 + lane;
@@ -328,6 +328,15 @@ static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int o
         // FP4 launches take 16 (12 x 2304x5120 25.3 -> 23.3 us, 16 x 2048x7168 38.1 -> 31.5); FP8
         // E8M0 at 32768x1280 was 5% slower with 16, so it keeps 8.
         const long wgs8 = (long)ceil_div(rows, 8) * njobs * ceil_div(k / WTraits<F>::CH, 64);
+        if constexpr (F == WFmt::FP4_GGUF) {
+            // 9-10 rows per CU: tiles of exactly that many rows make the launch one round over the CUs,
+            // so each CU reads the fp32 x chunk (twice the weight bytes of a 4-row tile) once, not 3
+            // times (2304x5120: 5.99 -> 5.06 us; 9-10 rows are 53-58 loads per lane, within the
+            // limit of loads in flight; 20 rows per CU, as at 5120x2304, are not: 5.47 -> 7.9 us)
+            const long per_cu = ((long)rows * njobs + device_cus() - 1) / device_cus();
+            if (per_cu == 9) return launch_r<F, XF32, M, 9>(jobs, njobs, rows, k, out_mode, st);
+            if (per_cu == 10) return launch_r<F, XF32, M, 10>(jobs, njobs, rows, k, out_mode, st);
+        }
         if constexpr (F == WFmt::FP4_GGUF)
             if (wgs8 >= 8192) return launch_r<F, XF32, M, 16>(jobs, njobs, rows, k, out_mode, st);
         if (wgs8 >= 4096) return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);

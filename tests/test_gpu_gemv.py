@@ -144,6 +144,31 @@ def test_stbl_gemv_mxfp4_gguf(gpu, rows, k):
     assert_gemv(got, got, want, tol=2.0 ** -8)
 
 
+@pytest.mark.parametrize("per_cu,n,trim", [(9, 1, 4), (10, 1, 7), (9, 2, 1), (10, 1, 0)])
+def test_stbl_gemv_mxfp4_one_round_tiles(gpu, per_cu, n, trim):
+    # launches with 9-10 rows per CU take tiles of that many rows (one workgroup per CU; on 256 CUs
+    # 9 x 256 - 4 = 2300 rows, the reference's 2304 x 5120 shape less a ragged last tile), also over
+    # two matrices whose tiles must not cross from one matrix into the next
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    rows, k = (per_cu * cus + n - 1) // n - trim, 2560
+    rng = np.random.default_rng(per_cu * 10 + n)
+    ys, ws, xs, wants = [], [], [], []
+    for j in range(n):
+        codes = rng.integers(0, 256, (rows, k // 2), dtype=np.uint8)
+        sc = rng.integers(118, 126, (rows, k // 32), dtype=np.uint8)
+        x = data.activation(1, k, seed=200 + j).float().numpy()[0]
+        wants.append(oracle.gemv_fp4(codes, sc, x[None])[0])
+        ws.append(torch.from_numpy(oracle.ocp_to_gguf17(codes, sc)).to(gpu))
+        xs.append(torch.from_numpy(x).to(gpu))
+        ys.append(torch.empty(rows, device=gpu))
+    if n == 1:
+        ops.stbl_gemv_mxfp4(ys[0], ws[0], xs[0], rows, k)
+    else:
+        ops.stbl_gemv_mxfp4_batch(ys, ws, xs, rows, k)
+    for y, want in zip(ys, wants):
+        assert_gemv(np_(y), np_(y), want, tol=2.0 ** -8)
+
+
 @pytest.mark.parametrize("rows,k,n", [(256, 1024, 16), (2304, 5120, 12), (5120, 2304, 6), (2300, 5120, 16),
                                       (40, 512, 3)])
 def test_stbl_gemv_mxfp4_batch(gpu, rows, k, n):
