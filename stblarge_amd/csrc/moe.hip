@@ -374,8 +374,10 @@ static inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 // Rows per workgroup. Several experts per launch: 4 gate and 4 up rows share a lane's x chunk, and
 // 8 down rows (4 with 4 tokens), measured best for the MoE steps (2 rows for more than one token
-// was 6-11% slower at T=4). One expert per launch (the FFN on its own): 2 and 2, which keep 4x more
-// workgroups in flight (measured 4-6% faster for one FP4 / FP8 expert).
+// was 6-11% slower at T=4). One expert per launch (the FFN on its own): 2 down rows, which keep 4x
+// more workgroups in flight (4 / 8 rows: 9.48 -> 9.48 / 9.58 us for one FP4 expert); gate/up takes
+// 4 and 4 rows for FP4, whose dword scale loads need 4+ rows (9.48 -> 9.25 us; 8 and 8: 10.2 us),
+// and 2 and 2 for FP8 (11.80 against 11.85 us with 4).
 template <WFmt F, int M, int R>
 static hipError_t launch_gateup_r(const MoeJobs &jobs, int n, const ExpertLayout &L, const uint16_t *x, uint16_t *h,
                                   int dim, int inter, float limit, int official, hipStream_t st) {
@@ -396,7 +398,7 @@ static hipError_t launch_gateup_r(const MoeJobs &jobs, int n, const ExpertLayout
 template <WFmt F, int M>
 static hipError_t launch_gateup(const MoeJobs &jobs, int n, const ExpertLayout &L, const uint16_t *x, uint16_t *h,
                                 int dim, int inter, float limit, int official, hipStream_t st) {
-    if (n == 1) return launch_gateup_r<F, M, 2>(jobs, n, L, x, h, dim, inter, limit, official, st);
+    if (n == 1) return launch_gateup_r<F, M, WTraits<F>::fp4 ? 4 : 2>(jobs, n, L, x, h, dim, inter, limit, official, st);
     return launch_gateup_r<F, M, 4>(jobs, n, L, x, h, dim, inter, limit, official, st);
 }
 
