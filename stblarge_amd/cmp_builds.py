@@ -128,17 +128,18 @@ def _cases(dev, seed):
                 assert fn(_p(y), _p(codes), _p(scales), _p(x), m, rows, k, 1, st) == 0
                 return [y]
             cases.append((f"gemv v2 fmt {fmt} {rows}x{k} m={m}", v2))
-    codes, scales = ops.quant_fp4(data.weight(7168, 2048, seed + 1, dev))
-    xs = [bf((1, 2048)) for _ in range(16)]
+    for rows, k in ((7168, 2048), (2048, 7168)):
+        codes, scales = ops.quant_fp4(data.weight(rows, k, seed + 1, dev))
+        xs = [bf((1, k)) for _ in range(16)]
 
-    def batch(lib):
-        ys = [_out(7168, dev) for _ in range(16)]
-        arr = ctypes.c_void_p * 16
-        assert lib.stbl_amd_gemv_fp4_batch(arr(*[y.data_ptr() for y in ys]), arr(*[codes.data_ptr()] * 16),
-                                           arr(*[scales.data_ptr()] * 16), arr(*[x.data_ptr() for x in xs]),
-                                           16, 1, 7168, 2048, 1, st) == 0
-        return ys
-    cases.append(("gemv_fp4_batch 16 x 7168x2048", batch))
+        def batch(lib, codes=codes, scales=scales, xs=xs, rows=rows, k=k):
+            ys = [_out(rows, dev) for _ in range(16)]
+            arr = ctypes.c_void_p * 16
+            assert lib.stbl_amd_gemv_fp4_batch(arr(*[y.data_ptr() for y in ys]), arr(*[codes.data_ptr()] * 16),
+                                               arr(*[scales.data_ptr()] * 16), arr(*[x.data_ptr() for x in xs]),
+                                               16, 1, rows, k, 1, st) == 0
+            return ys
+        cases.append((f"gemv_fp4_batch 16 x {rows}x{k}", batch))
 
     # expert FFN and MoE (official numerics, the engine's shared expert format)
     dim, inter = 5120, 2304

@@ -352,6 +352,12 @@ static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int o
         const long wgs8 = (long)ceil_div(rows, 8) * njobs * ceil_div(k / WTraits<F>::CH, 64);
         if (wgs8 >= 8192) return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
         const int cus = device_cus();
+        // one token of FP4 over rows of 4+ waves: 8-row tiles when they still fill every CU, halving the x
+        // reads per weight byte again (2048x7168: 3.85 -> 3.80 us; rows of one wave lose: 7168x2048
+        // 3.73 -> 4.62 us)
+        if constexpr (F == WFmt::FP4_OCP && M == 1)
+            if (k / WTraits<F>::CH > 3 * 64 && (long)ceil_div(rows, 8) * njobs >= cus)
+                return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
         const long busiest2 = ceil_div(ceil_div(rows, 2) * njobs, cus) * 2L;
         const long busiest4 = ceil_div(ceil_div(rows, 4) * njobs, cus) * 4L;
         const int min_waves = F == WFmt::FP4_OCP ? 2 : 3;

@@ -212,10 +212,12 @@ def test_gemv_batch(gpu, fmt, rows, k, n):
         assert_gemv(np_(y), np_(y16), want)
 
 
-def test_gemv_batch_ragged_rows_eight_row_tiles(gpu):
-    # 16 x 1100 rows at K = 7168 is enough workgroups for 8-row tiles; 1100 = 137 x 8 + 4 leaves the
-    # last tile half empty
-    rows, k, n = 1100, 7168, 16
+@pytest.mark.parametrize("rows,k", [(1100, 7168), (4100, 2048)])
+def test_gemv_batch_ragged_rows_eight_row_tiles(gpu, rows, k):
+    # 16 x 1100 rows at K = 7168 (or 16 x 4100 at K = 2048) are enough workgroups for 8-row tiles in
+    # workgroups of several row groups sharing x; 1100 = 137 x 8 + 4 leaves the last tile half empty,
+    # and 4100 rows leave most row groups of the last workgroup past the matrix
+    n = 16
     cs, ss, xs, wants = [], [], [], []
     for j in range(n):
         c, s = oracle.quant_fp4(data.weight(rows, k, seed=700 + j).numpy())
