@@ -224,13 +224,14 @@ def moe_workload(torch, tokens, steps, warmup_steps):
             "refill_GB_s": (st1["refill_bytes"] - st0["refill_bytes"]) / el / 1e9}
 
 
-def moe_allhit_workload(torch, tokens, steps, warmup, v41=False, use_graph=True):
+def moe_allhit_workload(torch, tokens, steps, warmup, v41=False, use_graph=True, fp8_shared=False):
     """C4's expert kernels alone with every expert resident (the kernel bound of the layer): per
     step, each token's 8 routed experts are drawn from 64 resident slots (1.5 GB, so weights come
     from HBM) plus the shared expert; algorithmic bytes = every distinct expert's weights once.
     v41: the reference engine's own MoE instead (stbl/model.cu:426-594 at stbl/bench_gemv.py:15's
     shapes): dim 5120, inter 2304, top-6 FP4 experts + an FP8 E8M0 shared expert, official numerics
-    (act_quant of the input and of the SwiGLU output), SwiGLU limit 10."""
+    (act_quant of the input and of the SwiGLU output), SwiGLU limit 10. fp8_shared: C4's shapes with
+    the shared expert in the engine's FP8 E8M0 32x32 format (stbl/model.cu:544-547) instead of FP4."""
     import numpy as np
 
     from stblarge_amd import data, ops
@@ -240,7 +241,7 @@ def moe_allhit_workload(torch, tokens, steps, warmup, v41=False, use_graph=True)
     if v41:
         dim, inter, topk = 5120, 2304, 6
     fmt = ops.FP4
-    sfmt = ops.FP8_E8M0 if v41 else fmt
+    sfmt = ops.FP8_E8M0 if v41 or fp8_shared else fmt
     base = ops.quant_expert(data.weight(inter, dim, 21, dev), data.weight(inter, dim, 22, dev),
                             data.weight(dim, inter, 23, dev), fmt)
     res = [base.clone() for _ in range(nres)]
@@ -269,7 +270,8 @@ def moe_allhit_workload(torch, tokens, steps, warmup, v41=False, use_graph=True)
     ms, n = timed_steps(torch, launch, len(plans), steps, warmup, use_graph)
     alg = np.mean([p[2] for p in plans]) * wbytes + sbytes + 4 * dim * tokens
     gbs = alg / (ms * 1e-3) / 1e9
-    name = f"moe_v41_allhit_t{tokens}_fp4_top6_fp8e8m0_shared" if v41 else f"moe_experts_allhit_t{tokens}_fp4"
+    name = (f"moe_v41_allhit_t{tokens}_fp4_top6_fp8e8m0_shared" if v41 else
+            f"moe_experts_allhit_t{tokens}_fp4" + ("_fp8e8m0_shared" if fp8_shared else ""))
     return {"workload": name, "ms_per_step": ms, "steps": n, "tokens_per_s":
             tokens / (ms * 1e-3), "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS}
 
@@ -855,8 +857,10 @@ def main():
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['us']:.2f} us, {r['GB_s']:.1f} GB/s", file=sys.stderr, flush=True)
     if args.only in ("all", "moe", "moeallhit"):
-        for t, v41 in ((1, False), (4, False), (1, True), (4, True)):
-            r = moe_allhit_workload(torch, t, max(100, args.steps // 10), 32, v41=v41, use_graph=not args.no_graph)
+        for t, v41, f8s in ((1, False, False), (4, False, False), (1, False, True), (4, False, True), (1, True, False),
+                            (4, True, False)):
+            r = moe_allhit_workload(torch, t, max(100, args.steps // 10), 32, v41=v41, use_graph=not args.no_graph,
+                                    fp8_shared=f8s)
             extra[r["workload"]] = r
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s, "
                   f"{r['GB_s']:.0f} GB/s", file=sys.stderr, flush=True)
