@@ -124,7 +124,9 @@ def gemv_workload(torch, fmt, rows, k, m, steps, warmup, use_graph=True):
 
 def gemv_batch_workload(torch, fmt, rows, k, steps, warmup, nb=16, use_graph=True):
     """Sustained GEMV bandwidth: nb same-shape GEMVs per launch (the reference's kMxBatch batching,
-    stbl/kernels.h:18-20), every launch on nb different weight matrices from a >= 512 MB rotation."""
+    stbl/kernels.h:18-20, is 16; the v2 batches take up to 64, about what the MoE step's gate/up
+    launch holds at 4 tokens), every launch on nb different weight matrices from a >= 512 MB
+    rotation."""
     from stblarge_amd import data, ops
 
     dev = torch.device("cuda:0")
@@ -805,10 +807,12 @@ def main():
             print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
                   flush=True)
     if args.only in ("all", "gemv", "batch"):
-        for fmt, rows, k in (("fp4", 7168, 2048), ("fp4", 2048, 7168), ("fp8", 7168, 2048), ("fp8", 2048, 7168)):
-            r = gemv_batch_workload(torch, fmt, rows, k, args.steps, args.warmup, use_graph=not args.no_graph)
+        for fmt, rows, k, nb in (("fp4", 7168, 2048, 16), ("fp4", 2048, 7168, 16), ("fp8", 7168, 2048, 16),
+                                 ("fp8", 2048, 7168, 16), ("fp4", 7168, 2048, 64), ("fp4", 2048, 7168, 64),
+                                 ("fp8", 7168, 2048, 64)):
+            r = gemv_batch_workload(torch, fmt, rows, k, args.steps, args.warmup, nb=nb, use_graph=not args.no_graph)
             extra[r["workload"]] = r
-            print(f"# {r['workload']}: {r['ms_per_launch'] * 1e3:.2f} us/launch of 16, {r['GB_s']:.0f} GB/s "
+            print(f"# {r['workload']}: {r['ms_per_launch'] * 1e3:.2f} us/launch of {nb}, {r['GB_s']:.0f} GB/s "
                   f"({100 * r['frac_hbm_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
     if args.only in ("all", "ffn"):
         from stblarge_amd import ops
@@ -890,9 +894,9 @@ def main():
         print(f"# eager launches: {r['ms_per_step'] * 1e3:.3f} us/step", file=sys.stderr, flush=True)
     if args.only in ("all", "fp4", "gemv", "batch", "ffn", "floor"):
         # bare-read floors at the single-launch rows' byte counts: FP4 / FP8 GEMV, FP4 / FP8 expert
-        # FFN, 16 FP4 / FP8 GEMVs per launch
+        # FFN, 16 FP4 / FP8 GEMVs per launch, 64 FP4 / FP8 GEMVs per launch
         floors = {}
-        for nbytes in (7817216, 14702080, 23425024, 44079616, 125075456, 235233280):
+        for nbytes in (7817216, 14702080, 23425024, 44079616, 125075456, 235233280, 500301824, 940933120):
             r = read_floor_workload(torch, nbytes, args.steps, args.warmup)
             floors[nbytes] = r
             extra[r["workload"]] = r

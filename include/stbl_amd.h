@@ -95,9 +95,9 @@ int stbl_amd_gemv_fp4(void *y, const void *codes, const void *scales, const void
 int stbl_amd_gemv_fp8(void *y, const void *codes, const float *scales, const void *x, int m, int rows, int k,
                       int y_f32, hipStream_t st);
 
-/* n <= 16 same-shape v2 GEMVs in one launch, each as stbl_amd_gemv_fp4 / _fp8: the batching of
- * stbl_gemv_mxfp4_batch (stbl/kernels.h:18-20) in the v2 formats. y, codes, scales and x are HOST
- * arrays of n device pointers. */
+/* n <= 64 same-shape v2 GEMVs in one launch, each as stbl_amd_gemv_fp4 / _fp8: the batching of
+ * stbl_gemv_mxfp4_batch (stbl/kernels.h:18-20, which stops at 16) in the v2 formats. y, codes, scales
+ * and x are HOST arrays of n device pointers. */
 int stbl_amd_gemv_fp4_batch(void *const *y, const void *const *codes, const void *const *scales, const void *const *x,
                             int n, int m, int rows, int k, int y_f32, hipStream_t st);
 int stbl_amd_gemv_fp8_batch(void *const *y, const void *const *codes, const void *const *scales, const void *const *x,

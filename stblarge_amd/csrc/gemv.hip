@@ -444,7 +444,7 @@ void stbl_gemv_fp8(float *y, const void *w, const void *scale, const float *x, i
 // aligned (the reference's preconditions, stbl/kernels.cu:138-139). y, w, x are host arrays.
 void stbl_gemv_mxfp4_batch(float *const *y, const void *const *w, const float *const *x, int n, int rows, int k,
                            hipStream_t st) {
-    if (!y || !w || !x || n <= 0 || n > kMaxJobs || rows <= 0 || k <= 0 || k % 256 != 0 || k / 32 > kMaxWaves * 64) {
+    if (!y || !w || !x || n <= 0 || n > kMxBatch || rows <= 0 || k <= 0 || k % 256 != 0 || k / 32 > kMaxWaves * 64) {
         abi_fail(hipErrorInvalidValue, "stbl_gemv_mxfp4_batch: bad arguments (n=%d rows=%d k=%d)", n, rows, k);
         return;
     }

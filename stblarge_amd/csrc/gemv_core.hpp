@@ -16,7 +16,8 @@ constexpr int kMaxWaves = 8;  // K <= 512 chunks: 16384 FP4 / 8192 FP8 elements
 // bytes), plus one for a block that starts mid-unit and one for its end.
 constexpr int kMaxStageRows = 8;
 constexpr int kMaxScaleUnits = kMaxStageRows * kMaxWaves * 64 / 16 + 2;
-constexpr int kMaxJobs = 16;  // matrices per launch (the reference's kMxBatch, stbl/kernels.h:18)
+constexpr int kMxBatch = 16;  // matrices per launch of the reference ABI's batch (stbl/kernels.h:18)
+constexpr int kMaxJobs = 64;  // matrices per launch of the v2 batches (the MoE step's gate/up launches hold up to 66)
 
 enum class WFmt { FP4_OCP, FP4_GGUF, FP8_B128, FP8_E8M0 };
 

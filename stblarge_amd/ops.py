@@ -173,10 +173,10 @@ def gemv_fp8(codes, scales, x, out_f32=False, out=None):
 
 
 def gemv_batch(codes, scales, xs, fmt, out_f32=False, outs=None):
-    """len(codes) <= 16 same-shape GEMVs in one launch: ys[j] = gemv(codes[j], scales[j], xs[j])."""
+    """len(codes) <= 64 same-shape GEMVs in one launch: ys[j] = gemv(codes[j], scales[j], xs[j])."""
     n = len(codes)
-    if not (len(scales) == n == len(xs)) or n == 0 or n > 16:
-        raise ValueError("gemv_batch: need 1..16 matching codes/scales/x")
+    if not (len(scales) == n == len(xs)) or n == 0 or n > 64:
+        raise ValueError("gemv_batch: need 1..64 matching codes/scales/x")
     rows = codes[0].shape[0]
     k = codes[0].shape[1] * (2 if fmt == FP4 else 1)
     sdt = torch.uint8 if fmt == FP4 else torch.float32

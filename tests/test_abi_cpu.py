@@ -67,6 +67,12 @@ def test_argument_checks_fail_without_touching_the_device():
     code, msg = _lib.last_error()
     assert code != 0 and "stbl_gemv_mxfp4" in msg
     assert _lib.last_error() == (0, "")
+    # batch sizes: the reference ABI's batch stops at its kMxBatch of 16, the v2 batches at 64
+    arr = (P * 65)(*[P(256)] * 65)
+    lib.stbl_gemv_mxfp4_batch(arr, arr, arr, 17, 8, 256, None)
+    assert "stbl_gemv_mxfp4_batch" in _lib.last_error()[1]
+    assert lib.stbl_amd_gemv_fp4_batch(arr, arr, arr, arr, 65, 1, 8, 64, 0, None) < 0
+    assert "1..64 matrices" in _lib.last_error()[1]
 
 
 def test_check_raises():

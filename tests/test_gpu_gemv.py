@@ -191,10 +191,11 @@ def test_stbl_gemv_mxfp4_batch(gpu, rows, k, n):
 
 
 @pytest.mark.parametrize("fmt", [0, 1])
-@pytest.mark.parametrize("rows,k,n", [(256, 1024, 16), (2048, 7168, 3)])
+@pytest.mark.parametrize("rows,k,n", [(256, 1024, 16), (2048, 7168, 3), (128, 1024, 64)])
 def test_gemv_batch(gpu, fmt, rows, k, n):
     # same-shape GEMVs in one launch (stbl_gemv_mxfp4_batch's batching, v2 formats), M = 2: 16 small
-    # matrices (2-row tiles), and 3 large ones (4-row tiles, FP4 scales as dwords from each matrix)
+    # matrices (2-row tiles), 3 large ones (4-row tiles, FP4 scales as dwords from each matrix), and
+    # the largest v2 batch, 64 matrices
     m = 2
     q = oracle.quant_fp4 if fmt == 0 else oracle.quant_fp8_b128
     ref = oracle.gemv_fp4 if fmt == 0 else oracle.gemv_fp8_b128
