@@ -646,7 +646,10 @@ uint64_t stbl_amd_moe_work_bytes(int t, int topk, int dim, int inter) {
 
 // stbl_amd_moe_experts with the library's static device scratch instead of `work`: no allocation
 // of any kind, for callers that cannot allocate. Refuses steps whose scratch would exceed
-// kMoeScratchBytes. Calls that overlap on one GPU share its scratch and race.
+// kMoeScratchBytes. Every scratch byte a step reads is written earlier in the same step (gate/up
+// writes each pair's SwiGLU output before down reads it, down each pair's output before the
+// combine), so nothing left by an earlier call is read and nothing is cleared. Calls that overlap on
+// one GPU share its scratch and race.
 int stbl_amd_moe_experts_noalloc(int fmt, void *y, const void *x, int t, int dim, int inter, const void *const *slots,
                                  int n_slots, const int *pick, const float *weights, int topk, int shared,
                                  int shared_fmt, float limit, int official, int y_f32, hipStream_t st) {
