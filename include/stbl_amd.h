@@ -228,7 +228,8 @@ int stbl_amd_gemm(int fmt, void *y, const void *codes, const void *scales, const
 int stbl_amd_gemm_q(int fmt, void *y, const void *codes, const void *scales, const void *aq, const void *as, int m,
                     int n, int k, int act_block, int y_f32, void *work, hipStream_t st);
 
-/* Scratch bytes for stbl_amd_gemm and stbl_amd_gemm_q. */
+/* Scratch bytes for stbl_amd_gemm and stbl_amd_gemm_q with m activation rows (n, k as in the call);
+ * a workspace of that size also serves every call with fewer rows. */
 uint64_t stbl_amd_gemm_work_bytes(int m, int n, int k);
 
 /* act_quant(x, block, "ue8m0") (ref/kernel.py:35-45) as the GEMM consumes it: x bf16 [rows][k] ->

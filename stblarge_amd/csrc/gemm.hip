@@ -276,6 +276,12 @@ static uint64_t part_bytes(const GemmPlan &p) {
     return p.slices > 1 ? (uint64_t)p.ntiles * p.slices * (p.mt * p.nt * 64) * 16 : 0;
 }
 
+// Bytes the partial tiles take at the front of `work`: the larger of the plans for m and for m <= 32
+// (the only way m changes the plan), so a workspace sized for m also serves every smaller m.
+static uint64_t part_reserve(int m, int n, int k) {
+    return a256(std::max(part_bytes(gemm_plan(m, n, k)), part_bytes(gemm_plan(1, n, k))));
+}
+
 template <int MT, int NT, int NW>
 static hipError_t launch_gemm_t(const GemmPlan &p, int fmt, void *y, const void *codes, const void *scales,
                                 const uint8_t *aq, int lda, const uint8_t *as_, int m, int n, int k, int shift,
@@ -337,7 +343,7 @@ extern "C" {
 
 uint64_t stbl_amd_gemm_work_bytes(int m, int n, int k) {
     if (m < 1 || n < 1 || k < 128) return 256;
-    return a256(part_bytes(gemm_plan(m, n, k))) + a256((uint64_t)m * k) + a256((uint64_t)m * (k / 32)) + 256;
+    return part_reserve(m, n, k) + a256((uint64_t)m * k) + a256((uint64_t)m * (k / 32)) + 256;
 }
 
 int stbl_amd_gemm_q(int fmt, void *y, const void *codes, const void *scales, const void *aq, const void *as, int m,
@@ -353,7 +359,7 @@ int stbl_amd_gemm(int fmt, void *y, const void *codes, const void *scales, const
                   int act_block, int y_f32, void *work, hipStream_t st) {
     if (int e = check_gemm("gemm", fmt, y, codes, scales, m, n, k, act_block, work)) return e;
     if (!x || !aligned16(x)) return abi_fail(hipErrorInvalidValue, "gemm: x must be 16-byte aligned");
-    uint8_t *aq = (uint8_t *)work + a256(part_bytes(gemm_plan(m, n, k)));
+    uint8_t *aq = (uint8_t *)work + part_reserve(m, n, k);
     uint8_t *as_ = aq + a256((uint64_t)m * k);
     const int n8 = m * k / 8;
     hipLaunchKernelGGL(k_act_quant_e4m3, dim3((n8 + 255) / 256), dim3(256), 0, st, (const uint16_t *)x, n8, act_block, aq, as_);

@@ -139,3 +139,14 @@ def test_moe_experts_host_jobs_at_the_largest_step():
         st = lib.stbl_amd_moe_experts_phase(0, P(0x30000), P(0x40000), t, 256, 128, slots, 2, pk, wt, topk, 1, 2, 0.0,
                                             0, 0, ready, phase, P(0x50000), None)
         assert st < 0 and "phase" in _lib.last_error()[1]
+
+
+def test_gemm_workspace_for_m_serves_every_smaller_m():
+    # the GEMM's tile plan depends on m (row groups when m > 32), and a plan with split-K partial
+    # tiles can need more workspace than one without: a workspace sized for m must still hold any
+    # smaller m's partials, activation codes and scales (n = 6100, K = 2048 switches from one plan
+    # without partials at m = 64 to a split-K plan at m <= 32)
+    lib = _lib.load()
+    for n, k in ((6100, 2048), (7168, 2048), (2048, 7168), (4096, 4096)):
+        sizes = [lib.stbl_amd_gemm_work_bytes(m, n, k) for m in range(1, 65)]
+        assert all(a <= b for a, b in zip(sizes, sizes[1:])), (n, k, sizes)
