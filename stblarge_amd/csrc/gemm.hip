@@ -16,6 +16,9 @@
 //                     k_gemm_reduce adds the slices in order (the kernel boundary is the
 //                     synchronization point); stbl_amd_gemm_q takes already quantized activations,
 //                     stbl_amd_gemm quantizes X first (one more launch).
+//   k_gemm_one        the same products in one launch over all of K, for m > 32 and K % 512 == 0
+//                     (the configurations' shapes): small tiles, half-line-balanced operand loads
+//                     and scales loaded four steps at a time.
 // Operand layout of the 16x16x128 f8f6f4 MFMA (probed on gfx950): lane l = r + 16 g holds row r of A
 // (column r of B); e4m3 operands hold K bytes [16g, 16g+16) and [64+16g, 64+16g+16) of the 128-K
 // step, e2m1 operands K elements [32g, 32g+32) (low nibble first); the lane's E8M0 scale covers K
@@ -234,7 +237,169 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const f32x4 *__restrict__ p
     }
 }
 
+// One-launch GEMM for K % 512 == 0: a workgroup owns a 16 MT x 16 NT output tile over all of K; wave w
+// takes the 4 SW consecutive 128-K steps [4 SW w, 4 SW w + 4 SW) (waves past K do nothing), and the
+// waves' tiles are summed through LDS in wave order, so the result does not depend on timing.
+// Three things keep the loads, which bound this kernel, few and cheap (each measured):
+//  - every load of a wave is issued before its first MFMA (a scheduling fence keeps the compiler
+//    from interleaving waits with the loads);
+//  - the operand loads alternate 64-byte halves: an MFMA operand load reads 16 rows x 64 bytes, all
+//    in the same half of their 128-byte lines, which the vector L1 serves at half rate. Lanes of odd
+//    rows (odd columns for W) read the other half first, and a per-lane select puts the halves back
+//    in operand order. For FP4 W, whose step is 64 bytes, steps s and s + 1 of a column are the two
+//    halves of one line, so steps come in pairs;
+//  - scales are loaded four steps per instruction (one dword of A scale bytes per row with
+//    act_block 128, 16 bytes per row or column for the per-32 scales), not one byte per step: a
+//    one-byte wave load costs the L1 as much as a 1 KB one. The MFMA reads the low byte of its scale
+//    operand, so each lane shifts its byte down.
+template <bool FP4W, int MT, int NT, int NW, int QW>
+__global__ __launch_bounds__(NW * 64) void k_gemm_one(const uint8_t *__restrict__ wc, const void *__restrict__ ws,
+                                                      const uint8_t *__restrict__ aq, const uint8_t *__restrict__ as_,
+                                                      void *__restrict__ y, int y_f32, int M, int N, int K, int lda,
+                                                      int act32, int ntiles) {
+    constexpr int SW = 4 * QW;  // steps per wave
+    constexpr int kTileVecs = MT * NT * 64;
+    constexpr int kThreads = NW * 64;
+    __shared__ f32x4 red[NW * kTileVecs];
+    const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool odd = r & 1;
+    const int h0 = odd ? 64 : 0, h1 = 64 - h0;
+    const int tile = blockIdx.x % ntiles, m0 = (blockIdx.x / ntiles) * 16 * MT;
+    const int n0 = tile * 16 * NT, KS = K >> 7;
+    const int s0 = wave * SW;
+    const int nst = max(0, min(SW, KS - s0));  // wave-uniform; a multiple of 4
+
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (nst > 0) {
+        // 1. loads: lane (r, g) holds rows 16 mt + r of A and columns n0 + 16 nt + r of W; step
+        // s < nst is step s0 + s of K (a wave has all or none of its SW steps: KS % 4 == 0, and
+        // steps past KS read step s0 again and are not used)
+        u32x4 av[SW][MT][2];
+        u32x4 bv[SW][NT][FP4W ? 1 : 2];
+        u32x4 asw[QW][MT];  // A scale bytes: dword 0 (act_block 128) or 16 bytes (act_block 32)
+        u32x4 bsw[QW][NT];  // FP4 W scale bytes, 16 per column per 4 steps
+        float wsc[SW];      // FP8 W: the 128 x 128 block scale of each step
+#pragma unroll
+        for (int s = 0; s < SW; s++) {
+            const size_t kb = (size_t)(s < nst ? s0 + s : s0) * 128;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const uint8_t *row = aq + (size_t)min(m0 + 16 * mt + r, M - 1) * lda + kb;
+                av[s][mt][0] = *(const u32x4 *)(row + h0 + 16 * g);
+                av[s][mt][1] = *(const u32x4 *)(row + h1 + 16 * g);
+            }
+            if constexpr (FP4W) {
+                if (s % 2 == 0) {
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++) {
+                        const uint8_t *row = wc + (size_t)min(n0 + 16 * nt + r, N - 1) * (K >> 1) + (kb >> 1);
+                        bv[s][nt][0] = *(const u32x4 *)(row + h0 + 16 * g);
+                        bv[s + 1][nt][0] = *(const u32x4 *)(row + h1 + 16 * g);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    const uint8_t *row = wc + (size_t)min(n0 + 16 * nt + r, N - 1) * K + kb;
+                    bv[s][nt][0] = *(const u32x4 *)(row + h0 + 16 * g);
+                    bv[s][nt][1] = *(const u32x4 *)(row + h1 + 16 * g);
+                }
+                wsc[s] = ((const float *)ws)[(size_t)(n0 >> 7) * KS + (kb >> 7)];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < QW; q++) {
+            const int sq = s0 + 4 * q;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const size_t m = min(m0 + 16 * mt + r, M - 1);
+                if (act32) asw[q][mt] = *(const u32x4 *)(as_ + m * (K >> 5) + 4 * sq);
+                else asw[q][mt][0] = *(const uint32_t *)(as_ + m * KS + sq);
+            }
+            if constexpr (FP4W) {
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    bsw[q][nt] = *(const u32x4 *)((const uint8_t *)ws + (size_t)min(n0 + 16 * nt + r, N - 1) * (K >> 5) + 4 * sq);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // 2. halves back in operand order, then the MFMAs, NT independent accumulators per step
+        const int gsh = 8 * g;
+#pragma unroll
+        for (int s = 0; s < SW; s++) {
+            i32x8 b[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                if constexpr (FP4W) {
+                    const u32x4 x0 = bv[s & ~1][nt][0], x1 = bv[s | 1][nt][0];
+                    const u32x4 b0 = (odd == (s & 1)) ? x0 : x1;
+                    b[nt] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], 0, 0, 0, 0};
+                } else {
+                    const u32x4 x0 = bv[s][nt][0], x1 = bv[s][nt][1];
+                    const u32x4 b0 = odd ? x1 : x0, b1 = odd ? x0 : x1;
+                    b[nt] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+                }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const u32x4 x0 = av[s][mt][0], x1 = av[s][mt][1];
+                const u32x4 a0 = odd ? x1 : x0, a1 = odd ? x0 : x1;
+                const i32x8 a = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+                const uint32_t aw = asw[s / 4][mt][act32 ? s % 4 : 0];
+                const int ascale = (int)(act32 ? aw >> gsh : aw >> (8 * (s % 4)));
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    if constexpr (FP4W) {
+                        const int bscale = (int)(bsw[s / 4][nt][s % 4] >> gsh);
+                        acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b[nt], acc[mt][nt], 0, 4, 0,
+                                                                                       ascale, 0, bscale);
+                    } else {
+                        const f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                            a, b[nt], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, ascale, 0, 127);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) acc[mt][nt][e] = fmaf(wsc[s], d[e], acc[mt][nt][e]);
+                    }
+                }
+            }
+        }
+    }
+    // 3. the workgroup's sum in wave order (idle waves add zeros); thread tid takes q = tid + kThreads j
+#pragma unroll
+    for (int t = 0; t < MT * NT; t++) red[(wave * MT * NT + t) * 64 + lane] = acc[t / NT][t % NT];
+    __syncthreads();
+    constexpr int kPer = (kTileVecs + kThreads - 1) / kThreads;
+#pragma unroll
+    for (int j = 0; j < kPer; j++) {
+        const int q = tid + kThreads * j;
+        if (q >= kTileVecs) break;
+        f32x4 v = red[q];
+#pragma unroll
+        for (int w = 1; w < NW; w++) v += red[w * kTileVecs + q];
+        // element e of v is row 16 mt + 4 g' + e, column n0 + 16 nt + r' of the lane q % 64
+        const int t = q >> 6, ql = q & 63, mt = t / NT, nt = t % NT;
+        const int n = n0 + 16 * nt + (ql & 15);
+        if (n >= N) continue;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int m = m0 + 16 * mt + 4 * (ql >> 4) + e;
+            if (m >= M) continue;
+            if (y_f32) ((float *)y)[(size_t)m * N + n] = v[e];
+            else ((uint16_t *)y)[(size_t)m * N + n] = f32_to_bf16_bits(v[e]);
+        }
+    }
+}
+
 // Tile shape and split of K, chosen per shape (each choice measured fastest for its shape):
+//   variant 4, k_gemm_one with 32 x 64 tiles on 4 waves of 4 steps, when K % 512 == 0, K <= 2048, m > 32
+//     and the tiles give >= 192 workgroups (7168 x 2048: 9.0 -> 6.6 us against variant 2);
+//   variant 3, k_gemm_one with 16 x 32 tiles on up to 16 waves of 4 steps, when K % 512 == 0,
+//     K <= 8192, m > 32 and the tiles give >= 192 workgroups (2048 x 7168: 11.7 -> 8.3 us against
+//     variant 0, and no partial tiles or second launch);
 //   variant 2, 32 x 64 tiles (two workgroups per 64 columns when m > 32) and 16 waves of one step
 //     each, when one slice covers K (<= 16 steps) and the tiles give >= 192 workgroups: per
 //     workgroup 32 rows of activations and 64 columns of weights instead of 64 and 32 (7168 x 2048);
@@ -251,10 +416,19 @@ struct GemmPlan {
     int variant, mt, nt, ntiles, mgroups, slices, steps;
 };
 
-static GemmPlan gemm_plan(int m, int n, int k) {
+// one_launch: variants 3 and 4 allowed (their scale loads need 16-byte aligned scale arrays).
+static GemmPlan gemm_plan(int m, int n, int k, bool one_launch = true) {
     GemmPlan p;
     const int ks = k / 128;
     p.mgroups = 1;
+    if (one_launch && ks % 4 == 0 && ks <= 16 && m > 32 && ((n + 63) / 64) * ((m + 31) / 32) >= 192) {
+        p.variant = 4, p.mt = 2, p.nt = 4, p.ntiles = (n + 63) / 64, p.mgroups = (m + 31) / 32, p.slices = 1, p.steps = ks;
+        return p;
+    }
+    if (one_launch && ks % 4 == 0 && ks <= 64 && m > 32 && ((n + 31) / 32) * ((m + 15) / 16) >= 192) {
+        p.variant = 3, p.mt = 1, p.nt = 2, p.ntiles = (n + 31) / 32, p.mgroups = (m + 15) / 16, p.slices = 1, p.steps = ks;
+        return p;
+    }
     if (ks <= 16 && m > 32 && 2 * ((n + 63) / 64) >= 192) {
         p.variant = 2, p.mt = 2, p.nt = 4, p.ntiles = (n + 63) / 64, p.mgroups = 2, p.slices = 1, p.steps = ks;
         return p;
@@ -277,9 +451,11 @@ static uint64_t part_bytes(const GemmPlan &p) {
 }
 
 // Bytes the partial tiles take at the front of `work`: the larger of the plans for m and for m <= 32
-// (the only way m changes the plan), so a workspace sized for m also serves every smaller m.
+// (the only way m changes the plan), so a workspace sized for m also serves every smaller m. Both
+// are the plans without variants 3 and 4, which need no partials: a call whose scale arrays are not
+// 16-byte aligned falls back to those plans.
 static uint64_t part_reserve(int m, int n, int k) {
-    return a256(std::max(part_bytes(gemm_plan(m, n, k)), part_bytes(gemm_plan(1, n, k))));
+    return a256(std::max(part_bytes(gemm_plan(m, n, k, false)), part_bytes(gemm_plan(1, n, k, false))));
 }
 
 template <int MT, int NT, int NW>
@@ -310,6 +486,23 @@ static hipError_t launch_gemm_plan(const GemmPlan &p, int fmt, void *y, const vo
                                    int y_f32, void *work, hipStream_t st) {
     f32x4 *part = (f32x4 *)work;
     const int shift = act_block == 32 ? 5 : 7;
+    if (p.variant >= 3) {
+        const dim3 grid(p.ntiles * p.mgroups);
+        const int a32 = act_block == 32;
+        if (p.variant == 3 && fmt == 0)
+            hipLaunchKernelGGL((k_gemm_one<true, 1, 2, 16, 1>), grid, dim3(1024), 0, st, (const uint8_t *)codes, scales, aq,
+                               as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
+        else if (p.variant == 3)
+            hipLaunchKernelGGL((k_gemm_one<false, 1, 2, 16, 1>), grid, dim3(1024), 0, st, (const uint8_t *)codes, scales, aq,
+                               as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
+        else if (fmt == 0)
+            hipLaunchKernelGGL((k_gemm_one<true, 2, 4, 4, 1>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales, aq,
+                               as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
+        else
+            hipLaunchKernelGGL((k_gemm_one<false, 2, 4, 4, 1>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales, aq,
+                               as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
+        return hipGetLastError();
+    }
     if (p.variant == 0)
         return launch_gemm_t<4, 4, 8>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
     if (p.variant == 1)
@@ -320,7 +513,10 @@ static hipError_t launch_gemm_plan(const GemmPlan &p, int fmt, void *y, const vo
 static hipError_t launch_gemm(int fmt, void *y, const void *codes, const void *scales, const uint8_t *aq,
                               const uint8_t *as_, int m, int n, int k, int act_block, int y_f32, void *work,
                               hipStream_t st) {
-    return launch_gemm_plan(gemm_plan(m, n, k), fmt, y, codes, scales, aq, k, as_, m, n, k, act_block, y_f32, work, st);
+    // variants 3 and 4 load scale words 16 bytes at a time; unaligned scale arrays take the other plans
+    const bool aligned = aligned16(as_) && (fmt != 0 || aligned16(scales));
+    return launch_gemm_plan(gemm_plan(m, n, k, aligned), fmt, y, codes, scales, aq, k, as_, m, n, k, act_block, y_f32,
+                            work, st);
 }
 
 static int check_gemm(const char *name, int fmt, const void *y, const void *codes, const void *scales, int m, int n,

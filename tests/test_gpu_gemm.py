@@ -90,6 +90,30 @@ def test_gemm_q_matches_gemm_and_oracle(gpu, fmt, block):
     assert bits_equal(y32, np_(ops.gemm(dc, ds, x.to(gpu), fmt, block, out_f32=True)))
 
 
+@pytest.mark.parametrize("which", ["act", "weight"])
+def test_gemm_q_unaligned_scales(gpu, which):
+    # the one-launch tile plans load scale words 16 bytes at a time; scale arrays that are not 16-byte
+    # aligned take the split-K plan, which reads them byte by byte: both must match the oracle
+    m, n, k = 64, 2048, 7168
+    w = data.weight(n, k, seed=91)
+    codes, scales = oracle.quant_fp4(w.numpy())
+    x = data.activation(m, k, seed=92)
+    want = _oracle_gemm(x, oracle.dequant_fp4(codes, scales), 128)
+    dc, ds = torch.from_numpy(codes).to(gpu), torch.from_numpy(scales).to(gpu)
+    aq, a_s = ops.act_quant_e4m3(x.to(gpu), 128)
+
+    def shifted(t):
+        buf = torch.zeros(t.numel() + 16, dtype=t.dtype, device=gpu)
+        v = buf[1:1 + t.numel()].view(t.shape)
+        v.copy_(t)
+        return v
+
+    a_s2, ds2 = (shifted(a_s), ds) if which == "act" else (a_s, shifted(ds))
+    y32 = np_(ops.gemm_q(dc, ds2, aq, a_s2, ops.FP4, 128, out_f32=True))
+    y16 = np_(ops.gemm_q(dc, ds2, aq, a_s2, ops.FP4, 128))
+    _check(y32, y16, want)
+
+
 def test_gemm_deterministic_and_work_reuse(gpu):
     # split-K partials are added in slice order, so repeated calls agree bit for bit; one work buffer
     # (sized for the largest shape) serves every shape
