@@ -27,6 +27,9 @@ __device__ __forceinline__ uint32_t ld_stream_u8(const uint8_t *p) { return __bu
 
 constexpr int kWave = 64;
 
+constexpr int pow2_at_least(int n) { return n <= 1 ? 1 : 2 * pow2_at_least((n + 1) / 2); }
+constexpr int log2_exact(int n) { return n <= 1 ? 0 : 1 + log2_exact(n / 2); }
+
 // ---- bf16 <-> fp32 -------------------------------------------------------------------------------
 
 __host__ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __builtin_bit_cast(float, h << 16); }
@@ -151,59 +154,53 @@ __device__ __forceinline__ float dpp_sum(float v) {
     return v;
 }
 
-// Sums N values per lane over the 64 lanes of a wave with N-1+6-log2(N) exchanges instead of 6N:
-// at each halving step a lane keeps one half of its list and adds the partner's copy of that half.
-// On return lane L holds the full sum of value index ((L >> 3) & 7) >> (3 - log2 N)... concretely
-// `reduced_index(L)` below; every lane of a group of 64/N lanes holds the same sum. N is a power
-// of two, 1 <= N <= 8.
-template <int N>
-__device__ __forceinline__ float wave_sum_transposed(float (&v)[N], int lane) {
-    if constexpr (N >= 8) {
-        const bool up = lane & 32;
+// One DPP step of wave_sum_rows: with HALF > 0 the lane keeps v[i] (or v[i + HALF] when `up`) for
+// i < HALF and adds the DPP partner's copy of it; with HALF == 0 it adds the partner's v[0].
+template <int CTRL, int HALF, int N>
+__device__ __forceinline__ void dpp_keep_step(float (&v)[N], bool up) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float keep = up ? v[i + 4] : v[i], give = up ? v[i] : v[i + 4];
-            v[i] = keep + __shfl_xor(give, 32, kWave);
-        }
+    for (int i = 0; i < (HALF > 0 ? HALF : 1); i++) {
+        const float keep = HALF > 0 ? (up ? v[i + HALF] : v[i]) : v[i];
+        const float give = HALF > 0 ? (up ? v[i] : v[i + HALF]) : v[i];
+        v[i] = keep + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, give), CTRL, 0xF, 0xF, false));
     }
-    if constexpr (N >= 4) {
-        constexpr int o = N >= 8 ? 16 : 32;
-        const bool up = lane & o;
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const float keep = up ? v[i + 2] : v[i], give = up ? v[i] : v[i + 2];
-            v[i] = keep + __shfl_xor(give, o, kWave);
-        }
-    }
-    if constexpr (N >= 2) {
-        constexpr int o = N >= 8 ? 8 : (N >= 4 ? 16 : 32);
-        const bool up = lane & o;
-        const float keep = up ? v[1] : v[0], give = up ? v[0] : v[1];
-        v[0] = keep + __shfl_xor(give, o, kWave);
-    }
-    constexpr int first = N >= 8 ? 4 : (N >= 4 ? 8 : (N >= 2 ? 16 : 32));
-    float s = v[0];
-#pragma unroll
-    for (int o = first; o > 0; o >>= 1) s += __shfl_xor(s, o, kWave);
-    return s;
 }
 
-// Which value index lane L holds after wave_sum_transposed<N>.
+// Sums each of N values over the 64 lanes of a wave (N a power of two, <= 32) in N - 1 + 6 - log2 N
+// exchange-and-add steps instead of 6 N. Each step pairs the lanes that differ in one lane bit (5,
+// 4, 3, 2, 1, 0 in that order): while more than one value is left, the lanes with the bit clear keep
+// the lower half of their list and the others the upper half, and each adds its partner's copy of
+// the half it keeps. Partners over bit 5 / bit 4 come from v_permlane32_swap / v_permlane16_swap,
+// which exchange two whole lists in one instruction (swap(A, B) = {A lo | B lo}, {A hi | B hi} over
+// 32- / 16-lane halves); over bits 3, 2, 1, 0 from DPP row_ror:8, row_half_mirror and quad_perm. Every
+// N pairs the same lanes in the same order (a sum of two lanes is the same whichever lane forms it),
+// so a value's total does not depend on N. On return lane L holds the total of value L >> (6 - log2
+// N), as do the other 64 / N lanes of its group.
 template <int N>
-__device__ __forceinline__ int reduced_index(int lane) {
-    if constexpr (N == 8) return ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
-    if constexpr (N == 4) return ((lane >> 5) & 1) * 2 + ((lane >> 4) & 1);
-    if constexpr (N == 2) return (lane >> 5) & 1;
-    return 0;
-}
-
-// Lane that holds value index i after wave_sum_transposed<N> (the lowest such lane).
-template <int N>
-__device__ __forceinline__ int holder_lane(int i) {
-    if constexpr (N == 8) return ((i >> 2) & 1) * 32 + ((i >> 1) & 1) * 16 + (i & 1) * 8;
-    if constexpr (N == 4) return ((i >> 1) & 1) * 32 + (i & 1) * 16;
-    if constexpr (N == 2) return (i & 1) * 32;
-    return 0;
+__device__ __forceinline__ float wave_sum_rows(float (&v)[N]) {
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16 || N == 32, "N: a power of two <= 32");
+    const int lane = __lane_id();
+    auto bits = [](float f) { return __builtin_bit_cast(uint32_t, f); };
+    auto flt = [](uint32_t u) { return __builtin_bit_cast(float, u); };
+    // bits 5 and 4: partner copies by lane swaps
+    constexpr int h5 = N >= 2 ? N / 2 : 1;
+#pragma unroll
+    for (int i = 0; i < h5; i++) {
+        const auto r = __builtin_amdgcn_permlane32_swap(bits(v[i]), bits(v[N >= 2 ? i + N / 2 : i]), false, false);
+        v[i] = flt(r[0]) + flt(r[1]);
+    }
+    constexpr int h4 = N >= 4 ? N / 4 : 1;
+#pragma unroll
+    for (int i = 0; i < h4; i++) {
+        const auto r = __builtin_amdgcn_permlane16_swap(bits(v[i]), bits(v[N >= 4 ? i + N / 4 : i]), false, false);
+        v[i] = flt(r[0]) + flt(r[1]);
+    }
+    // bits 3, 2, 1, 0: DPP; a lane keeps one value of each pair and adds its partner's copy of it
+    dpp_keep_step<0x128, N / 8>(v, lane & 8);   // row_ror:8 = lane ^ 8
+    dpp_keep_step<0x141, N / 16>(v, lane & 4);  // row_half_mirror: lane ^ 7 within 8
+    dpp_keep_step<0x4E, N / 32>(v, lane & 2);   // quad_perm [2,3,0,1] = lane ^ 2
+    dpp_keep_step<0xB1, 0>(v, lane & 1);        // quad_perm [1,0,3,2] = lane ^ 1
+    return v[0];
 }
 
 }  // namespace stbl

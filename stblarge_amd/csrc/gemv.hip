@@ -80,6 +80,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     else load_x_packed<M, CH>(xw, (const uint16_t *)J.x, k, cc * CH);
     u32x4 w[R];
     uint32_t sb[R];
+    GgufRaw graw[F == WFmt::FP4_GGUF ? R : 1];  // GGUF rows: raw dwords, realigned after every load is out
     uint32_t sdw = 0;
     if constexpr (DW) {  // rows and dwords clamped into the matrix; lanes j >= 16 R repeat the last row
         const int rr = min(lane >> 4, R - 1);
@@ -95,7 +96,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
         if constexpr (F == WFmt::FP4_OCP) {
             w[r] = ld_stream(J.w + row * (k >> 1) + (size_t)cc * 16);
         } else if constexpr (F == WFmt::FP4_GGUF) {
-            load_gguf_block(J.w + (row * nch + cc) * 17, sb[r], w[r]);
+            load_gguf_raw(J.w + (row * nch + cc) * 17, graw[r]);
         } else {
             w[r] = ld_stream(J.w + row * k + (size_t)cc * 16);
         }
@@ -103,8 +104,14 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     if constexpr (kStageScales && !kScalesEarly) load_scale_block();
     // With 2-4 tokens every load above is issued before anything below runs: without this fence the
     // scheduler trades registers for issue order and holds x loads of later tokens back behind the
-    // first waits (4 tokens: 6.7 instead of 6.0 us at 2048x7168). One token gains nothing from it.
-    if constexpr (M >= 2) __builtin_amdgcn_sched_barrier(0);
+    // first waits (4 tokens: 6.7 instead of 6.0 us at 2048x7168). One bf16 token gains nothing from
+    // it; with fp32 x (the GGUF blocks' five dword loads per row) the compiler otherwise puts waits
+    // between the rows' loads.
+    if constexpr (M >= 2 || XF32) __builtin_amdgcn_sched_barrier(0);
+    if constexpr (F == WFmt::FP4_GGUF) {
+#pragma unroll
+        for (int r = 0; r < R; r++) realign_gguf(graw[r], sb[r], w[r]);
+    }
     float lscale = 1.f;  // FP8: one block scale per lane for the whole tile
     if constexpr (F == WFmt::FP8_B128)
         lscale = ((const float *)J.s)[(size_t)(row0 >> 7) * ((k + 127) >> 7) + ((cc * 16) >> 7)];
@@ -129,9 +136,13 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
             sb[r] = (d >> (8 * (lane & 3))) & 255u;
         }
     }
-    // 2. products, scales, masking; 3. lane reduction
+    // 2. products, scales, masking; 3. lane reduction of all M * R values together (wave_sum_rows:
+    //    lane L ends with value L >> (6 - log2 NV), padded with zeros to a power of two)
+    constexpr int NV = pow2_at_least(M * R), kShift = 6 - log2_exact(NV);
     __shared__ float red[kMaxWaves][M * R];
-    float tot[M * R];
+    float vals[NV];
+#pragma unroll
+    for (int i = M * R; i < NV; i++) vals[i] = 0.f;
 #pragma unroll
     for (int r = 0; r < R; r++) {
         float s[M];
@@ -142,8 +153,11 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
         else if constexpr (F == WFmt::FP8_B128) scale = lscale;
         else scale = e8m0_to_f32(lsb);
 #pragma unroll
-        for (int t = 0; t < M; t++) tot[t * R + r] = dpp_sum(active ? s[t] * scale : 0.f);
+        for (int t = 0; t < M; t++) vals[t * R + r] = active ? s[t] * scale : 0.f;
     }
+    const float mine = wave_sum_rows<NV>(vals);
+    const int vi = lane >> kShift;
+    const bool holder = (lane & ((1 << kShift) - 1)) == 0 && vi < M * R;
     auto store = [&](int i, float v) {
         const int t = i / R, r = i % R;
         if (row0 + r >= rows) return;
@@ -153,16 +167,10 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
         else ((float *)J.y)[at] = bf16_round(v);
     };
     if (waves == 1) {
-        if (lane == 63) {
-#pragma unroll
-            for (int i = 0; i < M * R; i++) store(i, tot[i]);
-        }
+        if (holder) store(vi, mine);
         return;
     }
-    if (lane == 63) {
-#pragma unroll
-        for (int i = 0; i < M * R; i++) red[wave][i] = tot[i];
-    }
+    if (holder) red[wave][vi] = mine;
     __syncthreads();
     if ((int)threadIdx.x < M * R) {
         const int i = threadIdx.x;

@@ -42,19 +42,33 @@ enum OutMode { OUT_BF16 = 0, OUT_F32 = 1, OUT_F32_ROUNDED = 2 };
 
 // A GGUF block c of a row sits at byte 17 c, so it is only byte aligned: read the five dwords that
 // cover it from the enclosing 4-byte boundary (each dword starts inside the buffer, and a 4-byte
-// aligned dword never crosses a page) and realign with v_alignbyte.
-__device__ __forceinline__ void load_gguf_block(const uint8_t *blk, uint32_t &scale, u32x4 &codes) {
+// aligned dword never crosses a page) and realign with v_alignbyte. The loads and the realignment
+// are separate steps so that a kernel can issue every row's loads before it waits for the first.
+struct GgufRaw {
+    uint32_t v[5];
+    uint32_t sh;  // the block's byte offset in its first dword
+};
+
+__device__ __forceinline__ void load_gguf_raw(const uint8_t *blk, GgufRaw &raw) {
     // pointer arithmetic, not an integer round trip: the loads stay global loads (as flat loads they
     // cost 2-7% on the reference ABI's GEMVs)
-    const uint32_t sh = (uint32_t)((uintptr_t)blk & 3);
-    const uint32_t *d = (const uint32_t *)(blk - sh);
-    uint32_t v[5];
+    raw.sh = (uint32_t)((uintptr_t)blk & 3);
+    const uint32_t *d = (const uint32_t *)(blk - raw.sh);
 #pragma unroll
-    for (int i = 0; i < 5; i++) v[i] = d[i];
-    scale = (v[0] >> (8 * sh)) & 0xffu;
-    const uint32_t off = sh + 1;  // first code byte, 1..4 bytes past d
+    for (int i = 0; i < 5; i++) raw.v[i] = d[i];
+}
+
+__device__ __forceinline__ void realign_gguf(const GgufRaw &raw, uint32_t &scale, u32x4 &codes) {
+    scale = (raw.v[0] >> (8 * raw.sh)) & 0xffu;
+    const uint32_t off = raw.sh + 1;  // first code byte, 1..4 bytes past the first dword
 #pragma unroll
-    for (int j = 0; j < 4; j++) codes[j] = off == 4 ? v[j + 1] : __builtin_amdgcn_alignbyte(v[j + 1], v[j], off);
+    for (int j = 0; j < 4; j++) codes[j] = off == 4 ? raw.v[j + 1] : __builtin_amdgcn_alignbyte(raw.v[j + 1], raw.v[j], off);
+}
+
+__device__ __forceinline__ void load_gguf_block(const uint8_t *blk, uint32_t &scale, u32x4 &codes) {
+    GgufRaw raw;
+    load_gguf_raw(blk, raw);
+    realign_gguf(raw, scale, codes);
 }
 
 // x chunk of CH elements for M tokens, widened to fp32. x is bf16 or fp32 [M][k].
