@@ -90,15 +90,19 @@ __device__ __forceinline__ float chunk_scale(uint32_t sb, float lscale) {
     else return lscale;
 }
 
-// Sums v (one value per lane, reduced with dpp_sum) over the waves: lane 63 of every wave writes
-// red[wave][i]; after the barrier thread i < n holds the total of value i in *out.
+// Sums N per-lane values over the wave (wave_sum_rows, padded with zeros to a power of two) and over
+// the waves: the first lane holding each value's wave total writes red[wave][i]; after the barrier
+// thread i < N holds the total of value i in *out.
 template <int N>
-__device__ __forceinline__ bool wave_total(float (&tot)[N], float (*red)[N], float *out) {
+__device__ __forceinline__ bool wave_total(float (&vals)[N], float (*red)[N], float *out) {
+    constexpr int NV = pow2_at_least(N), kShift = 6 - log2_exact(NV);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    if (lane == 63) {
+    float p[NV];
 #pragma unroll
-        for (int i = 0; i < N; i++) red[wave][i] = tot[i];
-    }
+    for (int i = 0; i < NV; i++) p[i] = i < N ? vals[i] : 0.f;
+    const float mine = wave_sum_rows<NV>(p);
+    const int vi = lane >> kShift;
+    if ((lane & ((1 << kShift) - 1)) == 0 && vi < N) red[wave][vi] = mine;
     __syncthreads();
     const int i = threadIdx.x;
     if (i >= N) return false;
@@ -184,8 +188,8 @@ __global__ __launch_bounds__(512) void k_moe_gateup(MoeJobs jobs, ExpertLayout L
         const float a = chunk_scale<F>(sg[r], lg), b = chunk_scale<F>(su[r], lu);
 #pragma unroll
         for (int t = 0; t < M; t++) {
-            tot[(t * R + r) * 2] = dpp_sum(active ? sgv[t] * a : 0.f);
-            tot[(t * R + r) * 2 + 1] = dpp_sum(active ? suv[t] * b : 0.f);
+            tot[(t * R + r) * 2] = active ? sgv[t] * a : 0.f;
+            tot[(t * R + r) * 2 + 1] = active ? suv[t] * b : 0.f;
         }
     }
     // thread q = (t * R + r) * 2 + {0 gate, 1 up}; the even thread finishes the pair
@@ -258,7 +262,7 @@ __global__ __launch_bounds__(512) void k_moe_down(MoeJobs jobs, ExpertLayout L, 
         chunk_dot_packed<F, M, CH>(s, wd[r], xw);
         const float a = chunk_scale<F>(sd[r], ld);
 #pragma unroll
-        for (int t = 0; t < M; t++) tot[t * R + r] = dpp_sum(active ? s[t] * a : 0.f);
+        for (int t = 0; t < M; t++) tot[t * R + r] = active ? s[t] * a : 0.f;
     }
     float v = 0.f;
     if (!wave_total<M * R>(tot, red, &v)) return;
