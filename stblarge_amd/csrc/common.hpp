@@ -60,6 +60,13 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t s) {
     return __uint_as_float(b);
 }
 
+// The scaled conversions (v_cvt_scalef32_pk_{f32,bf16}_fp4, _bf16_fp8) multiply by 2^(e - 127) for a
+// scale operand whose exponent field is e, exactly as E8M0 defines it: measured on gfx950 against
+// e2m1 / e4m3 code x 2^(s - 127) for every scale byte s and code (s = 0 gives 2^-127, s = 255 NaN,
+// results rounded like a single product). So an E8M0 byte placed in the exponent field is the scale
+// operand, and a chunk's scale is applied inside its conversions instead of by a decode and a multiply.
+__device__ __forceinline__ float e8m0_cvt_scale(uint32_t s) { return __uint_as_float((s & 0xffu) << 23); }
+
 // 2^ceil(log2 t) for positive normal t by its exponent and mantissa bits (ref/kernel.py:22-26).
 __device__ __forceinline__ float pow2_ceil(float t) {
     const uint32_t b = __float_as_uint(t);
@@ -74,10 +81,11 @@ __device__ __forceinline__ f32x2 e4m3x2(uint32_t w, bool hi) {
     return hi ? __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true) : __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
 }
 
-// The two e2m1 codes of byte `sel` of w -> fp32 (low nibble in .x), exactly.
+// The two e2m1 codes of byte `sel` of w -> fp32 (low nibble in .x), exactly, times `cs` (a conversion
+// scale from e8m0_cvt_scale, or 1).
 template <int sel>
-__device__ __forceinline__ f32x2 e2m1x2(uint32_t w) {
-    return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, sel);
+__device__ __forceinline__ f32x2 e2m1x2(uint32_t w, float cs = 1.0f) {
+    return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, cs, sel);
 }
 
 // Scalar e4m3 decode (closed form), used where a single value is needed.

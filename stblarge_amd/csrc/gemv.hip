@@ -126,7 +126,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
         __syncthreads();
         const uint8_t *sl = (const uint8_t *)lds_sc + (((uintptr_t)J.s + (size_t)row0 * nch) & 15);
 #pragma unroll
-        for (int r = 0; r < R; r++) sb[r] = sl[min((size_t)r * nch + cc, sc_len - 1)];
+        for (int r = 0; r < R; r++) sb[r] = sl[r * nch + cc];
     }
 
     if constexpr (DW) {
@@ -145,13 +145,17 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     for (int i = M * R; i < NV; i++) vals[i] = 0.f;
 #pragma unroll
     for (int r = 0; r < R; r++) {
+        // E8M0 scales (FP4; FP8 E8M0 with bf16 x) go into the conversions; the FP8 fp32 block scale
+        // and the fp32-x FP8 path multiply the chunk sum
         float s[M];
-        if constexpr (XF32) chunk_dot<F, M, CH>(s, w[r], xf);
+        if constexpr (XF32 && T::fp4) chunk_dot<F, M, CH>(s, w[r], xf, e8m0_cvt_scale(sb[r]));
+        else if constexpr (XF32) chunk_dot<F, M, CH>(s, w[r], xf);
+        else if constexpr (T::fp4) chunk_dot_packed<F, M, CH>(s, w[r], xw, e8m0_cvt_scale(sb[r]));
+        else if constexpr (F == WFmt::FP8_E8M0) chunk_dot_packed<F, M, CH>(s, w[r], xw, e8m0_cvt_scale(lsb));
         else chunk_dot_packed<F, M, CH>(s, w[r], xw);
-        float scale;
-        if constexpr (T::fp4) scale = e8m0_to_f32(sb[r]);
-        else if constexpr (F == WFmt::FP8_B128) scale = lscale;
-        else scale = e8m0_to_f32(lsb);
+        float scale = 1.f;
+        if constexpr (F == WFmt::FP8_B128) scale = lscale;
+        else if constexpr (F == WFmt::FP8_E8M0 && XF32) scale = e8m0_to_f32(lsb);
 #pragma unroll
         for (int t = 0; t < M; t++) vals[t * R + r] = active ? s[t] * scale : 0.f;
     }

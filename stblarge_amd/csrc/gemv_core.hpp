@@ -98,15 +98,16 @@ __device__ __forceinline__ void load_x(float (&xf)[M][CH], const void *x, int k,
     }
 }
 
-// sum over the chunk of x * (unscaled) weight, for each token.
+// sum over the chunk of x * weight for each token; FP4 weights are converted times `cs` (their E8M0
+// scale as e8m0_cvt_scale, or 1), FP8 weights unscaled.
 template <WFmt F, int M, int CH>
-__device__ __forceinline__ void chunk_dot(float (&s)[M], const u32x4 w, const float (&xf)[M][CH]) {
+__device__ __forceinline__ void chunk_dot(float (&s)[M], const u32x4 w, const float (&xf)[M][CH], float cs = 1.0f) {
 #pragma unroll
     for (int t = 0; t < M; t++) s[t] = 0.f;
 #pragma unroll
     for (int d = 0; d < 4; d++) {
         if constexpr (WTraits<F>::fp4) {
-            const f32x2 a = e2m1x2<0>(w[d]), b = e2m1x2<1>(w[d]), c = e2m1x2<2>(w[d]), e = e2m1x2<3>(w[d]);
+            const f32x2 a = e2m1x2<0>(w[d], cs), b = e2m1x2<1>(w[d], cs), c = e2m1x2<2>(w[d], cs), e = e2m1x2<3>(w[d], cs);
 #pragma unroll
             for (int t = 0; t < M; t++) {
                 if constexpr (F == WFmt::FP4_OCP) {  // byte b: elements 2b, 2b+1
@@ -221,9 +222,11 @@ __device__ __forceinline__ float dot2(bf16x2 w, uint32_t x, float acc) {
     return __builtin_amdgcn_fdot2_f32_bf16(w, __builtin_bit_cast(bf16x2, x), acc, false);
 }
 
-// sum over the chunk of x * (unscaled) weight for each token; OCP FP4 or FP8 weights.
+// sum over the chunk of x * weight for each token; OCP FP4 or FP8 weights converted times `cs` (an
+// E8M0 scale as e8m0_cvt_scale, or 1).
 template <WFmt F, int M, int CH>
-__device__ __forceinline__ void chunk_dot_packed(float (&s)[M], const u32x4 w, const uint32_t (&xw)[M][CH / 2]) {
+__device__ __forceinline__ void chunk_dot_packed(float (&s)[M], const u32x4 w, const uint32_t (&xw)[M][CH / 2],
+                                                 float cs = 1.0f) {
     static_assert(F == WFmt::FP4_OCP || F == WFmt::FP8_B128 || F == WFmt::FP8_E8M0, "packed path: OCP FP4 or FP8");
     float s2[M];
 #pragma unroll
@@ -231,10 +234,10 @@ __device__ __forceinline__ void chunk_dot_packed(float (&s)[M], const u32x4 w, c
 #pragma unroll
     for (int d = 0; d < 4; d++) {
         if constexpr (F == WFmt::FP4_OCP) {  // byte b of dword d: elements 8d + 2b, +1 = x word 4d + b
-            const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 0);
-            const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 1);
-            const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 2);
-            const bf16x2 e = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 3);
+            const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], cs, 0);
+            const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], cs, 1);
+            const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], cs, 2);
+            const bf16x2 e = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], cs, 3);
 #pragma unroll
             for (int t = 0; t < M; t++) {
                 s[t] = dot2(a, xw[t][4 * d], s[t]);
@@ -243,8 +246,8 @@ __device__ __forceinline__ void chunk_dot_packed(float (&s)[M], const u32x4 w, c
                 s2[t] = dot2(e, xw[t][4 * d + 3], s2[t]);
             }
         } else {  // bytes 0,1 / 2,3 of dword d: elements 4d, 4d+1 / 4d+2, 4d+3 = x words 2d / 2d+1
-            const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[d], 1.0f, false);
-            const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[d], 1.0f, true);
+            const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[d], cs, false);
+            const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[d], cs, true);
 #pragma unroll
             for (int t = 0; t < M; t++) {
                 s[t] = dot2(a, xw[t][2 * d], s[t]);

@@ -69,10 +69,10 @@ struct SlotMat {
         return __builtin_nontemporal_load((const uint32_t *)(scales + row * (size_t)(k >> 5)) + dwi);
     }
     // FP8: the lane's block scale for a tile whose rows share row0's 128-row (fp32 scales) or
-    // 32-row (E8M0 scales) block
+    // 32-row (E8M0 scales, returned as the conversion scale of e8m0_cvt_scale) block
     __device__ __forceinline__ float block_scale(int row0, int cc) const {
         if constexpr (F == WFmt::FP8_E8M0)
-            return e8m0_to_f32(scales[(size_t)(row0 >> 5) * (k >> 5) + ((cc * 16) >> 5)]);
+            return e8m0_cvt_scale(scales[(size_t)(row0 >> 5) * (k >> 5) + ((cc * 16) >> 5)]);
         else return ((const float *)scales)[(size_t)(row0 >> 7) * ((k + 127) >> 7) + ((cc * 16) >> 7)];
     }
 };
@@ -84,10 +84,18 @@ __device__ __forceinline__ uint32_t dw_scale_byte(const uint32_t *sdw, int vr, i
     return (d >> (8 * (lane & 3))) & 255u;
 }
 
+// A chunk's scale: E8M0 scales (FP4 bytes; FP8 E8M0 blocks, already a conversion scale) go into the
+// conversions (conv_scale), the fp32 128x128 block scale multiplies the chunk sum (post_scale).
 template <WFmt F>
-__device__ __forceinline__ float chunk_scale(uint32_t sb, float lscale) {
-    if constexpr (WTraits<F>::fp4) return e8m0_to_f32(sb);
-    else return lscale;
+__device__ __forceinline__ float conv_scale(uint32_t sb, float lscale) {
+    if constexpr (WTraits<F>::fp4) return e8m0_cvt_scale(sb);
+    else if constexpr (F == WFmt::FP8_E8M0) return lscale;
+    else return 1.f;
+}
+template <WFmt F>
+__device__ __forceinline__ float post_scale(float lscale) {
+    if constexpr (F == WFmt::FP8_B128) return lscale;
+    else return 1.f;
 }
 
 // Sums N per-lane values over the wave (wave_sum_rows, padded with zeros to a power of two) and over
@@ -183,9 +191,9 @@ __global__ __launch_bounds__(512) void k_moe_gateup(MoeJobs jobs, ExpertLayout L
 #pragma unroll
     for (int r = 0; r < R; r++) {
         float sgv[M], suv[M];
-        chunk_dot_packed<F, M, CH>(sgv, wg[r], xw);
-        chunk_dot_packed<F, M, CH>(suv, wu[r], xw);
-        const float a = chunk_scale<F>(sg[r], lg), b = chunk_scale<F>(su[r], lu);
+        chunk_dot_packed<F, M, CH>(sgv, wg[r], xw, conv_scale<F>(sg[r], lg));
+        chunk_dot_packed<F, M, CH>(suv, wu[r], xw, conv_scale<F>(su[r], lu));
+        const float a = post_scale<F>(lg), b = post_scale<F>(lu);
 #pragma unroll
         for (int t = 0; t < M; t++) {
             tot[(t * R + r) * 2] = active ? sgv[t] * a : 0.f;
@@ -259,8 +267,8 @@ __global__ __launch_bounds__(512) void k_moe_down(MoeJobs jobs, ExpertLayout L, 
 #pragma unroll
     for (int r = 0; r < R; r++) {
         float s[M];
-        chunk_dot_packed<F, M, CH>(s, wd[r], xw);
-        const float a = chunk_scale<F>(sd[r], ld);
+        chunk_dot_packed<F, M, CH>(s, wd[r], xw, conv_scale<F>(sd[r], ld));
+        const float a = post_scale<F>(ld);
 #pragma unroll
         for (int t = 0; t < M; t++) tot[t * R + r] = active ? s[t] * a : 0.f;
     }
