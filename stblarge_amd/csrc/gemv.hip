@@ -56,7 +56,8 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     constexpr int kScaleLoads = R > 8 ? 2 : 1;  // units <= R nch / 16 + 2 <= kScaleLoads * threads
     // One slot past the block takes the writes of threads without a unit, so the LDS write is
     // unconditional: a conditional one lets the compiler sink the load into the branch.
-    __shared__ u32x4 lds_sc[kStageScales ? kMaxScaleUnits + 1 : 1];
+    constexpr int kScaleUnits = R * kMaxWaves * 64 / 16 + 2;  // 16-byte units of the staged block, at most
+    __shared__ u32x4 lds_sc[kStageScales ? kScaleUnits + 1 : 1];
     u32x4 scv[kScaleLoads] = {};
     size_t sc_len = 0;
     int sc_units = 0;
@@ -121,12 +122,12 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
 #pragma unroll
         for (int i = 0; i < kScaleLoads; i++) {
             const int u = threadIdx.x + i * blockDim.x;
-            lds_sc[u < sc_units ? u : kMaxScaleUnits] = scv[i];
+            lds_sc[u < sc_units ? u : kScaleUnits] = scv[i];
         }
         __syncthreads();
         const uint8_t *sl = (const uint8_t *)lds_sc + (((uintptr_t)J.s + (size_t)row0 * nch) & 15);
 #pragma unroll
-        for (int r = 0; r < R; r++) sb[r] = sl[r * nch + cc];
+        for (int r = 0; r < R; r++) sb[r] = sl[r * nch + cc];  // < R nch + 15: inside lds_sc
     }
 
     if constexpr (DW) {
@@ -362,7 +363,13 @@ static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int o
         return launch_r<F, XF32, M, 4>(jobs, njobs, rows, k, out_mode, st);
     } else {
         const long wgs8 = (long)ceil_div(rows, 8) * njobs * ceil_div(k / WTraits<F>::CH, 64);
-        if (wgs8 >= 8192) return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
+        if (wgs8 >= 8192) {
+            // one FP4 token over rows of 4+ waves: 16 rows (16 x 2048x7168: 21.4 -> 21.0 us, 64 x 76.4
+            // -> 73.6; rows of one wave lose: 16 x 7168x2048 20.3 -> 21.1)
+            if constexpr (F == WFmt::FP4_OCP && M == 1)
+                if (k / WTraits<F>::CH > 3 * 64) return launch_r<F, XF32, M, 16>(jobs, njobs, rows, k, out_mode, st);
+            return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
+        }
         const int cus = device_cus();
         // one token of FP4 over rows of 4+ waves: 8-row tiles when they still fill every CU, halving the x
         // reads per weight byte again (2048x7168: 3.85 -> 3.80 us; rows of one wave lose: 7168x2048

@@ -12,10 +12,10 @@
 namespace stbl {
 
 constexpr int kMaxWaves = 8;  // K <= 512 chunks: 16384 FP4 / 8192 FP8 elements
-// 16-byte units of a tile's OCP FP4 scale block (R <= kMaxStageRows rows of at most kMaxWaves * 64
-// bytes), plus one for a block that starts mid-unit and one for its end.
-constexpr int kMaxStageRows = 8;
-constexpr int kMaxScaleUnits = kMaxStageRows * kMaxWaves * 64 / 16 + 2;
+// A tile's OCP FP4 scale block is staged through LDS for tiles of at most kMaxStageRows rows (each
+// row at most kMaxWaves * 64 bytes; the block takes R * kMaxWaves * 64 / 16 units of 16 bytes, plus
+// one for a block that starts mid-unit and one for its end).
+constexpr int kMaxStageRows = 16;
 constexpr int kMxBatch = 16;  // matrices per launch of the reference ABI's batch (stbl/kernels.h:18)
 constexpr int kMaxJobs = 64;  // matrices per launch of the v2 batches (the MoE step's gate/up launches hold up to 66)
 

@@ -215,9 +215,8 @@ def test_gemv_batch(gpu, fmt, rows, k, n):
 
 @pytest.mark.parametrize("rows,k", [(1100, 7168), (4100, 2048)])
 def test_gemv_batch_ragged_rows_eight_row_tiles(gpu, rows, k):
-    # 16 x 1100 rows at K = 7168 (or 16 x 4100 at K = 2048) are enough workgroups for 8-row tiles in
-    # workgroups of several row groups sharing x; 1100 = 137 x 8 + 4 leaves the last tile half empty,
-    # and 4100 rows leave most row groups of the last workgroup past the matrix
+    # 16 x 1100 rows at K = 7168 take 16-row tiles (rows of 4 waves), 16 x 4100 at K = 2048 8-row
+    # tiles; 1100 = 68 x 16 + 12 and 4100 = 512 x 8 + 4 leave the last tile partly past the matrix
     n = 16
     cs, ss, xs, wants = [], [], [], []
     for j in range(n):
