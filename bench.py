@@ -337,8 +337,8 @@ def compat_gemv_workload(torch, kind, rows, k, steps, warmup, group_rows=0):
 def compat_batch_workload(torch, rows, k, n, steps, warmup):
     """stbl_gemv_mxfp4_batch as the reference engine issues it for one layer's experts
     (stbl/model.cu:536-539: gate and up of every selected expert in one call, then their down
-    projections in another): n GGUF matrices per launch, fp32 x, every launch on n different
-    matrices from a >= 512 MB rotation."""
+    projections in another): n GGUF matrices per launch, fp32 x quantized by stbl_act_quant_fp8 as
+    the engine's is (:516-540), every launch on n different matrices from a >= 512 MB rotation."""
     from stblarge_amd import _lib, ops
 
     dev = torch.device("cuda:0")
@@ -359,6 +359,8 @@ def compat_batch_workload(torch, rows, k, n, steps, warmup):
     w_arrs = [(P * n)(*[mats[i * n + j].data_ptr() for j in range(n)]) for i in range(sets)]
     lib = _lib.load()
     st = ops._stream
+    for x in xs:
+        lib.stbl_act_quant_fp8(P(x.data_ptr()), k, st())
 
     def launch(i):
         lib.stbl_gemv_mxfp4_batch(y_arr, w_arrs[i], x_arr, n, rows, k, st())

@@ -19,6 +19,7 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));  // an f8f6f4 MFMA operand
 
 // Loads of weights, which are read once per launch: the non-temporal hint lets the caches evict
 // them first (measured: a plain streaming read of 128 MiB to 1 GiB runs 10-14% faster with it).

@@ -30,8 +30,6 @@
 
 namespace stbl {
 
-typedef int i32x8 __attribute__((ext_vector_type(8)));
-
 constexpr int kGemmMaxM = 64;
 constexpr int kGemmMaxN = 1 << 20;
 

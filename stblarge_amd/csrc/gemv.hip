@@ -97,7 +97,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
         if constexpr (F == WFmt::FP4_OCP) {
             w[r] = ld_stream(J.w + row * (k >> 1) + (size_t)cc * 16);
         } else if constexpr (F == WFmt::FP4_GGUF) {
-            load_gguf_raw(J.w + (row * nch + cc) * 17, graw[r]);
+            load_gguf_raw_at(J.w + row * (size_t)(nch * 17), (uint32_t)cc * 17u, graw[r]);
         } else {
             w[r] = ld_stream(J.w + row * k + (size_t)cc * 16);
         }
@@ -106,9 +106,28 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     // With 2-4 tokens every load above is issued before anything below runs: without this fence the
     // scheduler trades registers for issue order and holds x loads of later tokens back behind the
     // first waits (4 tokens: 6.7 instead of 6.0 us at 2048x7168). One bf16 token gains nothing from
-    // it; with fp32 x (the GGUF blocks' five dword loads per row) the compiler otherwise puts waits
-    // between the rows' loads.
-    if constexpr (M >= 2 || XF32) __builtin_amdgcn_sched_barrier(0);
+    // it; with fp32 x (the GGUF blocks' five dword loads per row) or dword scales the compiler
+    // otherwise puts waits between the rows' loads (a row's registers reused for the last row).
+    if constexpr (M >= 2 || XF32 || DW) __builtin_amdgcn_sched_barrier(0);
+    // GGUF rows with fp32 x (the reference ABI): when every active lane's x chunk is bf16-exact, as the
+    // reference engine's x is (stbl_act_quant_fp8 writes e4m3 codes times powers of two,
+    // stbl/kernels.cu:54-63), the products take the packed-bf16 path (one conversion and one
+    // v_dot2_f32_bf16 per two weights instead of one conversion and two FMAs; the products are exact
+    // either way). xg[j] packs elements j and j + 16, the two nibbles of GGUF code byte j. Only the
+    // batched launches' 8- and 16-row tiles take it: with the one-round tiles of single GEMVs, whose
+    // time is load latency, the check and the second code path cost more than they save (2304x5120:
+    // 4.59 -> 4.87 us with random fp32 x).
+    constexpr bool kGgufX = F == WFmt::FP4_GGUF && XF32 && M == 1 && (R == 8 || R == 16);
+    bool gguf_bf16 = false;  // wave-uniform
+    [[maybe_unused]] uint32_t xg[kGgufX ? 16 : 1];
+    if constexpr (kGgufX) {
+        uint32_t low = 0;
+#pragma unroll
+        for (int i = 0; i < 32; i++) low |= __float_as_uint(xf[0][i]);
+        gguf_bf16 = __builtin_amdgcn_ballot_w64(active && (low & 0xffffu) != 0) == 0;
+#pragma unroll
+        for (int j = 0; j < 16; j++) xg[j] = (__float_as_uint(xf[0][j]) >> 16) | (__float_as_uint(xf[0][j + 16]) & 0xffff0000u);
+    }
     if constexpr (F == WFmt::FP4_GGUF) {
 #pragma unroll
         for (int r = 0; r < R; r++) realign_gguf(graw[r], sb[r], w[r]);
@@ -144,8 +163,14 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     float vals[NV];
 #pragma unroll
     for (int i = M * R; i < NV; i++) vals[i] = 0.f;
+    if constexpr (kGgufX) {
+        if (gguf_bf16) {
 #pragma unroll
-    for (int r = 0; r < R; r++) {
+            for (int r = 0; r < R; r++) vals[r] = active ? gguf_dot_bf16(w[r], xg, e8m0_cvt_scale(sb[r])) : 0.f;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R && !gguf_bf16; r++) {
         // E8M0 scales (FP4; FP8 E8M0 with bf16 x) go into the conversions; the FP8 fp32 block scale
         // and the fp32-x FP8 path multiply the chunk sum
         float s[M];

@@ -58,6 +58,17 @@ __device__ __forceinline__ void load_gguf_raw(const uint8_t *blk, GgufRaw &raw) 
     for (int i = 0; i < 5; i++) raw.v[i] = d[i];
 }
 
+// The same for block `off` bytes into a row at `base` (base wave-uniform, off per lane): the loads
+// take a scalar base and a 32-bit lane offset, with no 64-bit address arithmetic per lane (whose
+// register reuse once made the compiler wait for earlier loads before issuing the next row's).
+__device__ __forceinline__ void load_gguf_raw_at(const uint8_t *base, uint32_t off, GgufRaw &raw) {
+    const uint32_t a = (uint32_t)(uintptr_t)base & 3u, o = a + off;
+    raw.sh = o & 3u;
+    const uint32_t *d = (const uint32_t *)(base - a + (o & ~3u));
+#pragma unroll
+    for (int i = 0; i < 5; i++) raw.v[i] = d[i];
+}
+
 __device__ __forceinline__ void realign_gguf(const GgufRaw &raw, uint32_t &scale, u32x4 &codes) {
     scale = (raw.v[0] >> (8 * raw.sh)) & 0xffu;
     const uint32_t off = raw.sh + 1;  // first code byte, 1..4 bytes past the first dword
@@ -257,6 +268,20 @@ __device__ __forceinline__ void chunk_dot_packed(float (&s)[M], const u32x4 w, c
     }
 #pragma unroll
     for (int t = 0; t < M; t++) s[t] += s2[t];
+}
+
+// GGUF block codes (byte j: elements j and j + 16) times bf16-exact x packed as x[j] = elements j,
+// j + 16: one scaled conversion and one dot2 per code byte.
+__device__ __forceinline__ float gguf_dot_bf16(const u32x4 w, const uint32_t (&x)[16], float cs) {
+    float s = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        s = dot2(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], cs, 0), x[4 * d], s);
+        s2 = dot2(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], cs, 1), x[4 * d + 1], s2);
+        s = dot2(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], cs, 2), x[4 * d + 2], s);
+        s2 = dot2(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], cs, 3), x[4 * d + 3], s2);
+    }
+    return s + s2;
 }
 
 }  // namespace stbl

@@ -190,6 +190,68 @@ def test_stbl_gemv_mxfp4_batch(gpu, rows, k, n):
         assert_gemv(np_(y), np_(y), want, tol=2.0 ** -8)
 
 
+def _quantized_x(k, seed, gain=None):
+    # x as the reference engine hands it to the GGUF GEMVs: act_quant(x, 32) (stbl/model.cu:516-540),
+    # e4m3 codes times a power of two per 32 elements; `gain` spreads the blocks over 2^-30..2^40
+    x = data.activation(1, k, seed=seed).float().numpy()[0]
+    if gain is not None:
+        x = x * np.repeat(gain, 32).astype(np.float32)
+    return oracle.act_quant(x[None], 32, True)[2][0]
+
+
+@pytest.mark.parametrize("rows,k,n", [(2304, 5120, 1), (5120, 2304, 1), (2304, 5120, 12), (5120, 2304, 6),
+                                      (2300, 5120, 16), (999, 2560, 1), (40, 512, 3), (64, 256, 1)])
+def test_stbl_gemv_mxfp4_quantized_x(gpu, rows, k, n):
+    # with quantized x every wave takes the scaled-MFMA products (A = x's e4m3 codes and scales, B =
+    # the GGUF blocks as they lie); the reference engine's shapes and batches, 16-row tiles with a
+    # partial last tile, 9-10 row one-round tiles, 2-row and 1-row tiles
+    rng = np.random.default_rng(rows + k + n)
+    ys, ws, xs, wants = [], [], [], []
+    for j in range(n):
+        codes = rng.integers(0, 256, (rows, k // 2), dtype=np.uint8)
+        sc = rng.integers(118, 126, (rows, k // 32), dtype=np.uint8)
+        x = _quantized_x(k, 300 + j)
+        wants.append(oracle.gemv_fp4(codes, sc, x[None])[0])
+        ws.append(torch.from_numpy(oracle.ocp_to_gguf17(codes, sc)).to(gpu))
+        xs.append(torch.from_numpy(x).to(gpu))
+        ys.append(torch.empty(rows, device=gpu))
+    if n == 1:
+        ops.stbl_gemv_mxfp4(ys[0], ws[0], xs[0], rows, k)
+    else:
+        ops.stbl_gemv_mxfp4_batch(ys, ws, xs, rows, k)
+    for y, want in zip(ys, wants):
+        assert_gemv(np_(y), np_(y), want, tol=2.0 ** -8)
+
+
+def test_stbl_gemv_mxfp4_mixed_x(gpu):
+    # one launch over x that the MFMA products take and x they must not: (0) quantized x whose blocks
+    # span 2^-30..2^40, with zero blocks; (1) quantized x with one element moved off the e4m3 grid,
+    # so the wave holding its block takes the fp32 products and the other waves the MFMA; (2) x with
+    # an infinite element (every output inf or nan, as fp32 products give); (3) random fp32 x
+    rows, k = 640, 5120
+    rng = np.random.default_rng(17)
+    gain = 2.0 ** rng.integers(-30, 41, k // 32)
+    gain[[3, 90]] = 0.0
+    x0 = _quantized_x(k, 400, gain)
+    x1 = _quantized_x(k, 401)
+    x1[70 * 32 + 5] = np.nextafter(x1[70 * 32 + 5], np.float32(np.inf))
+    x2 = _quantized_x(k, 402)
+    x2[2000] = np.inf
+    x3 = data.activation(1, k, seed=403).float().numpy()[0]
+    ys, ws, xs, want = [], [], [], []
+    for j, x in enumerate((x0, x1, x2, x3)):
+        codes = rng.integers(0, 256, (rows, k // 2), dtype=np.uint8)
+        sc = rng.integers(118, 126, (rows, k // 32), dtype=np.uint8)
+        want.append(oracle.gemv_fp4(codes, sc, x[None])[0] if j != 2 else None)
+        ws.append(torch.from_numpy(oracle.ocp_to_gguf17(codes, sc)).to(gpu))
+        xs.append(torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(gpu))
+        ys.append(torch.empty(rows, device=gpu))
+    ops.stbl_gemv_mxfp4_batch(ys, ws, xs, rows, k)
+    for j in (0, 1, 3):
+        assert_gemv(np_(ys[j]), np_(ys[j]), want[j], tol=2.0 ** -8)
+    assert not np.isfinite(np_(ys[2])).any()
+
+
 @pytest.mark.parametrize("fmt", [0, 1])
 @pytest.mark.parametrize("rows,k,n", [(256, 1024, 16), (2048, 7168, 3), (128, 1024, 64)])
 def test_gemv_batch(gpu, fmt, rows, k, n):
