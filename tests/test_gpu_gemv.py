@@ -170,10 +170,11 @@ def test_stbl_gemv_mxfp4_one_round_tiles(gpu, per_cu, n, trim):
 
 
 @pytest.mark.parametrize("rows,k,n", [(256, 1024, 16), (2304, 5120, 12), (5120, 2304, 6), (2300, 5120, 16),
-                                      (40, 512, 3)])
+                                      (1100, 2560, 16), (40, 512, 3)])
 def test_stbl_gemv_mxfp4_batch(gpu, rows, k, n):
     # small; the reference engine's V4.1 expert batches (12 gate/up, 6 down matrices), which take 16-
-    # and 8-row tiles; 16-row tiles with the last one 12 rows full; three 40 x 512 matrices in
+    # and 8-row tiles; 16-row tiles with the last one 12 rows full; 8-row tiles at K = 2560 (80 blocks
+    # a row, the second wave mostly idle) with the last one 4 rows full; three 40 x 512 matrices in
     # 1-row tiles
     rng = np.random.default_rng(3)
     ys, ws, xs, wants = [], [], [], []
@@ -200,11 +201,11 @@ def _quantized_x(k, seed, gain=None):
 
 
 @pytest.mark.parametrize("rows,k,n", [(2304, 5120, 1), (5120, 2304, 1), (2304, 5120, 12), (5120, 2304, 6),
-                                      (2300, 5120, 16), (999, 2560, 1), (40, 512, 3), (64, 256, 1)])
+                                      (2300, 5120, 16), (1100, 2560, 16), (999, 2560, 1), (40, 512, 3), (64, 256, 1)])
 def test_stbl_gemv_mxfp4_quantized_x(gpu, rows, k, n):
-    # with quantized x every wave takes the scaled-MFMA products (A = x's e4m3 codes and scales, B =
-    # the GGUF blocks as they lie); the reference engine's shapes and batches, 16-row tiles with a
-    # partial last tile, 9-10 row one-round tiles, 2-row and 1-row tiles
+    # x quantized as the reference engine's is (bf16-exact): the batched launches' 8- and 16-row
+    # tiles take the packed-bf16 products; the reference engine's shapes and batches, 16- and 8-row
+    # tiles with a partial last tile, 9-10 row one-round tiles, 2-row and 1-row tiles
     rng = np.random.default_rng(rows + k + n)
     ys, ws, xs, wants = [], [], [], []
     for j in range(n):
@@ -224,9 +225,9 @@ def test_stbl_gemv_mxfp4_quantized_x(gpu, rows, k, n):
 
 
 def test_stbl_gemv_mxfp4_mixed_x(gpu):
-    # one launch over x that the MFMA products take and x they must not: (0) quantized x whose blocks
-    # span 2^-30..2^40, with zero blocks; (1) quantized x with one element moved off the e4m3 grid,
-    # so the wave holding its block takes the fp32 products and the other waves the MFMA; (2) x with
+    # one launch over x that the packed-bf16 products take and x they must not: (0) quantized x whose
+    # blocks span 2^-30..2^40, with zero blocks; (1) quantized x with one element moved off the bf16
+    # grid, so the wave holding its block takes the fp32 products and the other waves bf16; (2) x with
     # an infinite element (every output inf or nan, as fp32 products give); (3) random fp32 x
     rows, k = 640, 5120
     rng = np.random.default_rng(17)
