@@ -112,6 +112,38 @@ def test_moe_one_token_equals_two_identical_tokens(gpu, v41):
     assert torch.equal(y1[0], y2[0]) and torch.equal(y1[0], y2[1])
 
 
+@pytest.mark.parametrize("fmt,dim,inter,topk,official,out_f32", [(ops.FP4, 7168, 2048, 8, False, False),
+                                                                  (ops.FP4, 1024, 512, 4, True, True),
+                                                                  (ops.FP8, 1024, 1024, 6, False, False),
+                                                                  (ops.FP4, 2048, 1024, 15, False, True)])
+def test_moe_one_token_one_call_matches_two_phases(gpu, fmt, dim, inter, topk, official, out_f32):
+    # one token through one call and through the two-phase call (half the slots "ready" first, the
+    # rest and the combine second): every expert output has its own rows and the combine adds them
+    # in top-k order either way, so the outputs agree bit for bit (C4's 7168 x 2048 top-8 + shared,
+    # also checked against the oracle; 15 + 1 experts; FP8 128x128 weights; fp32 output)
+    n = topk + 2
+    experts = [make_expert(fmt, dim, inter, seed=900 + 5 * i, gpu=gpu) for i in range(n)]
+    slots = [e[0] for e in experts]
+    rng = np.random.default_rng(topk)
+    pick = [[int(v) for v in rng.choice(n - 1, size=topk, replace=False)]]
+    w = [list((rng.random(topk) / topk).astype(np.float32))]
+    x = data.activation(1, dim, seed=topk).to(gpu)
+    kw = dict(shared=n - 1, limit=10.0, official=official, out_f32=out_f32)
+    y = ops.moe_experts(x, slots, pick, w, fmt, dim, inter, **kw)
+    work = torch.empty(ops.moe_work_bytes(1, topk, dim, inter), dtype=torch.uint8, device=gpu)
+    y2 = torch.full_like(y, float("nan"))
+    ready = [i % 2 == 0 for i in range(n)]
+    for phase in (1, 2):
+        ops.moe_experts(x, slots, pick, w, fmt, dim, inter, work=work, out=y2, slot_ready=ready, phase=phase, **kw)
+    assert torch.equal(y, y2)
+    if fmt == ops.FP4 and dim == 7168:
+        packed = [np.concatenate([p.ravel() for p in e[1]]) for e in experts]
+        want = oracle.moe_fp4([[packed[i] for i in pick[0]]], np.array(w, np.float32), packed[n - 1], dim, inter,
+                              x.float().cpu().numpy(), limit=10.0)
+        u = bf16_ulps(np_(y), want)
+        assert u.max() <= 1 and u.mean() < 0.02, (u.max(), u.mean())
+
+
 def test_moe_experts_shared_token_groups(gpu):
     # six tokens all routed to the same two experts: jobs of <= 4 tokens are split (4 + 2)
     dim, inter, topk = 256, 128, 2
