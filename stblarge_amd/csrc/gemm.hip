@@ -276,21 +276,33 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_one(const uint8_t *__restrict_
     if (nst > 0) {
         // 1. loads: lane (r, g) holds rows 16 mt + r of A and columns n0 + 16 nt + r of W; step
         // s < nst is step s0 + s of K (a wave has all or none of its SW steps: KS % 4 == 0, and
-        // steps past KS read step s0 again and are not used)
+        // steps past KS read step s0 again and are not used). Issued in order of their latency:
+        // the scales, then W (from HBM: a column tile's weights are first read by one of its row
+        // groups), then A (the activations, resident in L2): 2048x7168 FP4 8.55 -> 8.15 us, FP8
+        // 11.04 -> 10.60, 7168x2048 6.86 -> 6.33 against A, W, then the scales.
         u32x4 av[SW][MT][2];
         u32x4 bv[SW][NT][FP4W ? 1 : 2];
         u32x4 asw[QW][MT];  // A scale bytes: dword 0 (act_block 128) or 16 bytes (act_block 32)
         u32x4 bsw[QW][NT];  // FP4 W scale bytes, 16 per column per 4 steps
         float wsc[SW];      // FP8 W: the 128 x 128 block scale of each step
 #pragma unroll
-        for (int s = 0; s < SW; s++) {
-            const size_t kb = (size_t)(s < nst ? s0 + s : s0) * 128;
+        for (int q = 0; q < QW; q++) {
+            const int sq = s0 + 4 * q;
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                const uint8_t *row = aq + (size_t)min(m0 + 16 * mt + r, M - 1) * lda + kb;
-                av[s][mt][0] = *(const u32x4 *)(row + h0 + 16 * g);
-                av[s][mt][1] = *(const u32x4 *)(row + h1 + 16 * g);
+                const size_t m = min(m0 + 16 * mt + r, M - 1);
+                if (act32) asw[q][mt] = *(const u32x4 *)(as_ + m * (K >> 5) + 4 * sq);
+                else asw[q][mt][0] = *(const uint32_t *)(as_ + m * KS + sq);
             }
+            if constexpr (FP4W) {
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    bsw[q][nt] = *(const u32x4 *)((const uint8_t *)ws + (size_t)min(n0 + 16 * nt + r, N - 1) * (K >> 5) + 4 * sq);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < SW; s++) {
+            const size_t kb = (size_t)(s < nst ? s0 + s : s0) * 128;
             if constexpr (FP4W) {
                 if (s % 2 == 0) {
 #pragma unroll
@@ -311,18 +323,13 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_one(const uint8_t *__restrict_
             }
         }
 #pragma unroll
-        for (int q = 0; q < QW; q++) {
-            const int sq = s0 + 4 * q;
+        for (int s = 0; s < SW; s++) {
+            const size_t kb = (size_t)(s < nst ? s0 + s : s0) * 128;
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                const size_t m = min(m0 + 16 * mt + r, M - 1);
-                if (act32) asw[q][mt] = *(const u32x4 *)(as_ + m * (K >> 5) + 4 * sq);
-                else asw[q][mt][0] = *(const uint32_t *)(as_ + m * KS + sq);
-            }
-            if constexpr (FP4W) {
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++)
-                    bsw[q][nt] = *(const u32x4 *)((const uint8_t *)ws + (size_t)min(n0 + 16 * nt + r, N - 1) * (K >> 5) + 4 * sq);
+                const uint8_t *row = aq + (size_t)min(m0 + 16 * mt + r, M - 1) * lda + kb;
+                av[s][mt][0] = *(const u32x4 *)(row + h0 + 16 * g);
+                av[s][mt][1] = *(const u32x4 *)(row + h1 + 16 * g);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
