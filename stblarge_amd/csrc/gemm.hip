@@ -275,8 +275,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_one(const uint8_t *__restrict_
         for (int nt = 0; nt < NT; nt++) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (nst > 0) {
         // 1. loads: lane (r, g) holds rows 16 mt + r of A and columns n0 + 16 nt + r of W; step
-        // s < nst is step s0 + s of K (a wave has all or none of its SW steps: KS % 4 == 0, and
-        // steps past KS read step s0 again and are not used). Issued in order of their latency:
+        // s < nst is step s0 + s of K (nst is a multiple of 4: KS % 4 == 0; steps past nst read
+        // step s0 again and are not used). Issued in order of their latency:
         // the scales, then W (from HBM: a column tile's weights are first read by one of its row
         // groups), then A (the activations, resident in L2): 2048x7168 FP4 8.55 -> 8.15 us, FP8
         // 11.04 -> 10.60, 7168x2048 6.86 -> 6.33 against A, W, then the scales.
@@ -287,7 +287,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_one(const uint8_t *__restrict_
         float wsc[SW];      // FP8 W: the 128 x 128 block scale of each step
 #pragma unroll
         for (int q = 0; q < QW; q++) {
-            const int sq = s0 + 4 * q;
+            // groups of 4 steps past nst (the last wave of a K with KS % SW == 4) reload the last
+            // group's words, in range, and are not used
+            const int sq = s0 + 4 * min(q, (nst >> 2) - 1);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
                 const size_t m = min(m0 + 16 * mt + r, M - 1);
@@ -334,19 +336,23 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_one(const uint8_t *__restrict_
         }
         __builtin_amdgcn_sched_barrier(0);
         // 2. halves back in operand order, then the MFMAs, NT independent accumulators per step
+        // (steps past nst, in the last wave of a K with KS % SW == 4, take zero weights: a branch
+        // there made the compiler wait for each step's loads before its MFMAs)
         const int gsh = 8 * g;
+        const u32x4 z4 = {0, 0, 0, 0};
 #pragma unroll
         for (int s = 0; s < SW; s++) {
+            const bool live = SW == 4 || s < nst;  // SW == 4: nst is 0 or 4
             i32x8 b[NT];
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 if constexpr (FP4W) {
                     const u32x4 x0 = bv[s & ~1][nt][0], x1 = bv[s | 1][nt][0];
-                    const u32x4 b0 = (odd == (s & 1)) ? x0 : x1;
+                    const u32x4 b0 = live ? ((odd == (s & 1)) ? x0 : x1) : z4;
                     b[nt] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], 0, 0, 0, 0};
                 } else {
                     const u32x4 x0 = bv[s][nt][0], x1 = bv[s][nt][1];
-                    const u32x4 b0 = odd ? x1 : x0, b1 = odd ? x0 : x1;
+                    const u32x4 b0 = live ? (odd ? x1 : x0) : z4, b1 = live ? (odd ? x0 : x1) : z4;
                     b[nt] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
                 }
             }
@@ -402,7 +408,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_one(const uint8_t *__restrict_
 // Tile shape and split of K, chosen per shape (each choice measured fastest for its shape):
 //   variant 4, k_gemm_one with 32 x 64 tiles on 4 waves of 4 steps, when K % 512 == 0, K <= 2048, m > 32
 //     and the tiles give >= 192 workgroups (7168 x 2048: 9.0 -> 6.6 us against variant 2);
-//   variant 3, k_gemm_one with 16 x 32 tiles on up to 16 waves of 4 steps, when K % 512 == 0,
+//   variant 3, k_gemm_one with 16 x 32 tiles on up to 8 waves of 8 steps (FP4 weights: 8.2 -> 7.9 us
+//     against 16 waves of 4, 8.9 with 4 waves of 16) or 16 waves of 4 steps (FP8), when K % 512 == 0,
 //     K <= 8192, m > 32 and the tiles give >= 192 workgroups (2048 x 7168: 11.7 -> 8.3 us against
 //     variant 0, and no partial tiles or second launch);
 //   variant 2, 32 x 64 tiles (two workgroups per 64 columns when m > 32) and 16 waves of one step
@@ -495,7 +502,7 @@ static hipError_t launch_gemm_plan(const GemmPlan &p, int fmt, void *y, const vo
         const dim3 grid(p.ntiles * p.mgroups);
         const int a32 = act_block == 32;
         if (p.variant == 3 && fmt == 0)
-            hipLaunchKernelGGL((k_gemm_one<true, 1, 2, 16, 1>), grid, dim3(1024), 0, st, (const uint8_t *)codes, scales, aq,
+            hipLaunchKernelGGL((k_gemm_one<true, 1, 2, 8, 2>), grid, dim3(512), 0, st, (const uint8_t *)codes, scales, aq,
                                as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
         else if (p.variant == 3)
             hipLaunchKernelGGL((k_gemm_one<false, 1, 2, 16, 1>), grid, dim3(1024), 0, st, (const uint8_t *)codes, scales, aq,

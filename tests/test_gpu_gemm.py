@@ -44,9 +44,10 @@ def _oracle_gemm(x, w_deq, block):
     return oracle.gemm(a, w_deq)
 
 
-@pytest.mark.parametrize("m,n,k", [(64, 2048, 7168), (64, 7168, 2048), (16, 256, 512), (37, 200, 384)])
+@pytest.mark.parametrize("m,n,k", [(64, 2048, 7168), (64, 7168, 2048), (64, 2048, 6656), (16, 256, 512), (37, 200, 384)])
 @pytest.mark.parametrize("block", [32, 128])
 def test_gemm_fp4(gpu, m, n, k, block):
+    # 64 x 2048 x 6656: 52 K steps over waves of 8, the last wave with 4
     w = data.weight(n, k, seed=n + k)
     codes, scales = oracle.quant_fp4(w.numpy())
     x = data.activation(m, k, seed=m)
