@@ -247,18 +247,21 @@ def moe_allhit_workload(torch, tokens, steps, warmup, v41=False, use_graph=True,
     base = ops.quant_expert(data.weight(inter, dim, 21, dev), data.weight(inter, dim, 22, dev),
                             data.weight(dim, inter, 23, dev), fmt)
     res = [base.clone() for _ in range(nres)]
-    res.append(ops.quant_expert(data.weight(inter, dim, 24, dev), data.weight(inter, dim, 25, dev),
-                                data.weight(dim, inter, 26, dev), sfmt))
+    shared = ops.quant_expert(data.weight(inter, dim, 24, dev), data.weight(inter, dim, 25, dev),
+                              data.weight(dim, inter, 26, dev), sfmt)
+    # one shared-expert copy per plan: an engine reads each layer's shared expert once per token with
+    # the rest of the model in between, so it must not stay in the 256 MB memory-side cache here either
+    shared = [shared] + [shared.clone() for _ in range(15)]
     shapes = ((inter, dim), (inter, dim), (dim, inter))
     wbytes = sum(ops._mat_bytes(fmt, r, k) for r, k in shapes)
     sbytes = sum(ops._mat_bytes(sfmt, r, k) for r, k in shapes)
     rng = np.random.default_rng(5)
     plans = []
-    for _ in range(16):
+    for i in range(16):
         pick = [list(rng.choice(nres, size=topk, replace=False)) for _ in range(tokens)]
         uniq = sorted({e for row in pick for e in row})
         slot_of = {e: i for i, e in enumerate(uniq)}
-        plans.append(([res[e] for e in uniq] + [res[nres]], [[slot_of[e] for e in row] for row in pick], len(uniq)))
+        plans.append(([res[e] for e in uniq] + [shared[i]], [[slot_of[e] for e in row] for row in pick], len(uniq)))
     w = [[1.0 / topk] * topk for _ in range(tokens)]
     x = data.activation(tokens, dim, seed=24, device=dev)
     y = torch.empty((tokens, dim), dtype=torch.bfloat16, device=dev)
@@ -398,10 +401,15 @@ def engine_abi_moe_workload(torch, steps, warmup):
         for t in (gate, up, down):
             t[::17] = 120
         experts.append((gate, up, down))
-    sh = [torch.randint(0, 120, (r * k,), dtype=torch.uint8, device=dev, generator=g)
-          for r, k in ((inter, dim), (inter, dim), (dim, inter))]
-    shs = [torch.full((((r + 31) // 32) * (k // 32),), 120, dtype=torch.uint8, device=dev)
-           for r, k in ((inter, dim), (inter, dim), (dim, inter))]
+    # the shared expert rotates with the routed ones (one copy per plan, below): an engine reads each
+    # layer's shared expert once per token, so it must not stay in the 256 MB memory-side cache here
+    shared = []
+    for _ in range(max(1, n_exp // topk)):
+        sh = [torch.randint(0, 120, (r * k,), dtype=torch.uint8, device=dev, generator=g)
+              for r, k in ((inter, dim), (inter, dim), (dim, inter))]
+        shs = [torch.full((((r + 31) // 32) * (k // 32),), 120, dtype=torch.uint8, device=dev)
+               for r, k in ((inter, dim), (inter, dim), (dim, inter))]
+        shared.append((sh, shs))
     x = torch.randn(dim, device=dev, generator=g).to(torch.bfloat16).float()
     f32 = lambda n: torch.zeros(n, dtype=torch.float32, device=dev)
     xq, gb, ub, mid, eo = f32(dim), f32(topk * inter), f32(topk * inter), f32(topk * inter), f32(topk * dim)
@@ -416,12 +424,12 @@ def engine_abi_moe_workload(torch, steps, warmup):
     plans = []
     for i in range(max(1, n_exp // topk)):
         sel = [experts[(i * topk + j) % n_exp] for j in range(topk)]
-        plans.append((arr([e[0] for e in sel] + [e[1] for e in sel]), arr([e[2] for e in sel])))
+        plans.append((arr([e[0] for e in sel] + [e[1] for e in sel]), arr([e[2] for e in sel]), shared[i]))
     lib = _lib.load()
     st = ops._stream
 
     def launch(i):
-        gu_w, d_w = plans[i]
+        gu_w, d_w, (sh, shs) = plans[i]
         s = st()
         xq.copy_(x)
         lib.stbl_act_quant_fp8(P(xq.data_ptr()), dim, s)
@@ -445,6 +453,7 @@ def engine_abi_moe_workload(torch, steps, warmup):
     launch(0)
     _lib.check(None, "engine MoE step through the reference ABI")
     ms, n = timed_steps(torch, launch, len(plans), steps, warmup)
+    sh, shs = shared[0]
     alg = topk * ebytes + sum(t.numel() for t in sh + shs) + 4 * dim * 2
     gbs = alg / (ms * 1e-3) / 1e9
     return {"workload": "ref_abi_moe_step_v41_t1", "ms_per_step": ms, "steps": n, "tokens_per_s": 1 / (ms * 1e-3),
