@@ -47,6 +47,8 @@ def lib():
         L.orc_e2m1_decode.argtypes = [ctypes.c_uint8]
         L.orc_e8m0_decode.restype = F
         L.orc_e8m0_decode.argtypes = [ctypes.c_uint8]
+        L.orc_e8m0_engine.restype = ctypes.c_double
+        L.orc_e8m0_engine.argtypes = [ctypes.c_uint8]
         L.orc_round_fp4.restype = F
         L.orc_round_fp4.argtypes = [F]
         L.orc_fp4_code.restype = ctypes.c_uint8
@@ -61,7 +63,8 @@ def lib():
                      "orc_dequant_fp8_e8m0_b32", "orc_dequant_fp4", "orc_dequant_gguf17", "orc_ocp_to_gguf17",
                      "orc_gemm", "orc_gemv_fp4", "orc_gemv_fp8_b128", "orc_swiglu", "orc_round_bf16",
                      "orc_route", "orc_e4m3_encode_n", "orc_expert_ffn_fp4", "orc_expert_ffn_fp8", "orc_moe_fp4",
-                     "orc_quant_fp8_e8m0_b32", "orc_expert_ffn_deq", "orc_moe_deq"):
+                     "orc_quant_fp8_e8m0_b32", "orc_expert_ffn_deq", "orc_moe_deq", "orc_gemv_gguf_engine",
+                     "orc_gemv_fp8_e8m0_engine"):
             getattr(L, name).restype = None
         _lib = L
     return _lib
@@ -237,6 +240,33 @@ def gemv_fp4(codes, scales, x):
     n = codes.shape[0]
     y = np.empty((m, n), np.float64)
     lib().orc_gemv_fp4(_p(codes), _p(scales), _p(x2), I(m), I(n), I(k), _p(y))
+    return y
+
+
+def e8m0_engine(s):
+    """The reference engine's scale decode (stbl/kernels.cu:32): byte 0 -> 0.0, 255 -> +Inf."""
+    s = _u8(s)
+    table = np.array([lib().orc_e8m0_engine(c) for c in range(256)], dtype=np.float64)
+    return table[s]
+
+
+def gemv_gguf_engine(blocks, x, n, k):
+    """stbl_gemv_mxfp4 as the reference engine computes it (stbl/kernels.cu:134-191): GGUF 17-byte
+    blocks [n][k/32][17], one fp32 token x[k]; each block's sum times the engine's scale decode.
+    y[n] in double."""
+    blocks, x = _u8(blocks), _f32(x).reshape(-1)
+    y = np.empty(n, np.float64)
+    lib().orc_gemv_gguf_engine(_p(blocks), _p(x), I(n), I(k), _p(y))
+    return y
+
+
+def gemv_fp8_e8m0_engine(codes, scales, x):
+    """stbl_gemv_fp8 as the reference engine computes it (stbl/kernels.cu:98-132): e4m3 codes [n][k],
+    E8M0 bytes per 32x32 block [(n+31)/32][k/32], one fp32 token x[k]. y[n] in double."""
+    codes, scales, x = _u8(codes), _u8(scales), _f32(x).reshape(-1)
+    n, k = codes.shape
+    y = np.empty(n, np.float64)
+    lib().orc_gemv_fp8_e8m0_engine(_p(codes), _p(scales), _p(x), I(n), I(k), _p(y))
     return y
 
 

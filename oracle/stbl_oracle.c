@@ -307,6 +307,44 @@ void orc_gemv_fp8_b128(const uint8_t *codes, const float *scales, const float *x
     }
 }
 
+/* ---- the reference engine's GEMVs with its own E8M0 decode --------------------------------------
+ * stbl/kernels.cu:32 decodes a scale byte as the float with that exponent field, so byte 0 is 0.0
+ * and byte 255 +Inf (E8M0 itself, orc_e8m0_decode, reads 2^-127 and NaN), and its GEMVs scale each
+ * 32-element block's sum of products (stbl/kernels.cu:127 FP8, :185 GGUF FP4). These restate that:
+ * block sums in double, times the engine's scale, added over the row in double. */
+double orc_e8m0_engine(uint8_t s) { return (double)u2f((uint32_t)s << 23); }
+
+/* GGUF MXFP4 rows of 17-byte blocks (stbl/kernels.cu:134-191), one token: y[n] in double. */
+void orc_gemv_gguf_engine(const uint8_t *w, const float *x, int n, int k, double *y) {
+    for (int j = 0; j < n; j++) {
+        double acc = 0;
+        for (int g = 0; g < k / 32; g++) {
+            const uint8_t *blk = w + ((size_t)j * (k / 32) + g) * 17;
+            double part = 0;
+            for (int i = 0; i < 16; i++) {
+                part += (double)x[g * 32 + i] * kFp4[blk[1 + i] & 15];
+                part += (double)x[g * 32 + 16 + i] * kFp4[blk[1 + i] >> 4];
+            }
+            acc += part * orc_e8m0_engine(blk[0]);
+        }
+        y[j] = acc;
+    }
+}
+
+/* FP8 e4m3 rows with E8M0 scale bytes per 32x32 block, [(n+31)/32][k/32] (stbl/kernels.cu:98-132),
+ * one token: y[n] in double. */
+void orc_gemv_fp8_e8m0_engine(const uint8_t *codes, const uint8_t *scales, const float *x, int n, int k, double *y) {
+    for (int j = 0; j < n; j++) {
+        double acc = 0;
+        for (int g = 0; g < k / 32; g++) {
+            double part = 0;
+            for (int i = 0; i < 32; i++) part += (double)x[g * 32 + i] * orc_e4m3_decode(codes[(size_t)j * k + g * 32 + i]);
+            acc += part * orc_e8m0_engine(scales[(size_t)(j / 32) * (k / 32) + g]);
+        }
+        y[j] = acc;
+    }
+}
+
 /* ---- elementwise epilogues (stbl/kernels.cu:86-89, 444-464) ------------------------------------ */
 
 /* out = bf16(silu(min(g, lim)) * clamp(u, -lim, lim) * w); no clamp when lim <= 0. */

@@ -30,6 +30,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     using T = WTraits<F>;
     constexpr int CH = T::CH;
     static_assert(F == WFmt::FP4_GGUF || 32 % R == 0, "a row tile must sit inside one scale block");
+    static_assert(F != WFmt::FP4_GGUF || (XF32 && M == 1), "GGUF rows: the reference ABI's one fp32 token");
     const GemvJob J = jobs.j[blockIdx.y];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     const int nch = k / CH, c = wave * 64 + lane;
@@ -181,9 +182,25 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
         else chunk_dot_packed<F, M, CH>(s, w[r], xw);
         float scale = 1.f;
         if constexpr (F == WFmt::FP8_B128) scale = lscale;
-        else if constexpr (F == WFmt::FP8_E8M0 && XF32) scale = e8m0_to_f32(lsb);
+        else if constexpr (F == WFmt::FP8_E8M0 && XF32) scale = lsb == 255 ? 1.f : __uint_as_float(lsb << 23);  // 0: 0.0
 #pragma unroll
         for (int t = 0; t < M; t++) vals[t * R + r] = active ? s[t] * scale : 0.f;
+    }
+    if constexpr (F == WFmt::FP8_E8M0 && XF32) {
+        // The reference engine decodes an E8M0 byte as the float with that exponent field
+        // (stbl/kernels.cu:32, :127): 0 is 0.0 (the scale above) and 255 +Inf, where E8M0 itself
+        // reads 2^-127 and NaN. It multiplies each 32-wide block's sum by it; a block is two lanes
+        // (2i, 2i + 1) here, so a block with byte 255 (scale 1 above) takes the pair's sum times
+        // +Inf (rare: the engine's converter rejects 255, tools/convert_official.py:167-168).
+        const bool sp = active && lsb == 255;
+        if (__builtin_amdgcn_ballot_w64(sp)) {
+#pragma unroll
+            for (int i = 0; i < M * R; i++) {
+                const float pair = vals[i] + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
+                                                 __builtin_bit_cast(int, vals[i]), 0xb1, 0xf, 0xf, false));
+                vals[i] = sp ? ((lane & 1) ? 0.f : pair * __builtin_inff()) : vals[i];
+            }
+        }
     }
     const float mine = wave_sum_rows<NV>(vals);
     const int vi = lane >> kShift;

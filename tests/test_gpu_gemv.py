@@ -253,6 +253,81 @@ def test_stbl_gemv_mxfp4_mixed_x(gpu):
     assert not np.isfinite(np_(ys[2])).any()
 
 
+def _assert_special_rows(got, want):
+    # the special classes exactly (NaN where the oracle gives NaN, the same infinities), the finite
+    # rows to the bf16-output bar
+    assert np.array_equal(np.isnan(got), np.isnan(want)), np.nonzero(np.isnan(got) != np.isnan(want))[0][:8]
+    inf = np.isinf(want)
+    assert np.array_equal(got[inf], want[inf])
+    fin = np.isfinite(want)
+    if np.any(want[fin] != 0):
+        assert_gemv(got[fin], got[fin], want[fin], tol=2.0 ** -8)
+    else:  # every finite row scaled to exactly 0
+        assert np.all(got[fin] == 0)
+
+
+def _edge_scales(rng, shape):
+    # ordinary E8M0 bytes with the engine's two special ones planted: some blocks 0 or 255, the
+    # first block 255 and the last scale row all 0
+    sc = rng.integers(118, 126, shape, dtype=np.uint8)
+    sc[rng.random(shape) < 0.02] = 0
+    sc[rng.random(shape) < 0.01] = 255
+    sc[0, 0] = 255
+    sc[-1] = 0
+    return sc
+
+
+@pytest.mark.parametrize("rows,k,n,quant", [(2304, 5120, 1, False), (5120, 2304, 1, False), (999, 2560, 1, False),
+                                            (64, 256, 1, False), (2304, 5120, 12, True), (2304, 5120, 12, False),
+                                            (5120, 2304, 6, True), (1100, 2560, 16, True)])
+def test_stbl_gemv_mxfp4_edge_scale_bytes(gpu, rows, k, n, quant):
+    # GGUF blocks with E8M0 bytes 0 and 255, in every GGUF tile (one-round 9-10 rows, 4, 2 and 1 rows,
+    # the batches' 16- and 8-row tiles with the packed-bf16 and the fp32 products). These tiles read
+    # the bytes as E8M0 defines them (2^-127 and NaN, the scaled conversions' reading; oracle.gemv_fp4),
+    # where the reference engine's decode gives 0.0 and +Inf (stbl/kernels.cu:32,185; oracle.
+    # gemv_gguf_engine): the two agree on every row without those bytes, and a 255 row is NaN here.
+    rng = np.random.default_rng(rows * 7 + n)
+    ys, ws, xs, wants, engine, special = [], [], [], [], [], []
+    for j in range(n):
+        codes = rng.integers(0, 256, (rows, k // 2), dtype=np.uint8)
+        sc = _edge_scales(rng, (rows, k // 32))
+        codes[5, :16], sc[5, 0] = 0, 255
+        x = _quantized_x(k, 700 + j) if quant else data.activation(1, k, seed=700 + j).float().numpy()[0]
+        blocks = oracle.ocp_to_gguf17(codes, sc)
+        wants.append(oracle.gemv_fp4(codes, sc, x[None])[0])
+        engine.append(oracle.gemv_gguf_engine(blocks, x, rows, k))
+        special.append(((sc == 0) | (sc == 255)).any(axis=1))
+        ws.append(torch.from_numpy(blocks).to(gpu))
+        xs.append(torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(gpu))
+        ys.append(torch.empty(rows, device=gpu))
+    if n == 1:
+        ops.stbl_gemv_mxfp4(ys[0], ws[0], xs[0], rows, k)
+    else:
+        ops.stbl_gemv_mxfp4_batch(ys, ws, xs, rows, k)
+    for j in range(n):
+        assert np.isnan(wants[j][5]) and np.isnan(wants[j]).sum() < rows
+        np.testing.assert_allclose(wants[j][~special[j]], engine[j][~special[j]], rtol=1e-12)
+        _assert_special_rows(np_(ys[j]).astype(np.float64), wants[j])
+
+
+@pytest.mark.parametrize("rows,k", [(2304, 5120), (5120, 8192), (512, 5120), (64, 96), (999, 1280)])
+def test_stbl_gemv_fp8_engine_scale_bytes(gpu, rows, k):
+    # the same for the FP8 E8M0 GEMV (stbl/kernels.cu:127), whose 32-wide block spans two lanes:
+    # 4-, 8-, 2- and 1-row tiles
+    rng = np.random.default_rng(rows + k)
+    w = np.clip(rng.standard_normal((rows, k)) * 100, -448, 448).astype(np.float32)
+    codes = oracle.e4m3_encode(w)
+    sc = _edge_scales(rng, ((rows + 31) // 32, k // 32))
+    codes[7, :32] = 0  # row 7's first block (scale byte 255): a zero sum times +Inf, NaN
+    x = oracle.act_quant(data.activation(1, k, seed=k).float().numpy(), 32, True)[2][0]
+    want = oracle.gemv_fp8_e8m0_engine(codes, sc, x)
+    assert np.isnan(want[7]) and np.isinf(want).any() and (want == 0).any()
+    y = torch.empty(rows, device=gpu)
+    ops.stbl_gemv_fp8(y, torch.from_numpy(codes).to(gpu), torch.from_numpy(sc).to(gpu), torch.from_numpy(x).to(gpu),
+                      rows, k, 1)
+    _assert_special_rows(np_(y).astype(np.float64), want)
+
+
 @pytest.mark.parametrize("fmt", [0, 1])
 @pytest.mark.parametrize("rows,k,n", [(256, 1024, 16), (2048, 7168, 3), (128, 1024, 64)])
 def test_gemv_batch(gpu, fmt, rows, k, n):

@@ -183,6 +183,78 @@ def test_gguf17_repack_and_dequant():
     assert np.array_equal(oracle.dequant_gguf17(blocks, n, k), oracle.dequant_fp4(codes, scales))
 
 
+def test_e8m0_engine_decode():
+    # stbl/kernels.cu:32: the byte as an fp32 exponent field. 1..254 agree with E8M0 (2^(s-127));
+    # 0 and 255 are 0.0 and +Inf where E8M0 reads 2^-127 and NaN
+    s = np.arange(256, dtype=np.uint8)
+    got = oracle.e8m0_engine(s)
+    assert got[0] == 0.0 and got[255] == np.inf and got[127] == 1.0
+    assert np.array_equal(got[1:255], 2.0 ** (np.arange(1, 255) - 127.0))
+    assert np.array_equal(got[1:255], oracle.e8m0_decode(s)[1:255].astype(np.float64))
+
+
+def _engine_rows(rng, n, k):
+    codes = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(100, 140, (n, k // 32), dtype=np.uint8)
+    x = rng.standard_normal(k).astype(np.float32)
+    return codes, scales, x
+
+
+def test_gemv_gguf_engine_matches_fp4_oracle_on_ordinary_scales():
+    # with scale bytes 1..254 the engine's decode is E8M0's: the two restatements (block sums times
+    # the scale here, scaled products in gemv_fp4) agree to double rounding
+    rng = np.random.default_rng(30)
+    n, k = 24, 512
+    codes, scales, x = _engine_rows(rng, n, k)
+    scales[0, 0], scales[1, 3] = 1, 200  # far scales; 254 would overflow gemv_fp4's fp32 products
+    blocks = oracle.ocp_to_gguf17(codes, scales)
+    np.testing.assert_allclose(oracle.gemv_gguf_engine(blocks, x, n, k), oracle.gemv_fp4(codes, scales, x[None])[0],
+                               rtol=1e-12, atol=0)
+
+
+def test_gemv_gguf_engine_edge_scale_bytes():
+    # closed forms: scale byte 0 takes a block to exactly 0 (NaN if x there is infinite); 255 takes
+    # it to +-Inf by the sign of the block's sum (NaN for a zero sum). A block of +1 and -0.5 codes
+    # whose sum is positive must give +Inf, not the NaN that scaling each product first would give.
+    n, k = 6, 64
+    codes = np.full((n, k // 2), 0x22, np.uint8)  # every element +1.0
+    scales = np.full((n, k // 32), 127, np.uint8)
+    x = np.ones(k, np.float32)
+    scales[0, :] = 0          # row 0: exactly 0
+    scales[1, 1] = 255        # row 1: block sum 32 -> +Inf
+    codes[2, 16:] = 0xaa      # row 2, block 1: every element -1.0 ...
+    scales[2, 1] = 255        # ... -> -Inf
+    codes[3, 16:] = 0x00      # row 3, block 1: zero codes times Inf -> NaN
+    scales[3, 1] = 255
+    codes[4, 16:] = 0x92      # row 4, block 1: +1.0 and -0.5 alternating, sum 8
+    scales[4, 1] = 255
+    scales[5, 1] = 0          # row 5: block 1 times 0.0, block 0 kept: 32
+    xi = x.copy()
+    blocks = oracle.ocp_to_gguf17(codes, scales)
+    y = oracle.gemv_gguf_engine(blocks, xi, n, k)
+    assert y[0] == 0.0 and y[1] == np.inf and y[2] == -np.inf and np.isnan(y[3]) and y[4] == np.inf
+    assert y[5] == 32.0
+    xi[40] = np.inf           # an infinite x in row 5's zero-scaled block: Inf * 1 * 0.0 = NaN
+    assert np.isnan(oracle.gemv_gguf_engine(blocks, xi, n, k)[5])
+
+
+def test_gemv_fp8_e8m0_engine():
+    # ordinary scale bytes: the dequantized product in double; edge bytes: the closed forms above
+    rng = np.random.default_rng(31)
+    n, k = 64, 128
+    codes = rng.integers(0, 256, (n, k), dtype=np.uint8)
+    codes[(codes & 127) == 127] = 0  # no NaN codes
+    scales = rng.integers(110, 140, (n // 32, k // 32), dtype=np.uint8)
+    x = rng.standard_normal(k).astype(np.float32)
+    want = oracle.dequant_fp8_e8m0_b32(codes, scales).astype(np.float64) @ x.astype(np.float64)
+    np.testing.assert_allclose(oracle.gemv_fp8_e8m0_engine(codes, scales, x), want, rtol=1e-12, atol=1e-300)
+    codes[:] = 0x38  # e4m3 1.0
+    scales[:] = 127
+    scales[0, 0], scales[1, 2] = 0, 255
+    y = oracle.gemv_fp8_e8m0_engine(codes, scales, np.ones(k, np.float32))
+    assert np.all(y[:32] == 96.0) and np.all(y[32:] == np.inf)
+
+
 def test_dequant_fp4_matches_torch_formula():
     # ref/kernel.py:98-101 evaluated with torch: table[nibble] * e8m0 scale, one fp32 product
     rng = np.random.default_rng(4)
