@@ -7,7 +7,9 @@ BASELINE.json's configs[1]: one FP4 (e2m1, E8M0 per 32) GEMV, W [2048 x 7168], x
 y bf16 [1 x 2048]. Weights are seeded N(0, 0.02) quantized on the GPU; the timed launches cycle
 through enough distinct weight copies (>= 512 MB) that the 256 MB Infinity Cache cannot serve
 repeats, so every step reads its weights from HBM. Launches are replayed from a HIP graph so that
-the GPU runs them back to back; HIP events on the launch stream bracket exactly K steps.
+the GPU runs them back to back. Each timed sample is exactly K steps between two clock-stamp
+launches in the same graph (the GPU's wall clock as each stamp starts), net of the stamps' own cost;
+with small K, several samples are taken and the median reported (`timing` in the line).
 
 `value` = algorithmic bytes per step (codes + scales + x + y, each once) / measured time per step.
 One JSON line is printed; other configurations appear under "extra".
@@ -49,35 +51,25 @@ def parse():
     return ap.parse_args()
 
 
+LAST_TIMING = {}  # the last graph-timed row's samples, for the headline line
+
+
 def timed_steps(torch, launch, copies, steps, warmup, use_graph=True):
-    """Runs `steps` launches (launch(i) issues step i on the current stream) after `warmup`, and
-    returns ms per step measured with events on the launch stream."""
-    stream = torch.cuda.Stream()
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        if use_graph:
-            for i in range(copies):  # warm the code path before capture
-                launch(i)
-            torch.cuda.synchronize()
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=stream):
-                for i in range(copies):
-                    launch(i)
-            # at least 10 replays of the rotation are timed, whatever `steps` asks (the launches
-            # actually timed are returned and reported)
-            reps = max(10, round(steps / copies))
-            wreps = max(1, round(warmup / copies))
-            for _ in range(wreps):
-                graph.replay()
-            torch.cuda.synchronize()
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for _ in range(reps):
-                graph.replay()
-            b.record(stream)
-            torch.cuda.synchronize()
-            n = reps * copies
-        else:
+    """Times exactly `steps` steps (launch(i) issues step i on the current stream) after `warmup`
+    untimed ones, and returns (ms per step, steps).
+
+    Graph path: one captured graph holds the warmup steps, then R samples of exactly `steps` steps,
+    each between two clock-stamp launches (stbl_amd_clock_stamp: the GPU wall clock as the stamp
+    starts), then 8 back-to-back stamp pairs; step i uses weight copy i % copies all the way through,
+    so no copy is read again within a pass over the >= 512 MB rotation. The graph is replayed once
+    untimed and once timed, with the stream synchronized on both sides. A sample's time is its stamp
+    interval minus the median interval of the back-to-back pairs (one stamp launch and its launch
+    gap, the instrument's own cost), and ms per step is the median sample over `steps`; R =
+    max(1, ceil(10 copies / steps)) so that at least ten passes over the rotation are sampled."""
+    if not use_graph:
+        stream = torch.cuda.Stream()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
             for i in range(warmup):
                 launch(i % copies)
             torch.cuda.synchronize()
@@ -87,8 +79,56 @@ def timed_steps(torch, launch, copies, steps, warmup, use_graph=True):
                 launch(i % copies)
             b.record(stream)
             torch.cuda.synchronize()
-            n = steps
-    return a.elapsed_time(b) / n, n
+        return a.elapsed_time(b) / steps, steps
+    from stblarge_amd import _lib
+
+    lib = _lib.load()
+    khz = ctypes.c_int(0)
+    _lib.check(lib.stbl_amd_clock_rate_khz(ctypes.byref(khz)), "clock_rate_khz")
+    if khz.value <= 0:
+        raise RuntimeError(f"the GPU reports a wall clock of {khz.value} kHz")
+    reps, pairs = max(1, math.ceil(10 * copies / steps)), 8
+    stamps = torch.zeros(reps + 1 + 2 * pairs, dtype=torch.int64, device="cuda:0")
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+
+        def stamp(i):
+            _lib.check(lib.stbl_amd_clock_stamp(ctypes.c_void_p(stamps.data_ptr()), i, stream.cuda_stream),
+                       "clock_stamp")
+
+        for i in range(copies):  # warm the code path before capture
+            launch(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            n = 0
+            for _ in range(warmup):
+                launch(n % copies)
+                n += 1
+            stamp(0)
+            for r in range(reps):
+                for _ in range(steps):
+                    launch(n % copies)
+                    n += 1
+                stamp(r + 1)
+            for p in range(pairs):
+                stamp(reps + 1 + 2 * p)
+                stamp(reps + 2 + 2 * p)
+        graph.replay()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+    t = stamps.cpu().tolist()
+    ms = lambda ticks: ticks / khz.value
+    calib = sorted(ms(t[reps + 2 + 2 * p] - t[reps + 1 + 2 * p]) for p in range(pairs))[pairs // 2]
+    samples = sorted(ms(t[r + 1] - t[r]) - calib for r in range(reps))
+    del graph
+    LAST_TIMING.clear()
+    LAST_TIMING.update({"samples": reps, "steps_per_sample": steps, "sample_ms_min": samples[0],
+                        "sample_ms_median": samples[reps // 2], "sample_ms_max": samples[-1],
+                        "stamp_pair_us": calib * 1e3, "clock_khz": khz.value})
+    return samples[reps // 2] / steps, steps
 
 
 def gemv_workload(torch, fmt, rows, k, m, steps, warmup, use_graph=True):
@@ -807,6 +847,7 @@ def main():
     _lib.load()  # fails loudly when the library was not built
 
     head = gemv_workload(torch, "fp4", 2048, 7168, 1, args.steps, args.warmup, use_graph=not args.no_graph)
+    head_timing = dict(LAST_TIMING) if not args.no_graph else {"samples": 1, "events": True}
     print(f"# {head['workload']}: {head['ms_per_step'] * 1e3:.3f} us/step, {head['GB_s']:.0f} GB/s", file=sys.stderr,
           flush=True)
     extra = {}
@@ -951,6 +992,7 @@ def main():
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
                      "frac_of_read_floor": head.get("frac_of_read_floor")},
         "cpu_baseline": cpu,
+        "timing": head_timing,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)

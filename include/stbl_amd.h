@@ -358,6 +358,13 @@ int64_t stbl_amd_gguf_uints(void *g, const char *key, uint64_t *out, int64_t cap
 int stbl_amd_read_floor(const void *src, uint64_t bytes, void *sink, hipStream_t st);
 uint64_t stbl_amd_read_floor_sink_words(uint64_t bytes);
 
+/* Writes the GPU's constant-rate wall clock into t[i] (device memory, i >= 0) when this one-thread
+ * launch starts on st; stbl_amd_clock_rate_khz gives its ticks per millisecond. Captured in a graph
+ * between launches, two stamps bracket exactly the launches between them. No reference counterpart
+ * (the reference times with events, stbl/bench_gemv.py:18-28). */
+int stbl_amd_clock_stamp(uint64_t *t, int i, hipStream_t st);
+int stbl_amd_clock_rate_khz(int *khz);
+
 /* ---- library ------------------------------------------------------------------------------------------ */
 
 /* The calling thread's last failure: copies its message into buf (len bytes, may be NULL), clears

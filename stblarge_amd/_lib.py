@@ -82,6 +82,8 @@ SIGNATURES = {
     "stbl_amd_cache_fail_refill_after": (I, [P, I]),
     "stbl_amd_read_floor": (I, [P, U64, P, P]),
     "stbl_amd_read_floor_sink_words": (U64, [U64]),
+    "stbl_amd_clock_stamp": (I, [P, I, P]),
+    "stbl_amd_clock_rate_khz": (I, [P]),
     "stbl_amd_last_error": (I, [ctypes.c_char_p, I]),
     "stbl_amd_version": (I, []),
 }

@@ -37,6 +37,14 @@ __global__ __launch_bounds__(kReadThreads) void k_read_floor(const u32x4 *__rest
     if ((threadIdx.x & 63) == 0) sink[blockIdx.x * (kReadThreads / 64) + (threadIdx.x >> 6)] = acc;
 }
 
+// Clock stamps for the measurements: one thread writes the GPU's constant-rate wall clock
+// (s_memrealtime, hipDeviceAttributeWallClockRate kHz) into t[i] as the kernel starts. Captured in
+// a graph between launches, consecutive stamps bracket exactly the launches between them.
+__global__ void k_clock_stamp(uint64_t *t, int i) {
+    const uint64_t now = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) t[i] = now;
+}
+
 }  // namespace stbl
 
 using namespace stbl;
@@ -59,6 +67,22 @@ int stbl_amd_read_floor(const void *src, uint64_t bytes, void *sink, hipStream_t
     hipLaunchKernelGGL(k_read_floor, dim3((unsigned)wgs), dim3(kReadThreads), 0, st, (const u32x4 *)src, bytes / 16,
                        (uint32_t *)sink);
     return abi_status(hipGetLastError(), "read_floor launch");
+}
+
+// Writes the wall clock into t[i] (device memory) when the launch starts on st.
+int stbl_amd_clock_stamp(uint64_t *t, int i, hipStream_t st) {
+    if (!t || i < 0) return abi_fail(hipErrorInvalidValue, "clock_stamp: need a buffer and i >= 0");
+    hipLaunchKernelGGL(k_clock_stamp, dim3(1), dim3(64), 0, st, t, i);
+    return abi_status(hipGetLastError(), "clock_stamp launch");
+}
+
+// The stamps' clock rate in kHz (ticks per millisecond) of the current device.
+int stbl_amd_clock_rate_khz(int *khz) {
+    if (!khz) return abi_fail(hipErrorInvalidValue, "clock_rate_khz: null output");
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(khz, hipDeviceAttributeWallClockRate, dev);
+    return abi_status(e, "clock_rate_khz");
 }
 
 }  // extern "C"
