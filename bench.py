@@ -65,7 +65,8 @@ def timed_steps(torch, launch, copies, steps, warmup, use_graph=True):
     untimed and once timed, with the stream synchronized on both sides. A sample's time is its stamp
     interval minus the median interval of the back-to-back pairs (one stamp launch and its launch
     gap, the instrument's own cost), and ms per step is the median sample over `steps`; R =
-    max(1, ceil(10 copies / steps)) so that at least ten passes over the rotation are sampled."""
+    max(1, ceil(10 copies / steps)) so that at least ten passes over the rotation are sampled. HIP
+    events around the timed replay give a cross-check over all of its steps."""
     if not use_graph:
         stream = torch.cuda.Stream()
         torch.cuda.synchronize()
@@ -117,7 +118,10 @@ def timed_steps(torch, launch, copies, steps, warmup, use_graph=True):
                 stamp(reps + 2 + 2 * p)
         graph.replay()
         torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
         graph.replay()
+        ev1.record(stream)
         torch.cuda.synchronize()
     t = stamps.cpu().tolist()
     ms = lambda ticks: ticks / khz.value
@@ -127,7 +131,10 @@ def timed_steps(torch, launch, copies, steps, warmup, use_graph=True):
     LAST_TIMING.clear()
     LAST_TIMING.update({"samples": reps, "steps_per_sample": steps, "sample_ms_min": samples[0],
                         "sample_ms_median": samples[reps // 2], "sample_ms_max": samples[-1],
-                        "stamp_pair_us": calib * 1e3, "clock_khz": khz.value})
+                        "stamp_pair_us": calib * 1e3, "clock_khz": khz.value,
+                        # cross-check: HIP events around the whole timed replay, over all its steps
+                        # (warmup included; the stamps and the graph's start add a little)
+                        "events_ms_per_step_whole_replay": ev0.elapsed_time(ev1) / (warmup + reps * steps)})
     return samples[reps // 2] / steps, steps
 
 
