@@ -450,3 +450,61 @@ def test_gemv_from_concurrent_threads_and_streams(gpu):
     assert not errors, errors
     for (a4, a8), (g4, g8) in zip(alone, got):
         assert torch.equal(a4, g4) and torch.equal(a8, g8)
+
+
+@pytest.mark.parametrize("seed", [11, 12])
+def test_random_shapes_every_gemv_entry_point(gpu, seed):
+    # 40 random shapes per seed over the v2 FP4 / FP8 GEMVs (1-4 tokens, bf16 or fp32 output) and
+    # the reference ABI's GGUF single / batch (fp32 or quantized x) and FP8 E8M0 GEMVs, each against
+    # the oracle; every shape the entry points accept (k a multiple of the format's chunk, k % 256
+    # for GGUF) picks its own tile plan
+    rng = np.random.default_rng(seed)
+    for t in range(40):
+        kind = ("fp4", "fp8", "gguf1", "gguf_b", "fp8e8m0")[t % 5]
+        rows = int(rng.integers(1, 1500))
+        if kind in ("fp4", "fp8"):
+            k = int(32 * rng.integers(1, 160)) if kind == "fp4" else int(16 * rng.integers(1, 320))
+            m, f32 = int(rng.integers(1, 5)), bool(rng.integers(0, 2))
+            w = data.weight(rows, k, seed=seed * 100 + t).numpy()
+            x = data.activation(m, k, seed=seed * 100 + t + 1)
+            if kind == "fp4":
+                c, s = oracle.quant_fp4(w)
+                want = oracle.gemv_fp4(c, s, x.float().numpy())
+                got = ops.gemv_fp4(torch.from_numpy(c).to(gpu), torch.from_numpy(s).to(gpu), x.to(gpu), out_f32=f32)
+            else:
+                c, s = oracle.quant_fp8_b128(w)
+                want = oracle.gemv_fp8_b128(c, s, x.float().numpy())
+                got = ops.gemv_fp8(torch.from_numpy(c).to(gpu), torch.from_numpy(s).to(gpu), x.to(gpu), out_f32=f32)
+            g = np_(got.float())
+            assert_gemv(g, None if f32 else g, want, tol=1e-5 if f32 else 2.0 ** -8)
+        elif kind in ("gguf1", "gguf_b"):
+            k, n = int(256 * rng.integers(1, 24)), 1 if kind == "gguf1" else int(rng.integers(2, 17))
+            quant = bool(rng.integers(0, 2))
+            ys, ws, xs, wants = [], [], [], []
+            for j in range(n):
+                codes = rng.integers(0, 256, (rows, k // 2), dtype=np.uint8)
+                sc = rng.integers(118, 126, (rows, k // 32), dtype=np.uint8)
+                x = data.activation(1, k, seed=seed * 1000 + t * 17 + j).float().numpy()[0]
+                if quant:
+                    x = oracle.act_quant(x[None], 32, True)[2][0]
+                wants.append(oracle.gemv_fp4(codes, sc, x[None])[0])
+                ws.append(torch.from_numpy(oracle.ocp_to_gguf17(codes, sc)).to(gpu))
+                xs.append(torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(gpu))
+                ys.append(torch.empty(rows, device=gpu))
+            if n == 1:
+                ops.stbl_gemv_mxfp4(ys[0], ws[0], xs[0], rows, k)
+            else:
+                ops.stbl_gemv_mxfp4_batch(ys, ws, xs, rows, k)
+            for j in range(n):
+                assert_gemv(np_(ys[j]), np_(ys[j]), wants[j], tol=2.0 ** -8)
+        else:
+            k = int(32 * rng.integers(1, 256))
+            w = np.clip(rng.standard_normal((rows, k)) * 100, -448, 448).astype(np.float32)
+            codes = oracle.e4m3_encode(w)
+            sc = rng.integers(113, 121, ((rows + 31) // 32, k // 32), dtype=np.uint8)
+            x = oracle.act_quant(data.activation(1, k, seed=seed * 100 + t).float().numpy(), 32, True)[2][0]
+            want = oracle.gemv_fp8_e8m0_engine(codes, sc, x)
+            y = torch.empty(rows, device=gpu)
+            ops.stbl_gemv_fp8(y, torch.from_numpy(codes).to(gpu), torch.from_numpy(sc).to(gpu),
+                              torch.from_numpy(x).to(gpu), rows, k, 1)
+            assert_gemv(np_(y), np_(y), want, tol=2.0 ** -8)
