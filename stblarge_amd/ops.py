@@ -473,33 +473,42 @@ def _work_for(work, m, n, k, device):
     return work
 
 
+GEMM_MAX_M = 64  # rows per stbl_amd_gemm / stbl_amd_gemm_q launch
+
+
 def gemm(codes, scales, x, fmt, act_block=128, out_f32=False, work=None):
-    """Y [M, N] = act_quant(X, act_block) . Wdeq^T for M <= 64 (fp4_gemm / fp8_gemm of ref/kernel.py).
-    `work` (from gemm_work) may be passed to reuse the scratch across calls on one stream."""
+    """Y [M, N] = act_quant(X, act_block) . Wdeq^T (fp4_gemm / fp8_gemm of ref/kernel.py), any M: one
+    launch per 64 rows (each output row depends only on its own activation row). `work` (from
+    gemm_work) may be passed to reuse the scratch across calls on one stream."""
     _need(x, torch.bfloat16, "x", 2)
     m, k = x.shape
     n = _gemm_shapes(codes, scales, fmt, k)
-    work = _work_for(work, m, n, k, x.device)
+    work = _work_for(work, min(m, GEMM_MAX_M), n, k, x.device)
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=x.device)
-    _lib.check(_lib.load().stbl_amd_gemm(fmt, _ptr(y), _ptr(codes), _ptr(scales), _ptr(x), m, n, k, act_block,
-                                         int(out_f32), _ptr(work), _stream()), "gemm")
+    for r0 in range(0, m, GEMM_MAX_M):
+        mc = min(GEMM_MAX_M, m - r0)
+        _lib.check(_lib.load().stbl_amd_gemm(fmt, _ptr(y[r0:r0 + mc]), _ptr(codes), _ptr(scales), _ptr(x[r0:r0 + mc]),
+                                             mc, n, k, act_block, int(out_f32), _ptr(work), _stream()), "gemm")
     return y
 
 
 def gemm_q(codes, scales, aq, a_s, fmt, act_block=128, out_f32=False, work=None):
     """Y [M, N] = (Aq * a_s) . Wdeq^T with the activations already quantized: aq e4m3 codes uint8 [M, K],
     a_s E8M0 scale bytes uint8 [M, K / act_block] (act_quant_e4m3's output), as ref/kernel.py's
-    fp8_gemm(a, a_s, b, b_s) takes them."""
+    fp8_gemm(a, a_s, b, b_s) takes them; any M, one launch per 64 rows."""
     _need(aq, torch.uint8, "aq", 2)
     _need(a_s, torch.uint8, "a_s", 2)
     m, k = aq.shape
     if tuple(a_s.shape) != (m, k // act_block):
         raise ValueError(f"a_s {tuple(a_s.shape)} does not match aq {tuple(aq.shape)} at block {act_block}")
     n = _gemm_shapes(codes, scales, fmt, k)
-    work = _work_for(work, m, n, k, aq.device)
+    work = _work_for(work, min(m, GEMM_MAX_M), n, k, aq.device)
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=aq.device)
-    _lib.check(_lib.load().stbl_amd_gemm_q(fmt, _ptr(y), _ptr(codes), _ptr(scales), _ptr(aq), _ptr(a_s), m, n, k,
-                                           act_block, int(out_f32), _ptr(work), _stream()), "gemm_q")
+    for r0 in range(0, m, GEMM_MAX_M):
+        mc = min(GEMM_MAX_M, m - r0)
+        _lib.check(_lib.load().stbl_amd_gemm_q(fmt, _ptr(y[r0:r0 + mc]), _ptr(codes), _ptr(scales), _ptr(aq[r0:r0 + mc]),
+                                               _ptr(a_s[r0:r0 + mc]), mc, n, k, act_block, int(out_f32), _ptr(work),
+                                               _stream()), "gemm_q")
     return y
 
 

@@ -71,6 +71,25 @@ def test_gemm_fp8(gpu, m, n, k):
 
 
 @pytest.mark.parametrize("fmt", [0, 1])
+def test_gemm_more_than_64_rows(gpu, fmt):
+    # M = 150 runs as launches of 64, 64 and 22 rows (ref/kernel.py's GEMMs take any M): against the
+    # oracle, and each 64-row block equal to a call on those rows alone, gemm and gemm_q alike
+    m, n, k = 150, 1024, 2048
+    w = data.weight(n, k, seed=91 + fmt)
+    q, deq = (oracle.quant_fp4, oracle.dequant_fp4) if fmt == 0 else (oracle.quant_fp8_b128, oracle.dequant_fp8_b128)
+    codes, scales = q(w.numpy())
+    x = data.activation(m, k, seed=92)
+    want = _oracle_gemm(x, deq(codes, scales), 128)
+    dc, ds, xg = torch.from_numpy(codes).to(gpu), torch.from_numpy(scales).to(gpu), x.to(gpu)
+    y32 = np_(ops.gemm(dc, ds, xg, fmt, 128, out_f32=True))
+    _check(y32, np_(ops.gemm(dc, ds, xg, fmt, 128)), want)
+    assert np.array_equal(y32[64:128], np_(ops.gemm(dc, ds, xg[64:128].contiguous(), fmt, 128, out_f32=True)))
+    assert np.array_equal(y32[128:], np_(ops.gemm(dc, ds, xg[128:].contiguous(), fmt, 128, out_f32=True)))
+    aq, a_s = ops.act_quant_e4m3(xg, 128)
+    assert np.array_equal(np_(ops.gemm_q(dc, ds, aq, a_s, fmt, 128, out_f32=True)), y32)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
 @pytest.mark.parametrize("block", [32, 128])
 def test_gemm_q_matches_gemm_and_oracle(gpu, fmt, block):
     # fp8_gemm(a, a_s, b, b_s) form: the activation quantized by a separate call (ref/kernel.py:85-102)
