@@ -16,7 +16,7 @@ import torch
 import oracle
 from stblarge_amd import data, ops
 from stblarge_amd.moe import ExpertCache, MoELayer
-from util import assert_gemv, bf16_ulps, np_, read_device
+from util import assert_gemv, assert_moe_sum, bf16_ulps, np_, read_device
 
 pytestmark = pytest.mark.gpu
 
@@ -516,3 +516,41 @@ def test_moe_experts_byte_scales_fallback(gpu):
         want = oracle.moe_fp4([[packed[i] for i in row] for row in pick], w, packed[n - 1], dim, inter,
                               x.float().numpy())
         assert bf16_ulps(y, want).max() <= 1
+
+
+def test_moe_random_configurations(gpu):
+    # 24 random expert steps over the three expert formats, a shared expert of the routed format or
+    # of the engine's FP8 E8M0 one, raw and official numerics, SwiGLU limit or none, 1-16 tokens,
+    # top-1..8 of up to 15 routed experts, against the dequantized composition
+    rng = np.random.default_rng(2024)
+    for case in range(24):
+        fmt = (ops.FP4, ops.FP8, ops.FP8_E8M0)[case % 3]
+        sfmt = fmt if rng.random() < 0.6 else (ops.FP8_E8M0 if fmt == ops.FP4 else fmt)
+        dim, inter = int(256 * rng.integers(1, 5)), int(128 * rng.integers(1, 5))
+        t, topk = int(rng.integers(1, 17)), int(rng.integers(1, 9))
+        nr = int(rng.integers(topk, topk + 8))
+        official, limit = bool(rng.integers(0, 2)), float(rng.choice([0.0, 7.0]))
+        slots, dq = [], []
+        for i in range(nr):
+            s, parts = make_expert(fmt, dim, inter, seed=5000 + 100 * case + 3 * i, gpu=gpu)
+            slots.append(s)
+            dq.append(deq_parts(fmt, parts))
+        shd, sh = None, -1
+        if rng.random() < 0.7:
+            s, parts = make_expert(sfmt, dim, inter, seed=9000 + case, gpu=gpu)
+            slots.append(s)
+            shd, sh = deq_parts(sfmt, parts), len(slots) - 1
+        pick = [list(rng.choice(nr, size=topk, replace=False)) for _ in range(t)]
+        w = (rng.random((t, topk)) / topk).astype(np.float32)
+        x = data.activation(t, dim, seed=case)
+        y = np_(ops.moe_experts(x.to(gpu), slots, pick, w.tolist(), fmt, dim, inter, shared=sh, limit=limit,
+                                official=official, shared_fmt=sfmt if sh >= 0 and sfmt != fmt else -1).float())
+        xs = x.float().numpy()
+        want = oracle.moe_deq([[dq[i] for i in row] for row in pick], w, shd, xs, limit, official)
+        terms = np.zeros((t, dim))
+        for ti in range(t):
+            for j, e in enumerate(pick[ti]):
+                terms[ti] += np.abs(oracle.expert_ffn_deq(*dq[e], xs[ti], float(w[ti, j]), limit, official))
+            if shd is not None:
+                terms[ti] += np.abs(oracle.expert_ffn_deq(*shd, xs[ti], 1.0, limit, official))
+        assert_moe_sum(y, want, terms)
