@@ -482,6 +482,8 @@ def gemm(codes, scales, x, fmt, act_block=128, out_f32=False, work=None):
     gemm_work) may be passed to reuse the scratch across calls on one stream."""
     _need(x, torch.bfloat16, "x", 2)
     m, k = x.shape
+    if m < 1:
+        raise ValueError("gemm: x has no rows")
     n = _gemm_shapes(codes, scales, fmt, k)
     work = _work_for(work, min(m, GEMM_MAX_M), n, k, x.device)
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=x.device)
@@ -499,6 +501,8 @@ def gemm_q(codes, scales, aq, a_s, fmt, act_block=128, out_f32=False, work=None)
     _need(aq, torch.uint8, "aq", 2)
     _need(a_s, torch.uint8, "a_s", 2)
     m, k = aq.shape
+    if m < 1:
+        raise ValueError("gemm_q: aq has no rows")
     if tuple(a_s.shape) != (m, k // act_block):
         raise ValueError(f"a_s {tuple(a_s.shape)} does not match aq {tuple(aq.shape)} at block {act_block}")
     n = _gemm_shapes(codes, scales, fmt, k)
