@@ -102,11 +102,12 @@ def test_gemv_fp4_zero_and_extreme_inputs(gpu):
 @pytest.mark.parametrize("rows,k,round_out", [(1000, 1280, 1), (2048, 7168, 0), (64, 96, 1),
                                                # the attention-side shapes of stbl/bench_gemv.py:103-107
                                                (32768, 1280, 1), (5120, 8192, 1), (1280, 5120, 0), (512, 5120, 1),
-                                               (16388, 1280, 1), (999, 1280, 1)])
+                                               (16388, 1280, 1), (999, 1280, 1), (2304, 5120, 1), (2560, 1280, 0),
+                                               (2300, 2048, 1)])
 def test_stbl_gemv_fp8_e8m0(gpu, rows, k, round_out):
     # stbl/test_kernels.py:82-98 input idiom: e4m3 weights, E8M0 scales 2^U[-14,-7] per 32x32;
     # 16388 x 1280 takes 8-row tiles, the last one half full; 999 x 1280 2-row tiles, the last one
-    # half full; 64 x 96 1-row tiles
+    # half full; 64 x 96 1-row tiles; 2304 x 5120, 2560 x 1280 and 2300 x 2048 (ragged) 4-row tiles
     rng = np.random.default_rng(rows)
     w = np.clip(rng.standard_normal((rows, k)) * 100, -448, 448).astype(np.float32)
     codes = oracle.e4m3_encode(w)
