@@ -725,7 +725,7 @@ def file_stack_workload(torch, guess_quality, n_layers=4, n_experts=24, topk=6, 
 def read_floor_workload(torch, nbytes, steps, warmup):
     """The bare streaming read of nbytes in one launch (stbl_amd_read_floor), timed exactly as the
     GEMV rows are: graph replays of launches that each read a different slice of a >= 512 MB buffer
-    (so the 256 MB Infinity Cache cannot serve repeats), events on the launch stream."""
+    (so the 256 MB Infinity Cache cannot serve repeats), exact-K samples as timed_steps takes them."""
     from stblarge_amd import _lib, ops
 
     dev = torch.device("cuda:0")
