@@ -51,3 +51,24 @@ def test_timed_steps_samples_exactly_the_requested_steps(gpu):
     assert tm["samples"] == math.ceil(10 * copies / 7) and tm["steps_per_sample"] == 7
     assert tm["sample_ms_min"] <= tm["sample_ms_median"] <= tm["sample_ms_max"]
     assert abs(tm["sample_ms_median"] / 7 - ms) < 1e-12
+
+
+def test_bench_line_reports_the_requested_steps(gpu):
+    # the driver's form: `--steps K --warmup W` gives one JSON line whose steps is K, with the
+    # roofline and the timing samples (the CPU baseline leg is skipped here to keep the test short)
+    import json
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--only", "fp4", "--no-cpu", "--steps", "20",
+                        "--warmup", "5"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [ln for ln in r.stdout.splitlines() if ln.strip()]
+    assert len(lines) == 1
+    d = json.loads(lines[0])
+    assert d["steps"] == 20 and d["warmup"] == 5 and d["n_gpus"] == 1
+    assert d["timing"]["steps_per_sample"] == 20 and d["timing"]["samples"] >= 10
+    assert abs(d["value"] - 7817216 / (d["ms_per_step"] * 1e-3) / 1e9) < 0.01 * d["value"]
+    assert d["roofline"]["achieved"] == d["value"] and 0 < d["roofline"]["frac"] < 1
