@@ -840,6 +840,9 @@ def cpu_scalar_oracle(seconds):
 
 def main():
     args = parse()
+    if args.steps < 1 or args.warmup < 0:
+        print(f"bench.py needs --steps >= 1 and --warmup >= 0 (got {args.steps}, {args.warmup})", file=sys.stderr)
+        sys.exit(2)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the path is single-GPU; see the sharding notes): --gpus {args.gpus} "
               "is not supported", file=sys.stderr)

@@ -26,3 +26,8 @@ def test_more_than_one_gpu_is_refused():
 def test_no_gpu_fails_loudly():
     r = run("--steps", "1", "--warmup", "0")
     assert r.returncode == 2 and "needs a GPU" in r.stderr and r.stdout == ""
+
+
+def test_steps_below_one_are_refused():
+    r = run("--steps", "0")
+    assert r.returncode == 2 and "--steps >= 1" in r.stderr and r.stdout == ""
