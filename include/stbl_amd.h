@@ -38,12 +38,15 @@ void stbl_round_bf16(float *x, int n, hipStream_t st);
 
 /* stbl/kernels.h:14-15 -- y[r] = sum_k x[k] * e4m3(w[r][k]) * 2^(scale[r/32][k/32]-127); y rounded
  * to bf16 when round_out. w [rows][k] e4m3, scale E8M0 [(rows+31)/32][k/32], x fp32 [k], y fp32
- * [rows]. k % 32 == 0, k <= 8192, w and x 16-byte aligned. */
+ * [rows]. Scale bytes decode as the engine's (stbl/kernels.cu:32): 0 -> 0.0, 255 -> +Inf times the
+ * 32-block's sum. k % 32 == 0 (any k), w and x 16-byte aligned. */
 void stbl_gemv_fp8(float *y, const void *w, const void *scale, const float *x, int rows, int k, int round_out,
                    hipStream_t st);
 
 /* stbl/kernels.h:16 -- MXFP4 rows of GGUF 17-byte blocks ([E8M0][16 bytes: element i low nibble,
- * 16+i high nibble]); y = bf16(W x) stored as fp32. k % 256 == 0, k <= 16384, w 8-byte aligned. */
+ * 16+i high nibble]); y = bf16(W x) stored as fp32. Scale bytes decode as the engine's
+ * (stbl/kernels.cu:32, :185): 0 -> 0.0, 255 -> +Inf times the block's sum. k % 256 == 0 (any k), w
+ * 8-byte aligned. */
 void stbl_gemv_mxfp4(float *y, const void *w, const float *x, int rows, int k, hipStream_t st);
 
 /* y[r] = sum_i x_r[i] * w[r][i] in fp32 (bf16-rounded when round_out), bf16 weights [rows][k]; x_r = x

@@ -164,24 +164,32 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     float vals[NV];
 #pragma unroll
     for (int i = M * R; i < NV; i++) vals[i] = 0.f;
+    // GGUF rows (the reference ABI) take each block's sum at scale 1 times the engine's decode of the
+    // block's scale byte, the float with that exponent field (stbl/kernels.cu:32, :185): byte 0 gives
+    // 0.0 and 255 +Inf (the block's sum times +Inf: +-Inf, or NaN for a zero sum), where E8M0 (and the
+    // scaled conversions) read 2^-127 and NaN. For bytes 1..254 this is the same product as a scale
+    // inside the conversions (a power of two), and measured no slower on the GGUF tiles (2304x5120
+    // 4.48 -> 4.35 us; a ballot-guarded fix-up for 0 and 255 instead cost 4-6%).
     if constexpr (kGgufX) {
         if (gguf_bf16) {
 #pragma unroll
-            for (int r = 0; r < R; r++) vals[r] = active ? gguf_dot_bf16(w[r], xg, e8m0_cvt_scale(sb[r])) : 0.f;
+            for (int r = 0; r < R; r++) vals[r] = active ? gguf_dot_bf16(w[r], xg, 1.0f) * __uint_as_float(sb[r] << 23) : 0.f;
         }
     }
 #pragma unroll
     for (int r = 0; r < R && !gguf_bf16; r++) {
-        // E8M0 scales (FP4; FP8 E8M0 with bf16 x) go into the conversions; the FP8 fp32 block scale
-        // and the fp32-x FP8 path multiply the chunk sum
+        // E8M0 scales (OCP FP4; FP8 E8M0 with bf16 x) go into the conversions; the GGUF blocks, the
+        // FP8 fp32 block scale and the fp32-x FP8 path multiply the chunk sum
         float s[M];
-        if constexpr (XF32 && T::fp4) chunk_dot<F, M, CH>(s, w[r], xf, e8m0_cvt_scale(sb[r]));
+        if constexpr (F == WFmt::FP4_GGUF) chunk_dot<F, M, CH>(s, w[r], xf, 1.0f);
+        else if constexpr (XF32 && T::fp4) chunk_dot<F, M, CH>(s, w[r], xf, e8m0_cvt_scale(sb[r]));
         else if constexpr (XF32) chunk_dot<F, M, CH>(s, w[r], xf);
         else if constexpr (T::fp4) chunk_dot_packed<F, M, CH>(s, w[r], xw, e8m0_cvt_scale(sb[r]));
         else if constexpr (F == WFmt::FP8_E8M0) chunk_dot_packed<F, M, CH>(s, w[r], xw, e8m0_cvt_scale(lsb));
         else chunk_dot_packed<F, M, CH>(s, w[r], xw);
         float scale = 1.f;
-        if constexpr (F == WFmt::FP8_B128) scale = lscale;
+        if constexpr (F == WFmt::FP4_GGUF) scale = __uint_as_float(sb[r] << 23);
+        else if constexpr (F == WFmt::FP8_B128) scale = lscale;
         else if constexpr (F == WFmt::FP8_E8M0 && XF32) scale = lsb == 255 ? 1.f : __uint_as_float(lsb << 23);  // 0: 0.0
 #pragma unroll
         for (int t = 0; t < M; t++) vals[t * R + r] = active ? s[t] * scale : 0.f;
@@ -322,7 +330,75 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(float *__restrict__ y, const 
     }
 }
 
+// Reference-ABI GEMVs over any K (stbl/kernels.cu:104-131 and :159-189 loop over K in 32-block
+// slices): the one-pass tiles above hold at most kMaxWaves * 64 chunks per row, so longer rows
+// (FP8 K > 8192, GGUF FP4 K > 16384; no call site of the reference engine has them) take this
+// kernel. A 256-thread workgroup owns R rows; thread j sums the 32-element blocks j, j + 256, ... of
+// each row: the block's products at scale 1 (the same conversions as the tiles), times the engine's
+// decode of the block's scale byte (the float with that exponent field: 0 gives 0.0, 255 +Inf,
+// stbl/kernels.cu:32), added to the row's running sum. Lanes reduce with DPP, the 4 waves through
+// LDS in wave order. GGUF: w [rows][k/32][17]; FP8: w [rows][k] e4m3 with E8M0 bytes
+// [(rows+31)/32][k/32] in the job's s. x fp32 [k].
+template <bool GGUF, int R>
+__global__ __launch_bounds__(256) void k_gemv_abi_longk(GemvJobs jobs, int rows, int k, int out_mode) {
+    const GemvJob J = jobs.j[blockIdx.y];
+    const int nblk = k >> 5, row0 = blockIdx.x * R;
+    const float *x = (const float *)J.x;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
+    for (int b = threadIdx.x; b < nblk; b += 256) {
+        float xf[1][32];
+        load_x<true, 1, 32>(xf, x, k, b * 32);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const size_t row = (size_t)min(row0 + r, rows - 1);
+            float bsum;
+            uint32_t sbyte;
+            if constexpr (GGUF) {
+                u32x4 codes;
+                load_gguf_block(J.w + row * (size_t)nblk * 17 + (size_t)b * 17, sbyte, codes);
+                float s[1];
+                chunk_dot<WFmt::FP4_GGUF, 1, 32>(s, codes, xf, 1.0f);
+                bsum = s[0];
+            } else {
+                const uint8_t *p = J.w + row * (size_t)k + (size_t)b * 32;
+                const u32x4 w0 = ld_stream(p), w1 = ld_stream(p + 16);
+                sbyte = ((const uint8_t *)J.s)[(row >> 5) * (size_t)nblk + b];
+                float lo[1][16], hi[1][16], s0[1], s1[1];
+#pragma unroll
+                for (int i = 0; i < 16; i++) lo[0][i] = xf[0][i], hi[0][i] = xf[0][16 + i];
+                chunk_dot<WFmt::FP8_E8M0, 1, 16>(s0, w0, lo);
+                chunk_dot<WFmt::FP8_E8M0, 1, 16>(s1, w1, hi);
+                bsum = s0[0] + s1[0];
+            }
+            acc[r] += bsum * __uint_as_float((sbyte & 0xffu) << 23);
+        }
+    }
+    __shared__ float red[4][R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const float t = dpp_sum(acc[r]);
+        if (lane == 63) red[wave][r] = t;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < R && row0 + (int)threadIdx.x < rows) {
+        const int r = threadIdx.x;
+        const float v = ((red[0][r] + red[1][r]) + red[2][r]) + red[3][r];
+        ((float *)J.y)[row0 + r] = out_mode == OUT_F32 ? v : bf16_round(v);
+    }
+}
+
 static inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// The reference ABI's rows beyond the one-pass tiles' K (see k_gemv_abi_longk).
+template <bool GGUF>
+static hipError_t launch_longk(const GemvJobs &jobs, int njobs, int rows, int k, int out_mode, hipStream_t st) {
+    hipLaunchKernelGGL((k_gemv_abi_longk<GGUF, 4>), dim3(ceil_div(rows, 4), njobs), dim3(256), 0, st, jobs, rows, k,
+                       out_mode);
+    return hipGetLastError();
+}
 
 template <WFmt F, bool XF32, int M, int R>
 static hipError_t launch_r(const GemvJobs &jobs, int njobs, int rows, int k, int out_mode, hipStream_t st) {
@@ -490,22 +566,22 @@ int stbl_amd_gemv_fp8_batch(void *const *y, const void *const *codes, const void
 // stbl/kernels.h:14-15. Requires k % 32 == 0 and 16-byte aligned rows, as the reference does.
 void stbl_gemv_fp8(float *y, const void *w, const void *scale, const float *x, int rows, int k, int round_out,
                    hipStream_t st) {
-    if (!y || !w || !scale || !x || rows <= 0 || k <= 0 || k % 32 != 0 || k / 16 > kMaxWaves * 64 || !aligned16(w) ||
-        !aligned16(x)) {
+    if (!y || !w || !scale || !x || rows <= 0 || k <= 0 || k % 32 != 0 || !aligned16(w) || !aligned16(x)) {
         abi_fail(hipErrorInvalidValue, "stbl_gemv_fp8: bad arguments (rows=%d k=%d)", rows, k);
         return;
     }
     GemvJobs jobs = {};
     jobs.j[0] = GemvJob{(const uint8_t *)w, scale, x, y};
-    abi_status(launch<WFmt::FP8_E8M0, true, 1>(jobs, 1, rows, k, round_out ? OUT_F32_ROUNDED : OUT_F32, st),
-               "stbl_gemv_fp8 launch");
+    const int mode = round_out ? OUT_F32_ROUNDED : OUT_F32;
+    if (k / 16 > kMaxWaves * 64) abi_status(launch_longk<false>(jobs, 1, rows, k, mode, st), "stbl_gemv_fp8 launch");
+    else abi_status(launch<WFmt::FP8_E8M0, true, 1>(jobs, 1, rows, k, mode, st), "stbl_gemv_fp8 launch");
 }
 
 // stbl/kernels.h:19-20. n <= 16 same-shape matrices in one launch; needs k % 256 == 0 and w 8-byte
 // aligned (the reference's preconditions, stbl/kernels.cu:138-139). y, w, x are host arrays.
 void stbl_gemv_mxfp4_batch(float *const *y, const void *const *w, const float *const *x, int n, int rows, int k,
                            hipStream_t st) {
-    if (!y || !w || !x || n <= 0 || n > kMxBatch || rows <= 0 || k <= 0 || k % 256 != 0 || k / 32 > kMaxWaves * 64) {
+    if (!y || !w || !x || n <= 0 || n > kMxBatch || rows <= 0 || k <= 0 || k % 256 != 0) {
         abi_fail(hipErrorInvalidValue, "stbl_gemv_mxfp4_batch: bad arguments (n=%d rows=%d k=%d)", n, rows, k);
         return;
     }
@@ -517,7 +593,10 @@ void stbl_gemv_mxfp4_batch(float *const *y, const void *const *w, const float *c
         }
         jobs.j[j] = GemvJob{(const uint8_t *)w[j], nullptr, x[j], y[j]};
     }
-    abi_status(launch<WFmt::FP4_GGUF, true, 1>(jobs, n, rows, k, OUT_F32_ROUNDED, st), "stbl_gemv_mxfp4_batch launch");
+    if (k / 32 > kMaxWaves * 64)
+        abi_status(launch_longk<true>(jobs, n, rows, k, OUT_F32_ROUNDED, st), "stbl_gemv_mxfp4_batch launch");
+    else
+        abi_status(launch<WFmt::FP4_GGUF, true, 1>(jobs, n, rows, k, OUT_F32_ROUNDED, st), "stbl_gemv_mxfp4_batch launch");
 }
 
 // stbl/kernels.h:16.

@@ -280,24 +280,24 @@ def _edge_scales(rng, shape):
 
 @pytest.mark.parametrize("rows,k,n,quant", [(2304, 5120, 1, False), (5120, 2304, 1, False), (999, 2560, 1, False),
                                             (64, 256, 1, False), (2304, 5120, 12, True), (2304, 5120, 12, False),
-                                            (5120, 2304, 6, True), (1100, 2560, 16, True)])
+                                            (5120, 2304, 6, True), (1100, 2560, 16, True), (300, 20480, 1, True),
+                                            (64, 16640, 3, False)])
 def test_stbl_gemv_mxfp4_edge_scale_bytes(gpu, rows, k, n, quant):
     # GGUF blocks with E8M0 bytes 0 and 255, in every GGUF tile (one-round 9-10 rows, 4, 2 and 1 rows,
-    # the batches' 16- and 8-row tiles with the packed-bf16 and the fp32 products). These tiles read
-    # the bytes as E8M0 defines them (2^-127 and NaN, the scaled conversions' reading; oracle.gemv_fp4),
-    # where the reference engine's decode gives 0.0 and +Inf (stbl/kernels.cu:32,185; oracle.
-    # gemv_gguf_engine): the two agree on every row without those bytes, and a 255 row is NaN here.
+    # the batches' 16- and 8-row tiles with the packed-bf16 and the fp32 products, and the any-K
+    # kernel past 16384): the reference engine decodes byte 0 as 0.0 and 255 as +Inf times the
+    # block's sum (stbl/kernels.cu:32,185; oracle.gemv_gguf_engine), so a row with a 255 block is
+    # +-Inf (NaN when it also holds -+Inf, or the block's sum is 0), and a 0 block adds nothing.
     rng = np.random.default_rng(rows * 7 + n)
-    ys, ws, xs, wants, engine, special = [], [], [], [], [], []
+    ys, ws, xs, engine = [], [], [], []
     for j in range(n):
         codes = rng.integers(0, 256, (rows, k // 2), dtype=np.uint8)
         sc = _edge_scales(rng, (rows, k // 32))
-        codes[5, :16], sc[5, 0] = 0, 255
+        codes[5, :16], sc[5, 0] = 0, 255  # row 5's first block: a zero sum times +Inf, NaN
+        sc[6, :] = 0  # row 6: every block scaled to 0.0
         x = _quantized_x(k, 700 + j) if quant else data.activation(1, k, seed=700 + j).float().numpy()[0]
         blocks = oracle.ocp_to_gguf17(codes, sc)
-        wants.append(oracle.gemv_fp4(codes, sc, x[None])[0])
         engine.append(oracle.gemv_gguf_engine(blocks, x, rows, k))
-        special.append(((sc == 0) | (sc == 255)).any(axis=1))
         ws.append(torch.from_numpy(blocks).to(gpu))
         xs.append(torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(gpu))
         ys.append(torch.empty(rows, device=gpu))
@@ -306,9 +306,59 @@ def test_stbl_gemv_mxfp4_edge_scale_bytes(gpu, rows, k, n, quant):
     else:
         ops.stbl_gemv_mxfp4_batch(ys, ws, xs, rows, k)
     for j in range(n):
-        assert np.isnan(wants[j][5]) and np.isnan(wants[j]).sum() < rows
-        np.testing.assert_allclose(wants[j][~special[j]], engine[j][~special[j]], rtol=1e-12)
-        _assert_special_rows(np_(ys[j]).astype(np.float64), wants[j])
+        want = engine[j]
+        assert np.isnan(want[5]) and want[6] == 0 and np.isinf(want).any() and np.isfinite(want).any()
+        got = np_(ys[j]).astype(np.float64)
+        assert got[6] == 0
+        _assert_special_rows(got, want)
+
+
+@pytest.mark.parametrize("rows,k,n", [(130, 20480, 1), (37, 16640, 2), (64, 32768, 1)])
+def test_stbl_gemv_mxfp4_any_k(gpu, rows, k, n):
+    # rows longer than the one-pass tiles hold (16384 elements: 512 GGUF blocks) take the any-K
+    # kernel, as the reference's kernel loops over K (stbl/kernels.cu:159-189); the engine's x
+    # (act_quant) and random fp32 x
+    rng = np.random.default_rng(k + n)
+    ys, ws, xs, wants = [], [], [], []
+    for j in range(n):
+        codes = rng.integers(0, 256, (rows, k // 2), dtype=np.uint8)
+        sc = rng.integers(118, 126, (rows, k // 32), dtype=np.uint8)
+        x = _quantized_x(k, 900 + j) if j % 2 == 0 else data.activation(1, k, seed=900 + j).float().numpy()[0]
+        blocks = oracle.ocp_to_gguf17(codes, sc)
+        wants.append(oracle.gemv_gguf_engine(blocks, x, rows, k))
+        ws.append(torch.from_numpy(blocks).to(gpu))
+        xs.append(torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(gpu))
+        ys.append(torch.empty(rows, device=gpu))
+    if n == 1:
+        ops.stbl_gemv_mxfp4(ys[0], ws[0], xs[0], rows, k)
+    else:
+        ops.stbl_gemv_mxfp4_batch(ys, ws, xs, rows, k)
+    for y, want in zip(ys, wants):
+        assert_gemv(np_(y), np_(y), want, tol=2.0 ** -8)
+
+
+@pytest.mark.parametrize("rows,k,round_out", [(100, 12288, 1), (70, 8224, 0), (33, 24576, 1)])
+def test_stbl_gemv_fp8_any_k(gpu, rows, k, round_out):
+    # FP8 E8M0 rows past 8192 elements (the one-pass tiles' 512 chunks of 16) take the any-K kernel,
+    # as the reference's loops over 32-block slices (stbl/kernels.cu:104-131); engine scale bytes 0
+    # and 255 planted as in the one-pass test
+    rng = np.random.default_rng(rows + k)
+    w = np.clip(rng.standard_normal((rows, k)) * 100, -448, 448).astype(np.float32)
+    codes = oracle.e4m3_encode(w)
+    sc = rng.integers(127 - 14, 127 - 6, ((rows + 31) // 32, k // 32), dtype=np.uint8)
+    sc[0, 3], sc[1, 0] = 255, 0  # rows 0-31 +-Inf (one block times +Inf); rows 32-63 lose a block
+    x = oracle.act_quant(data.activation(1, k, seed=k).float().numpy(), 32, True)[2][0]
+    want = oracle.gemv_fp8_e8m0_engine(codes, sc, x)
+    assert np.isinf(want[:32]).all() and np.isfinite(want[32:]).all()
+    y = torch.empty(rows, device=gpu)
+    ops.stbl_gemv_fp8(y, torch.from_numpy(codes).to(gpu), torch.from_numpy(sc).to(gpu), torch.from_numpy(x).to(gpu),
+                      rows, k, round_out)
+    got = np_(y).astype(np.float64)
+    if round_out:
+        _assert_special_rows(got, want)
+    else:
+        assert np.array_equal(got[:32], want[:32])
+        assert_gemv(got[32:], None, want[32:])
 
 
 @pytest.mark.parametrize("rows,k", [(2304, 5120), (5120, 8192), (512, 5120), (64, 96), (999, 1280)])
