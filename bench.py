@@ -45,6 +45,11 @@ def parse():
     ap.add_argument("--moe-warmup", type=int, default=1000)
     ap.add_argument("--eager", action="store_true", help="also time launches issued one by one from Python")
     ap.add_argument("--no-graph", action="store_true", help="launch every step from Python (for counter runs)")
+    ap.add_argument("--rows-out", default=None, help="write every row's full figures to this JSON file")
+    ap.add_argument("--trace-summary", default=None, metavar="CSV",
+                    help="print the per-dispatch summary of a rocprofv3 kernel-trace CSV and exit (no GPU)")
+    ap.add_argument("--trace-kernel", default=r"k_gemv<\(stbl::WFmt\)0, false, 1,",
+                    help="kernel-name regex for --trace-summary (default: the headline FP4 GEMV kernel)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="after the workloads, copy 64 MiB device to device 5 times (the reference transfer for "
                          "scaling HBM byte counters)")
@@ -54,7 +59,7 @@ def parse():
 LAST_TIMING = {}  # the last graph-timed row's samples, for the headline line
 
 
-def timed_steps(torch, launch, copies, steps, warmup, use_graph=True):
+def timed_steps(torch, launch, copies, steps, warmup, use_graph=True, isolated=0):
     """Times exactly `steps` steps (launch(i) issues step i on the current stream) after `warmup`
     untimed ones, and returns (ms per step, steps).
 
@@ -66,7 +71,12 @@ def timed_steps(torch, launch, copies, steps, warmup, use_graph=True):
     interval minus the median interval of the back-to-back pairs (one stamp launch and its launch
     gap, the instrument's own cost), and ms per step is the median sample over `steps`; R =
     max(1, ceil(10 copies / steps)) so that at least ten passes over the rotation are sampled. HIP
-    events around the timed replay give a cross-check over all of its steps."""
+    events around the timed replay give a cross-check over all of its steps.
+
+    isolated > 0 adds that many single launches after the pairs, each alone between two stamps with
+    a stamp pair before it (no step of its own kind running before or after it, the condition a
+    profiler's serialized dispatches run in); their median, net of the stamps' cost, is reported as
+    isolated_launch_us next to the steady-state samples."""
     if not use_graph:
         stream = torch.cuda.Stream()
         torch.cuda.synchronize()
@@ -89,7 +99,8 @@ def timed_steps(torch, launch, copies, steps, warmup, use_graph=True):
     if khz.value <= 0:
         raise RuntimeError(f"the GPU reports a wall clock of {khz.value} kHz")
     reps, pairs = max(1, math.ceil(10 * copies / steps)), 8
-    stamps = torch.zeros(reps + 1 + 2 * pairs, dtype=torch.int64, device="cuda:0")
+    iso0 = reps + 1 + 2 * pairs
+    stamps = torch.zeros(iso0 + 3 * isolated, dtype=torch.int64, device="cuda:0")
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
@@ -116,6 +127,12 @@ def timed_steps(torch, launch, copies, steps, warmup, use_graph=True):
             for p in range(pairs):
                 stamp(reps + 1 + 2 * p)
                 stamp(reps + 2 + 2 * p)
+            for j in range(isolated):
+                stamp(iso0 + 3 * j)
+                stamp(iso0 + 3 * j + 1)
+                launch(n % copies)
+                n += 1
+                stamp(iso0 + 3 * j + 2)
         graph.replay()
         torch.cuda.synchronize()
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -134,11 +151,14 @@ def timed_steps(torch, launch, copies, steps, warmup, use_graph=True):
                         "stamp_pair_us": calib * 1e3, "clock_khz": khz.value,
                         # cross-check: HIP events around the whole timed replay, over all its steps
                         # (warmup included; the stamps and the graph's start add a little)
-                        "events_ms_per_step_whole_replay": ev0.elapsed_time(ev1) / (warmup + reps * steps)})
+                        "events_ms_per_step_whole_replay": ev0.elapsed_time(ev1) / (warmup + reps * steps + isolated)})
+    if isolated:
+        iso = sorted(ms(t[iso0 + 3 * j + 2] - t[iso0 + 3 * j + 1]) - calib for j in range(isolated))
+        LAST_TIMING.update({"isolated_launches": isolated, "isolated_launch_us": iso[isolated // 2] * 1e3})
     return samples[reps // 2] / steps, steps
 
 
-def gemv_workload(torch, fmt, rows, k, m, steps, warmup, use_graph=True):
+def gemv_workload(torch, fmt, rows, k, m, steps, warmup, use_graph=True, isolated=0):
     from stblarge_amd import data, ops
 
     dev = torch.device("cuda:0")
@@ -162,7 +182,7 @@ def gemv_workload(torch, fmt, rows, k, m, steps, warmup, use_graph=True):
     def launch(i):
         fn(cs[i], ss[i], x, out=y)
 
-    ms, n = timed_steps(torch, launch, copies, steps, warmup, use_graph)
+    ms, n = timed_steps(torch, launch, copies, steps, warmup, use_graph, isolated=isolated if use_graph else 0)
     gbs = alg / (ms * 1e-3) / 1e9
     return {"workload": f"{fmt}_gemv_{rows}x{k}_m{m}", "rows": rows, "k": k, "m": m, "ms_per_step": ms,
             "steps": n, "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS, "weight_copies": copies,
@@ -191,12 +211,12 @@ def gemv_batch_workload(torch, fmt, rows, k, steps, warmup, nb=16, use_graph=Tru
     def launch(i):
         ops.gemv_batch(cs[i], ss[i], xs, f, outs=ys)
 
-    ms, n = timed_steps(torch, launch, groups, max(20, steps // nb), max(4, warmup // nb), use_graph)
+    ms, n = timed_steps(torch, launch, groups, steps, warmup, use_graph)
     per = data.algorithmic_bytes_fp4(rows, k, 1) if fmt == "fp4" else data.algorithmic_bytes_fp8(rows, k, 1)
     alg = nb * per
     gbs = alg / (ms * 1e-3) / 1e9
-    return {"workload": f"{fmt}_gemv_batch{nb}_{rows}x{k}_m1", "ms_per_launch": ms, "gemv_per_launch": nb,
-            "launches": n, "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS}
+    return {"workload": f"{fmt}_gemv_batch{nb}_{rows}x{k}_m1", "ms_per_step": ms, "gemv_per_launch": nb,
+            "steps": n, "alg_bytes": alg, "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS}
 
 
 def ffn_workload(torch, fmt, steps, warmup, use_graph=True):
@@ -838,8 +858,164 @@ def cpu_scalar_oracle(seconds):
             "sample": f"{reps} x orc_gemv_fp4 (scalar C, fp64 accumulate) in {el:.1f} s on one core of {_cpu_model()}"}
 
 
+# rows whose figures the stdout line carries (every row goes to stderr and to --rows-out)
+LINE_ROWS = (
+    "fp4_gemv_7168x2048_m1", "fp8_gemv_2048x7168_m1", "fp8_gemv_7168x2048_m1", "fp4_gemv_2048x7168_m4",
+    "fp8_gemv_2048x7168_m4", "fp4_gemv_batch16_7168x2048_m1", "fp8_gemv_batch16_7168x2048_m1",
+    "fp4_gemv_batch64_7168x2048_m1", "fp8_gemv_batch64_7168x2048_m1", "fp4_expert_ffn_7168x2048_m1",
+    "fp8_expert_ffn_7168x2048_m1", "fp4_gemm_q_m64_2048x7168", "fp8_gemm_q_m64_2048x7168", "fp4_gemm_m64_2048x7168",
+    "fp8_gemm_m64_2048x7168", "fp4_gemm_q_m64_7168x2048", "ref_abi_gemv_mxfp4_2304x5120",
+    "ref_abi_gemv_mxfp4_5120x2304", "ref_abi_gemv_fp8_2304x5120", "ref_abi_gemv_mxfp4_batch12_2304x5120",
+    "ref_abi_gemv_mxfp4_batch6_5120x2304", "ref_abi_moe_step_v41_t1", "moe_experts_allhit_t1_fp4",
+    "moe_experts_allhit_t4_fp4", "moe_experts_allhit_t1_fp4_fp8e8m0_shared", "moe_v41_allhit_t1_fp4_top6_fp8e8m0_shared",
+    "moe_v41_allhit_t4_fp4_top6_fp8e8m0_shared", "moe_layer_t1_fp4_256x_top8_lru64", "moe_layer_t4_fp4_256x_top8_lru64",
+    "expert_file_direct_v41_1x_r8", "expert_file_stack_4l_v41_top6_prefetch_q1", "read_floor_7817216B",
+)
+LINE_MAX_BYTES = 4096
+
+
+def _r(v, nd=3):
+    """v rounded to nd significant digits (None stays None)."""
+    if v is None or v == 0:
+        return v
+    return round(v, max(0, nd - 1 - int(math.floor(math.log10(abs(v))))))
+
+
+def compact_row(r):
+    """A row's figures for the stdout line: [us per step, GB/s, fraction of 8 TB/s] for GEMV-like rows
+    (with TFLOP/s for GEMMs, tokens/s for MoE steps); a short dict for the LRU, file-tier and CPU rows."""
+    if "hit_rate" in r and "refill_GB_s" in r:
+        return {"ms": _r(r["ms_per_step"]), "tok_s": _r(r["tokens_per_s"]), "hit": _r(r["hit_rate"]),
+                "refill_GB_s": _r(r["refill_GB_s"])}
+    if "ms_per_lookup_median" in r:
+        return {"ms_per_expert": _r(r["ms_per_expert"]), "GB_s": _r(r["GB_s"]), "direct": r["direct"]}
+    if "ms_per_token" in r:
+        return {"ms_per_token": _r(r["ms_per_token"]), "hit": _r(r["hit_rate"])}
+    if "ms_per_gemv" in r:
+        return {"GB_s": _r(r["GB_s"]), "cores": r["cores"]}
+    out = [_r(r["ms_per_step"] * 1e3), _r(r["GB_s"]), _r(r["frac_hbm_peak"])]
+    if "TFLOP_s" in r:
+        out.append(_r(r["TFLOP_s"]))
+    elif "tokens_per_s" in r:
+        out.append(_r(r["tokens_per_s"]))
+    return out
+
+
+def stderr_text(r):
+    """One short human-readable line per row."""
+    w = r["workload"]
+    if "hit_rate" in r and "refill_GB_s" in r:
+        return (f"# {w}: {r['ms_per_step']:.3f} ms/step, {r['tokens_per_s']:.0f} tok/s, hit {r['hit_rate']:.3f}, "
+                f"refill {r['refill_GB_s']:.1f} GB/s")
+    if "ms_per_lookup_median" in r:
+        return f"# {w}: {r['ms_per_expert']:.2f} ms/expert, {r['GB_s']:.2f} GB/s"
+    if "ms_per_token" in r:
+        return f"# {w}: {r['ms_per_token']:.1f} ms/token, hit {r['hit_rate']:.2f}"
+    if "us" in r:  # stbl/bench_gemv.py's own method
+        return f"# {w}: {r['us']:.2f} us, {r['GB_s']:.0f} GB/s"
+    if "ms_per_gemv" in r:
+        return f"# {w}: {r['GB_s']:.2f} GB/s"
+    t = f"# {w}: {r['ms_per_step'] * 1e3:.2f} us, {r['GB_s']:.0f} GB/s ({100 * r['frac_hbm_peak']:.1f}%)"
+    if "TFLOP_s" in r:
+        t += f", {r['TFLOP_s']:.0f} TFLOP/s"
+    elif "tokens_per_s" in r:
+        t += f", {r['tokens_per_s']:.0f} tok/s"
+    if "frac_of_read_floor" in r:
+        t += f", {100 * r['frac_of_read_floor']:.0f}% of bare read"
+    return t
+
+
+def make_line(head, extra, cpu, timing, warmup, traffic=None, profiled=None):
+    """The one JSON line bench.py prints on stdout (at most LINE_MAX_BYTES): the headline row's
+    figures with its roofline, the target shape's rows, the CPU baseline, the timing samples and the
+    LINE_ROWS figures of the other rows that ran."""
+    gbs = head["GB_s"]
+    target = {}
+    for key, name in (("fp4", "fp4_gemv_7168x2048_m1"), ("fp8", "fp8_gemv_7168x2048_m1"),
+                      ("fp4_batch16", "fp4_gemv_batch16_7168x2048_m1"), ("fp8_batch16", "fp8_gemv_batch16_7168x2048_m1")):
+        if name in extra:
+            target[key] = {"us": _r(extra[name]["ms_per_step"] * 1e3), "GB_s": _r(extra[name]["GB_s"]),
+                           "frac": _r(extra[name]["frac_hbm_peak"])}
+    roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+            "frac_of_read_floor": _r(head.get("frac_of_read_floor"))}
+    if "isolated_launch_us" in timing:
+        iso = timing["isolated_launch_us"]
+        roof["isolated_launch_us"] = _r(iso, 4)
+        roof["isolated_frac"] = round(head["alg_bytes"] / (iso * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)
+    if profiled:
+        roof["profiled"] = profiled
+    tm = {k: (_r(v, 4) if isinstance(v, float) else v) for k, v in timing.items()}
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": head["steps"],
+        "warmup": warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "e2m1 weights x bf16 activations, f32 accumulate",
+        "data": "synthetic (seeded N(0,0.02) weights quantized on the GPU, N(0,1) bf16 x)",
+        "config": {"workload": head["workload"], "rows": head["rows"], "k": head["k"], "m": head["m"],
+                   "weight_copies": head["weight_copies"],
+                   "rotation_MB": round(head["weight_copies"] * head["alg_bytes"] / 1e6, 1)},
+        "roofline": roof,
+        "target_7168x2048": target,
+        "cpu_baseline": cpu,
+        "timing": tm,
+        "extra_cols": "[us/step, GB/s, frac of 8 TB/s, TFLOP/s | tok/s]",
+        "extra": {n: compact_row(extra[n]) for n in LINE_ROWS if n in extra},
+    }
+    return line
+
+
+def profiled_headline():
+    """The headline kernel's figures from the committed rocprofv3 kernel-trace summary
+    (profiles/gemv_fp4_2048x7168_kernel_trace.md, `profiled_*:` lines), or None."""
+    path = os.path.join(ROOT, "profiles", "gemv_fp4_2048x7168_kernel_trace.md")
+    out = {}
+    try:
+        for line in open(path):
+            if line.startswith("profiled_") and ":" in line:
+                k, v = line.split(":", 1)
+                out[k.strip()[len("profiled_"):]] = float(v.split()[0])
+    except (OSError, ValueError):
+        return None
+    return out or None
+
+
+def trace_summary(path, kernel_regex):
+    """Per-dispatch figures of a rocprofv3 --kernel-trace CSV (…_kernel_trace.csv) for the kernels
+    whose name matches kernel_regex: calls, median and mean duration, and the median and mean
+    start-to-start spacing and idle gap between consecutive dispatches of those kernels with no other
+    dispatch between them (the step time the profiled run itself saw). Returns a dict (ns)."""
+    import csv
+    import re
+    import statistics
+
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    pat = re.compile(kernel_regex)
+    hit = [i for i, r in enumerate(rows) if pat.search(r["Kernel_Name"])]
+    st = [int(r["Start_Timestamp"]) for r in rows]
+    en = [int(r["End_Timestamp"]) for r in rows]
+    dur = [en[i] - st[i] for i in hit]
+    nxt = [(i, j) for i, j in zip(hit, hit[1:]) if j == i + 1]
+    sp = [st[j] - st[i] for i, j in nxt]
+    gap = [st[j] - en[i] for i, j in nxt]
+    med = lambda v: statistics.median(v) if v else None
+    avg = lambda v: statistics.mean(v) if v else None
+    return {"calls": len(hit), "dur_median_ns": med(dur), "dur_mean_ns": avg(dur), "spacing_median_ns": med(sp),
+            "spacing_mean_ns": avg(sp), "gap_median_ns": med(gap), "pairs": len(nxt)}
+
+
 def main():
     args = parse()
+    if args.trace_summary:
+        print(json.dumps(trace_summary(args.trace_summary, args.trace_kernel)))
+        return
     if args.steps < 1 or args.warmup < 0:
         print(f"bench.py needs --steps >= 1 and --warmup >= 0 (got {args.steps}, {args.warmup})", file=sys.stderr)
         sys.exit(2)
@@ -855,121 +1031,86 @@ def main():
     from stblarge_amd import _lib
 
     _lib.load()  # fails loudly when the library was not built
-
-    head = gemv_workload(torch, "fp4", 2048, 7168, 1, args.steps, args.warmup, use_graph=not args.no_graph)
-    head_timing = dict(LAST_TIMING) if not args.no_graph else {"samples": 1, "events": True}
-    print(f"# {head['workload']}: {head['ms_per_step'] * 1e3:.3f} us/step, {head['GB_s']:.0f} GB/s", file=sys.stderr,
-          flush=True)
+    K, W, graph = args.steps, args.warmup, not args.no_graph
     extra = {}
+
+    def report(r):
+        extra[r["workload"]] = r
+        print(stderr_text(r), file=sys.stderr, flush=True)
+
+    head = gemv_workload(torch, "fp4", 2048, 7168, 1, K, W, use_graph=graph, isolated=64)
+    head_timing = dict(LAST_TIMING) if graph else {"samples": 1, "events": True}
+    print(stderr_text(head), file=sys.stderr, flush=True)
     if args.only in ("all", "gemv"):
         for fmt, rows, k, m in (("fp4", 7168, 2048, 1), ("fp8", 2048, 7168, 1), ("fp8", 7168, 2048, 1),
                                 ("fp4", 2048, 7168, 4), ("fp8", 2048, 7168, 4)):
-            r = gemv_workload(torch, fmt, rows, k, m, args.steps, args.warmup)
-            extra[r["workload"]] = r
-            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
-                  flush=True)
+            report(gemv_workload(torch, fmt, rows, k, m, K, W, use_graph=graph))
     if args.only in ("all", "gemv", "batch"):
         for fmt, rows, k, nb in (("fp4", 7168, 2048, 16), ("fp4", 2048, 7168, 16), ("fp8", 7168, 2048, 16),
                                  ("fp8", 2048, 7168, 16), ("fp4", 7168, 2048, 64), ("fp4", 2048, 7168, 64),
                                  ("fp8", 7168, 2048, 64)):
-            r = gemv_batch_workload(torch, fmt, rows, k, args.steps, args.warmup, nb=nb, use_graph=not args.no_graph)
-            extra[r["workload"]] = r
-            print(f"# {r['workload']}: {r['ms_per_launch'] * 1e3:.2f} us/launch of {nb}, {r['GB_s']:.0f} GB/s "
-                  f"({100 * r['frac_hbm_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
+            report(gemv_batch_workload(torch, fmt, rows, k, K, W, nb=nb, use_graph=graph))
     if args.only in ("all", "ffn"):
         from stblarge_amd import ops
 
         for fmt in (ops.FP4, ops.FP8):
-            r = ffn_workload(torch, fmt, max(200, args.steps // 4), args.warmup, use_graph=not args.no_graph)
-            extra[r["workload"]] = r
-            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
-                  flush=True)
+            report(ffn_workload(torch, fmt, K, W, use_graph=graph))
     if args.only in ("all", "gemm"):
         from stblarge_amd import ops
 
         for fmt, pq, n, k in [(ops.FP4, True, 2048, 7168), (ops.FP8, True, 2048, 7168), (ops.FP4, False, 2048, 7168),
                               (ops.FP8, False, 2048, 7168), (ops.FP4, True, 7168, 2048)]:
-            r = gemm_workload(torch, fmt, max(200, args.steps // 4), args.warmup, n=n, k=k, prequant=pq,
-                              use_graph=not args.no_graph)
-            extra[r["workload"]] = r
-            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s, "
-                  f"{r['TFLOP_s']:.0f} TFLOP/s ({100 * r['frac_mfma_peak']:.1f}% MFMA)", file=sys.stderr, flush=True)
+            report(gemm_workload(torch, fmt, K, W, n=n, k=k, prequant=pq, use_graph=graph))
     if args.only in ("all", "refabi"):
         for kind, rows, k, grp in (("mxfp4", 2304, 5120, 0), ("mxfp4", 5120, 2304, 0), ("fp8", 2304, 5120, 0),
                                    ("fp8", 5120, 2304, 0), ("bf16", 4096, 5120, 0), ("fp8", 32768, 1280, 0),
                                    ("fp8", 5120, 8192, 0), ("fp8", 1280, 5120, 0), ("fp8", 512, 5120, 0),
                                    ("bf16", 8192, 4096, 1024), ("f32", 256, 5120, 0)):
-            r = compat_gemv_workload(torch, kind, rows, k, args.steps, args.warmup, grp)
-            extra[r["workload"]] = r
-            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
-                  flush=True)
+            report(compat_gemv_workload(torch, kind, rows, k, K, W, grp))
         # the engine's expert batches at V4.1 shapes, top-6: 12 gate/up matrices, then 6 down
         for rows, k, n in ((2304, 5120, 12), (5120, 2304, 6)):
-            r = compat_batch_workload(torch, rows, k, n, max(200, args.steps // 4), args.warmup)
-            extra[r["workload"]] = r
-            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.2f} us/step, {r['GB_s']:.0f} GB/s", file=sys.stderr,
-                  flush=True)
-        r = engine_abi_moe_workload(torch, max(200, args.steps // 4), args.warmup)
-        extra[r["workload"]] = r
-        print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.2f} us/step ({r['launches_per_step']} launches), "
-              f"{r['GB_s']:.0f} GB/s", file=sys.stderr, flush=True)
-    if args.only in ("all", "refabi"):
+            report(compat_batch_workload(torch, rows, k, n, K, W))
+        report(engine_abi_moe_workload(torch, K, W))
         # stbl/bench_gemv.py's own method and rows (:95-107): cache-resident weights, eager launches
         for kind, rows, k, grp in (("mxfp4", 2304, 5120, 0), ("mxfp4", 5120, 2304, 0), ("fp8", 2304, 5120, 0),
                                    ("fp8", 5120, 2304, 0), ("bf16", 4096, 5120, 0), ("bf16", 8192, 4096, 1024),
                                    ("fp8", 32768, 1280, 0), ("fp8", 5120, 8192, 0), ("fp8", 1280, 5120, 0),
                                    ("fp8", 512, 5120, 0), ("copy", 0, 0, 0)):
-            r = ref_method_workload(torch, kind, rows, k, grp)
-            extra[r["workload"]] = r
-            print(f"# {r['workload']}: {r['us']:.2f} us, {r['GB_s']:.1f} GB/s", file=sys.stderr, flush=True)
+            report(ref_method_workload(torch, kind, rows, k, grp))
     if args.only in ("all", "moe", "moeallhit"):
         for t, v41, f8s in ((1, False, False), (4, False, False), (1, False, True), (4, False, True), (1, True, False),
                             (4, True, False)):
-            r = moe_allhit_workload(torch, t, max(100, args.steps // 10), 32, v41=v41, use_graph=not args.no_graph,
-                                    fp8_shared=f8s)
-            extra[r["workload"]] = r
-            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s, "
-                  f"{r['GB_s']:.0f} GB/s", file=sys.stderr, flush=True)
+            report(moe_allhit_workload(torch, t, K, W, v41=v41, use_graph=graph, fp8_shared=f8s))
         for t in ((1, 4) if args.only != "moeallhit" else ()):
-            r = moe_workload(torch, t, args.moe_steps, args.moe_warmup)
-            extra[r["workload"]] = r
-            print(f"# {r['workload']}: {r['ms_per_step']:.3f} ms/step, {r['tokens_per_s']:.0f} tok/s, hit rate "
-                  f"{r['hit_rate']:.3f}, {r['misses_per_token']:.2f} misses/token, refill {r['refill_GB_s']:.1f} GB/s",
-                  file=sys.stderr, flush=True)
+            report(moe_workload(torch, t, args.moe_steps, args.moe_warmup))
     if args.only in ("all", "file"):
         for mode, per, readers in (("direct", 1, 8), ("direct", 6, 8), ("direct", 1, 4), ("direct", 1, 16),
                                    ("cold", 1, 8), ("cold", 6, 8), ("warm", 1, 8), ("warm", 6, 8)):
-            r = file_tier_workload(torch, mode, readers, per_lookup=per, lookups=30 if per == 1 else 6)
-            extra[r["workload"]] = r
-            print(f"# {r['workload']}: {r['ms_per_lookup_median']:.2f} ms/lookup (p90 {r['ms_per_lookup_p90']:.2f}), "
-                  f"{r['ms_per_expert']:.2f} ms/expert, {r['GB_s']:.2f} GB/s, reading {100 * r['read_share']:.0f}%",
-                  file=sys.stderr, flush=True)
+            report(file_tier_workload(torch, mode, readers, per_lookup=per, lookups=30 if per == 1 else 6))
     if args.only in ("all", "filestack"):
         for q in (None, 0.0, 0.5, 1.0):
-            r = file_stack_workload(torch, q)
-            extra[r["workload"]] = r
-            print(f"# {r['workload']}: {r['ms_per_token']:.1f} ms/token, hit rate {r['hit_rate']:.2f}, demand reads "
-                  f"{r['demand_GB_read']:.2f} GB, prefetch {r['prefetch']}", file=sys.stderr, flush=True)
+            report(file_stack_workload(torch, q))
     if args.eager:
-        r = gemv_workload(torch, "fp4", 2048, 7168, 1, args.steps, args.warmup, use_graph=False)
-        extra["fp4_gemv_2048x7168_m1_eager"] = r
-        print(f"# eager launches: {r['ms_per_step'] * 1e3:.3f} us/step", file=sys.stderr, flush=True)
+        r = gemv_workload(torch, "fp4", 2048, 7168, 1, K, W, use_graph=False)
+        r["workload"] += "_eager"
+        report(r)
     if args.only in ("all", "fp4", "gemv", "batch", "ffn", "floor"):
         # bare-read floors at the single-launch rows' byte counts: FP4 / FP8 GEMV, FP4 / FP8 expert
         # FFN, 16 FP4 / FP8 GEMVs per launch, 64 FP4 / FP8 GEMVs per launch
         floors = {}
         for nbytes in (7817216, 14702080, 23425024, 44079616, 125075456, 235233280, 500301824, 940933120):
-            r = read_floor_workload(torch, nbytes, args.steps, args.warmup)
+            r = read_floor_workload(torch, nbytes, K, W)
             floors[nbytes] = r
-            extra[r["workload"]] = r
-            print(f"# {r['workload']}: {r['ms_per_step'] * 1e3:.3f} us/step, {r['GB_s']:.0f} GB/s "
-                  f"({100 * r['frac_hbm_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
+            report(r)
         for row in [head] + list(extra.values()):
             if "alg_bytes" in row and not row["workload"].startswith("read_floor"):
                 attach_floor(row, floors)
         if "frac_of_read_floor" in head:
             print(f"# headline: {100 * head['frac_of_read_floor']:.1f}% of the bare read of its bytes",
                   file=sys.stderr, flush=True)
+    if "isolated_launch_us" in head_timing:
+        print(f"# headline launch alone between stamps: {head_timing['isolated_launch_us']:.2f} us (median of "
+              f"{head_timing['isolated_launches']})", file=sys.stderr, flush=True)
     if args.copy_calib:
         a = torch.empty(64 << 20, dtype=torch.uint8, device="cuda:0")
         b = torch.empty_like(a)
@@ -980,32 +1121,17 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baseline(args.cpu_seconds)
         extra["cpu_scalar_oracle"] = cpu_scalar_oracle(min(args.cpu_seconds, 5.0))
-        print(f"# cpu baseline: {cpu['value']:.2f} GB/s ({cpu['sample']}); scalar oracle "
-              f"{extra['cpu_scalar_oracle']['GB_s']:.2f} GB/s", file=sys.stderr, flush=True)
-    gbs = head["GB_s"]
-    line = {
-        "metric": METRIC,
-        "value": round(gbs, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": head["steps"],
-        "warmup": args.warmup,
-        "ms_per_step": head["ms_per_step"],
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "e2m1 weights x bf16 activations, f32 accumulate",
-        "data": "synthetic (seeded N(0,0.02) weights quantized on the GPU, N(0,1) bf16 x)",
-        "config": {"workload": head["workload"], "rows": 2048, "k": 7168, "m": 1,
-                   "weight_copies": head["weight_copies"], "rotation_MB": round(head["weight_copies"] * 7.8, 1)},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
-                     "frac_of_read_floor": head.get("frac_of_read_floor")},
-        "cpu_baseline": cpu,
-        "timing": head_timing,
-        "extra": extra,
-    }
-    print(json.dumps(line), flush=True)
+        print(f"# cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads; scalar oracle "
+              f"{extra['cpu_scalar_oracle']['GB_s']:.2f} GB/s on 1", file=sys.stderr, flush=True)
+    if args.rows_out:
+        with open(args.rows_out, "w") as f:
+            json.dump({"head": head, "timing": head_timing, "cpu_baseline": cpu, "rows": extra}, f, indent=1)
+    line = make_line(head, extra, cpu, head_timing, W, traffic=measured_traffic(), profiled=profiled_headline())
+    text = json.dumps(line, separators=(",", ":"))
+    if len(text) > LINE_MAX_BYTES:  # keep the line whole for readers that keep only a tail of the output
+        line["extra"] = {}
+        text = json.dumps(line, separators=(",", ":"))
+    print(text, flush=True)
 
 
 if __name__ == "__main__":

@@ -72,3 +72,29 @@ def test_bench_line_reports_the_requested_steps(gpu):
     assert d["timing"]["steps_per_sample"] == 20 and d["timing"]["samples"] >= 10
     assert abs(d["value"] - 7817216 / (d["ms_per_step"] * 1e-3) / 1e9) < 0.01 * d["value"]
     assert d["roofline"]["achieved"] == d["value"] and 0 < d["roofline"]["frac"] < 1
+    # the headline launch alone between stamps takes at least a bare launch and at most a few steps
+    assert d["timing"]["isolated_launches"] == 64
+    assert 0.5 * d["ms_per_step"] * 1e3 < d["roofline"]["isolated_launch_us"] < 10 * d["ms_per_step"] * 1e3
+
+
+@pytest.mark.timeout(900)
+def test_bench_driver_form_prints_one_whole_line(gpu):
+    # exactly the driver's command: every row, the CPU baseline; stdout is one JSON line of at most
+    # 4 KB carrying the roofline, the CPU baseline and the target shape's rows, and stdout + stderr
+    # stay well inside the tail the driver keeps
+    import json
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "1", "--steps", "20", "--warmup", "5"],
+                       capture_output=True, text=True, timeout=850)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [ln for ln in r.stdout.splitlines() if ln.strip()]
+    assert len(lines) == 1 and len(lines[0]) <= bench.LINE_MAX_BYTES, [len(x) for x in lines]
+    assert len(r.stdout) + len(r.stderr) < 12000, (len(r.stdout), len(r.stderr))
+    d = json.loads(lines[0])
+    assert d["steps"] == 20 and d["warmup"] == 5 and d["roofline"]["bound"] == "hbm"
+    assert d["cpu_baseline"]["value"] > 0 and d["cpu_baseline"]["cores"] >= 1
+    assert {"fp4", "fp8"} <= set(d["target_7168x2048"]) and len(d["extra"]) >= 20
