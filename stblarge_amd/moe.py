@@ -224,7 +224,17 @@ class MoELayer:
                     after_reads()
                 return ops.moe_experts(x, slots, pick, w, self.fmt, self.dim, self.inter, **kw)
             if any(ready):
-                ops.moe_experts(x, slots, pick, w, self.fmt, self.dim, self.inter, slot_ready=ready, phase=1, **kw)
+                try:
+                    ops.moe_experts(x, slots, pick, w, self.fmt, self.dim, self.inter, slot_ready=ready, phase=1,
+                                    **kw)
+                except BaseException:
+                    # end the open lookup (its reads and waits) so the cache takes the next one; the
+                    # phase-1 error is the one reported
+                    try:
+                        self.cache.lookup_end()
+                    except Exception:
+                        pass
+                    raise
             self.cache.lookup_end()
             if after_reads:
                 after_reads()

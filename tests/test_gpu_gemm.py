@@ -151,3 +151,30 @@ def test_gemm_deterministic_and_work_reuse(gpu):
         else:
             first[(m, n, k)] = y
             assert rel_err(y, _oracle_gemm(x, oracle.dequant_fp4(codes, scales), 128)) <= 1e-3
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("block", [32, 128])
+@pytest.mark.parametrize("m,n,k,shift", [(16, 7168, 2048, False), (22, 7168, 2048, False), (40, 7168, 2048, False),
+                                         (40, 2048, 7168, False), (64, 7168, 2048, True)])
+def test_gemm_tile_plans(gpu, fmt, block, m, n, k, shift):
+    # each tile plan of the GEMM against the oracle: 64 x 32 tiles in one slice (m <= 32 at N >= 6144,
+    # also the 22-row tail of a 150-row call), one-launch 32 x 64 tiles with a partial second row
+    # group (40 rows at 7168x2048), one-launch 16 x 32 tiles with a partial third group (40 rows at
+    # 2048x7168), and two 32-row groups of 64-column tiles when the activation scales are not
+    # 16-byte aligned (the one-launch plans load them 16 bytes at a time)
+    w = data.weight(n, k, seed=n + k + m)
+    q, deq = (oracle.quant_fp4, oracle.dequant_fp4) if fmt == 0 else (oracle.quant_fp8_b128, oracle.dequant_fp8_b128)
+    codes, scales = q(w.numpy())
+    x = data.activation(m, k, seed=m + 7)
+    want = _oracle_gemm(x, deq(codes, scales), block)
+    dc, ds = torch.from_numpy(codes).to(gpu), torch.from_numpy(scales).to(gpu)
+    aq, a_s = ops.act_quant_e4m3(x.to(gpu), block)
+    if shift:
+        buf = torch.zeros(a_s.numel() + 16, dtype=a_s.dtype, device=gpu)
+        a_s2 = buf[1:1 + a_s.numel()].view(a_s.shape)
+        a_s2.copy_(a_s)
+        a_s = a_s2
+    y32 = np_(ops.gemm_q(dc, ds, aq, a_s, fmt, block, out_f32=True))
+    y16 = np_(ops.gemm_q(dc, ds, aq, a_s, fmt, block))
+    _check(y32, y16, want)

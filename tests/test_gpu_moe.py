@@ -394,6 +394,38 @@ def test_cache_refill_failure_leaves_slot_unmapped(gpu):
     cache.close()
 
 
+def test_moe_layer_phase1_failure_ends_the_lookup(gpu, monkeypatch):
+    # a step whose first phase (the resident experts) raises must still end the cache's open
+    # lookup: the error reaches the caller and the next step's lookup and result are normal
+    dim, inter, n, topk, slots = 256, 128, 8, 2, 4
+    fmt = ops.FP4
+    slot_bytes, _ = ops.expert_layout(fmt, dim, inter)
+    pool = torch.empty(n * slot_bytes, dtype=torch.uint8, pin_memory=True)
+    packed = []
+    for e in range(n):
+        s, parts = make_expert(fmt, dim, inter, seed=500 + 3 * e, gpu=gpu)
+        pool[e * slot_bytes:(e + 1) * slot_bytes].copy_(s.cpu())
+        packed.append(np.concatenate([p.ravel() for p in parts]))
+    layer = MoELayer(fmt, dim, inter, pool, n, topk, slots)
+    x = data.activation(1, dim, seed=5).to(gpu)
+    layer.forward(x, None, route=([[0, 1]], [[0.5, 0.5]]))  # experts 0 and 1 resident
+    real = ops.moe_experts
+
+    def failing(*a, phase=0, **kw):
+        if phase == 1:
+            raise RuntimeError("planted phase-1 failure")
+        return real(*a, phase=phase, **kw)
+
+    monkeypatch.setattr(ops, "moe_experts", failing)
+    with pytest.raises(RuntimeError, match="planted"):
+        layer.forward(x, None, route=([[0, 2]], [[0.5, 0.5]]))  # 0 resident, 2 refilled: two phases
+    monkeypatch.setattr(ops, "moe_experts", real)
+    y = np_(layer.forward(x, None, route=([[3, 0]], [[0.75, 0.25]])))
+    want = oracle.moe_fp4([[packed[3], packed[0]]], [[0.75, 0.25]], None, dim, inter, x.float().cpu().numpy())
+    assert bf16_ulps(y, want).max() <= 1
+    layer.close()
+
+
 def test_moe_layer_end_to_end(gpu):
     dim, inter, n, topk, slots = 256, 128, 24, 3, 12  # <= 12 distinct experts per 4-token step
     fmt = ops.FP4
