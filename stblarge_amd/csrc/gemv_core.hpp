@@ -157,37 +157,6 @@ __device__ __forceinline__ void chunk_dot(float (&s)[M], const u32x4 w, const fl
     }
 }
 
-// In-register act_quant(x, 32, "ue8m0", inplace=True) of the lane's chunk (ref/kernel.py:35-45; the
-// reference engine's stbl_act_quant_fp8, stbl/kernels.cu:54-63): per 32 values s = 2^ceil(log2(
-// max(amax, 1e-4) / 448)), x = bf16(e4m3(clamp(x / s, +-448)) * s). A 16-element chunk shares its
-// 32-block with the neighbouring lane (lanes 2b and 2b+1), whose amax comes over by DPP.
-template <int M, int CH>
-__device__ __forceinline__ void act_quant_chunk(float (&xf)[M][CH]) {
-    static_assert(CH == 32 || CH == 16, "chunk must be one or half an act_quant block");
-#pragma unroll
-    for (int t = 0; t < M; t++) {
-        float a = 0.f;
-#pragma unroll
-        for (int i = 0; i < CH; i++) a = fmaxf(a, fabsf(xf[t][i]));
-        if constexpr (CH == 16)
-            a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0xB1, 0xF, 0xF, false)));
-        const float s = pow2_ceil(fmaxf(a, 1e-4f) * (1.0f / 448.0f));
-        // 1/s is a power of two too (s lies in [2^-22, 2^120]), so x * inv is x / s exactly; the
-        // hardware conversion rounds to nearest even like the reference's cast (it equals the
-        // software encoder f32_to_e4m3 on every bf16 input, and x / s of a bf16 x is a bf16 value);
-        // e4m3(q) * s is exact and bf16-representable, so bf16(e4m3(q) * s) needs no rounding step.
-        const float inv = __uint_as_float((254u - ((__float_as_uint(s) >> 23) & 0xffu)) << 23);
-#pragma unroll
-        for (int i = 0; i < CH; i += 2) {
-            const float q0 = fminf(fmaxf(xf[t][i] * inv, -448.f), 448.f);
-            const float q1 = fminf(fmaxf(xf[t][i + 1] * inv, -448.f), 448.f);
-            const f32x2 d = e4m3x2((uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0, false), false);
-            xf[t][i] = d.x * s;
-            xf[t][i + 1] = d.y * s;
-        }
-    }
-}
-
 // ---- packed-bf16 path (v2 formats): weights converted to bf16 pairs, v_dot2_f32_bf16 ---------------
 //
 // With bf16 activations the lane keeps its x chunk as packed bf16 words (word i = elements 2i, 2i+1)
@@ -213,20 +182,41 @@ __device__ __forceinline__ void load_x_packed(uint32_t (&xw)[M][CH / 2], const u
     }
 }
 
-// act_quant_chunk on packed words: the quantized values are bf16 values, so they pack back exactly.
+// In-register act_quant(x, 32, "ue8m0", inplace=True) of the lane's chunk of packed bf16 words
+// (word i = elements 2i, 2i + 1; ref/kernel.py:35-45, the reference engine's stbl_act_quant_fp8,
+// stbl/kernels.cu:54-63): per 32 values s = 2^ceil(log2(max(amax, 1e-4) / 448)), x = bf16(e4m3(
+// clamp(x / s, +-448)) * s). A 16-element chunk shares its 32-block with the neighbouring lane
+// (lanes 2b and 2b+1), whose amax comes over by DPP. 1/s is a power of two too (s lies in [2^-22,
+// 2^120]), so x * inv is x / s exactly; v_cvt_pk_fp8_f32 rounds to nearest even like the
+// reference's cast (it equals the software encoder f32_to_e4m3 on every bf16 input, and x / s of a
+// bf16 x is a bf16 value). bf16(e4m3(q) * s) of each pair is one scaled conversion
+// (v_cvt_scalef32_pk_bf16_fp8 multiplies by the power of two whose exponent field its scale operand
+// carries: s itself; e4m3 * s is a bf16 value, so the product is exact), so the words are rebuilt
+// without widening, multiplying and repacking.
 template <int M, int CH>
 __device__ __forceinline__ void act_quant_packed(uint32_t (&xw)[M][CH / 2]) {
-    float xf[M][CH];
+    static_assert(CH == 32 || CH == 16, "chunk must be one or half an act_quant block");
 #pragma unroll
-    for (int t = 0; t < M; t++)
+    for (int t = 0; t < M; t++) {
+        float a = 0.f;
 #pragma unroll
-        for (int i = 0; i < CH / 2; i++) xf[t][2 * i] = bf16_lo(xw[t][i]), xf[t][2 * i + 1] = bf16_hi(xw[t][i]);
-    act_quant_chunk<M, CH>(xf);
+        for (int i = 0; i < CH / 2; i++) a = fmaxf(fmaxf(a, fabsf(bf16_lo(xw[t][i]))), fabsf(bf16_hi(xw[t][i])));
+        if constexpr (CH == 16)
+            a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0xB1, 0xF, 0xF, false)));
+        const float s = pow2_ceil(fmaxf(a, 1e-4f) * (1.0f / 448.0f));
+        const float inv = __uint_as_float((254u - ((__float_as_uint(s) >> 23) & 0xffu)) << 23);
 #pragma unroll
-    for (int t = 0; t < M; t++)
-#pragma unroll
-        for (int i = 0; i < CH / 2; i++)
-            xw[t][i] = (__float_as_uint(xf[t][2 * i]) >> 16) | (__float_as_uint(xf[t][2 * i + 1]) & 0xffff0000u);
+        for (int i = 0; i < CH / 2; i += 2) {
+            const float q0 = fminf(fmaxf(bf16_lo(xw[t][i]) * inv, -448.f), 448.f);
+            const float q1 = fminf(fmaxf(bf16_hi(xw[t][i]) * inv, -448.f), 448.f);
+            const float q2 = fminf(fmaxf(bf16_lo(xw[t][i + 1]) * inv, -448.f), 448.f);
+            const float q3 = fminf(fmaxf(bf16_hi(xw[t][i + 1]) * inv, -448.f), 448.f);
+            int p = __builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0, false);
+            p = __builtin_amdgcn_cvt_pk_fp8_f32(q2, q3, p, true);
+            xw[t][i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)p, s, false));
+            xw[t][i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)p, s, true));
+        }
+    }
 }
 
 __device__ __forceinline__ float dot2(bf16x2 w, uint32_t x, float acc) {

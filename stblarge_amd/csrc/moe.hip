@@ -18,6 +18,7 @@
 // lane's own chunk of the activation, so it costs no launch and no memory traffic.
 // The router is k_route: sigmoid scores, top-k by score + bias with ties to the lower id, weights
 // renormalized in top-k order (stbl/model.cu:444-451, :528-530 with sigmoid for sqrt-softplus).
+#include <algorithm>
 #include <mutex>
 
 #include "abi_util.hpp"
@@ -33,6 +34,7 @@ constexpr int kMoeMaxPick = 17;  // top-k + shared
 
 struct MoeJob {
     const uint8_t *slot;
+    int fmt;                   // the slot's format (ExpertFmt); read by the mixed-format kernels
     int m;                     // tokens of this job, 1..4
     int tok[kMoeMaxTok];       // token rows of x
     int pair[kMoeMaxTok];      // rows of the intermediate / output buffers
@@ -126,12 +128,13 @@ __device__ __forceinline__ bool wave_total(float (&vals)[N], float (*red)[N], fl
 // DW (FP4, scale rows a multiple of 4 bytes): the scale bytes of the 2R rows come as dwords, lane j
 // loading dword j % 16 of the wave's segment of row j / 16 (gate rows, then up rows), and each lane
 // takes its byte with ds_bpermute; otherwise one byte load per row per lane.
+// The body runs in any workgroup of at least ceil(dim / CH / 64) waves: waves past the job's K (in
+// the mixed-format launches, whose workgroups are sized for the format with the most waves) load
+// nothing and add zeros.
 template <WFmt F, int M, int R, bool DW>
-__global__ __launch_bounds__(512) void k_moe_gateup(MoeJobs jobs, ExpertLayout L, const uint16_t *__restrict__ x,
-                                                    uint16_t *__restrict__ h, int dim, int inter, float limit,
-                                                    int official) {
+__device__ __forceinline__ void gateup_job(const MoeJob &J, const ExpertLayout &L, const uint16_t *__restrict__ x,
+                                           uint16_t *__restrict__ h, int dim, int inter, float limit, int official) {
     constexpr int CH = WTraits<F>::CH;
-    const MoeJob &J = jobs.j[blockIdx.y];
     const SlotMat<F> G(J.slot, L, 0, dim, inter), U(J.slot, L, 1, dim, inter);
     const int lane = threadIdx.x & 63, c = (threadIdx.x >> 6) * 64 + lane, nch = dim / CH;
     const bool active = c < nch;
@@ -143,61 +146,64 @@ __global__ __launch_bounds__(512) void k_moe_gateup(MoeJobs jobs, ExpertLayout L
     const int t_out = min((int)(threadIdx.x >> 1) / R, M - 1);
     const int pair_out = J.pair[t_out];
     const float w_out = J.w[t_out];
-
-    uint32_t xw[M][CH / 2];
-#pragma unroll
-    for (int t = 0; t < M; t++) {
-        uint32_t tmp[1][CH / 2];
-        load_x_packed<1, CH>(tmp, x + (size_t)J.tok[t < m ? t : 0] * dim, dim, cc * CH);
-#pragma unroll
-        for (int i = 0; i < CH / 2; i++) xw[t][i] = tmp[0][i];
-    }
-    u32x4 wg[R], wu[R];
-    uint32_t sg[R], su[R];
-    uint32_t sdw[(2 * R + 3) / 4];
-    if constexpr (DW) {
-        // virtual rows 0..R-1 gate, R..2R-1 up; rows and dwords clamped into the matrices
-        const int wave = threadIdx.x >> 6, dwi = min(wave * 16 + (lane & 15), (nch >> 2) - 1);
-#pragma unroll
-        for (int q = 0; q < (2 * R + 3) / 4; q++) {
-            const int vr = min(4 * q + (lane >> 4), 2 * R - 1);
-            const size_t row = (size_t)min(row0 + (vr < R ? vr : vr - R), inter - 1);
-            sdw[q] = vr < R ? G.load_scale_dword(row, dwi) : U.load_scale_dword(row, dwi);
-        }
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const size_t row = (size_t)min(row0 + r, inter - 1);
-            wg[r] = G.load_codes(row, cc);
-            wu[r] = U.load_codes(row, cc);
-        }
-    } else {
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const size_t row = (size_t)min(row0 + r, inter - 1);
-            G.load(row, cc, wg[r], sg[r]);
-            U.load(row, cc, wu[r], su[r]);
-        }
-    }
-    float lg = 1.f, lu = 1.f;
-    if constexpr (!WTraits<F>::fp4) lg = G.block_scale(row0, cc), lu = U.block_scale(row0, cc);
-    if (official) act_quant_packed<M, CH>(xw);
-    if constexpr (DW) {
-#pragma unroll
-        for (int r = 0; r < R; r++) sg[r] = dw_scale_byte(sdw, r, lane), su[r] = dw_scale_byte(sdw, R + r, lane);
-    }
-
     __shared__ float red[kMaxWaves][2 * M * R];
     float tot[2 * M * R];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        float sgv[M], suv[M];
-        chunk_dot_packed<F, M, CH>(sgv, wg[r], xw, conv_scale<F>(sg[r], lg));
-        chunk_dot_packed<F, M, CH>(suv, wu[r], xw, conv_scale<F>(su[r], lu));
-        const float a = post_scale<F>(lg), b = post_scale<F>(lu);
+    for (int i = 0; i < 2 * M * R; i++) tot[i] = 0.f;
+    if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * 64 < nch) {
+        uint32_t xw[M][CH / 2];
 #pragma unroll
         for (int t = 0; t < M; t++) {
-            tot[(t * R + r) * 2] = active ? sgv[t] * a : 0.f;
-            tot[(t * R + r) * 2 + 1] = active ? suv[t] * b : 0.f;
+            uint32_t tmp[1][CH / 2];
+            load_x_packed<1, CH>(tmp, x + (size_t)J.tok[t < m ? t : 0] * dim, dim, cc * CH);
+#pragma unroll
+            for (int i = 0; i < CH / 2; i++) xw[t][i] = tmp[0][i];
+        }
+        u32x4 wg[R], wu[R];
+        uint32_t sg[R], su[R];
+        uint32_t sdw[(2 * R + 3) / 4];
+        if constexpr (DW) {
+            // virtual rows 0..R-1 gate, R..2R-1 up; rows and dwords clamped into the matrices
+            const int wave = threadIdx.x >> 6, dwi = min(wave * 16 + (lane & 15), (nch >> 2) - 1);
+#pragma unroll
+            for (int q = 0; q < (2 * R + 3) / 4; q++) {
+                const int vr = min(4 * q + (lane >> 4), 2 * R - 1);
+                const size_t row = (size_t)min(row0 + (vr < R ? vr : vr - R), inter - 1);
+                sdw[q] = vr < R ? G.load_scale_dword(row, dwi) : U.load_scale_dword(row, dwi);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const size_t row = (size_t)min(row0 + r, inter - 1);
+                wg[r] = G.load_codes(row, cc);
+                wu[r] = U.load_codes(row, cc);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const size_t row = (size_t)min(row0 + r, inter - 1);
+                G.load(row, cc, wg[r], sg[r]);
+                U.load(row, cc, wu[r], su[r]);
+            }
+        }
+        float lg = 1.f, lu = 1.f;
+        if constexpr (!WTraits<F>::fp4) lg = G.block_scale(row0, cc), lu = U.block_scale(row0, cc);
+        if (official) act_quant_packed<M, CH>(xw);
+        if constexpr (DW) {
+#pragma unroll
+            for (int r = 0; r < R; r++) sg[r] = dw_scale_byte(sdw, r, lane), su[r] = dw_scale_byte(sdw, R + r, lane);
+        }
+
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float sgv[M], suv[M];
+            chunk_dot_packed<F, M, CH>(sgv, wg[r], xw, conv_scale<F>(sg[r], lg));
+            chunk_dot_packed<F, M, CH>(suv, wu[r], xw, conv_scale<F>(su[r], lu));
+            const float a = post_scale<F>(lg), b = post_scale<F>(lu);
+#pragma unroll
+            for (int t = 0; t < M; t++) {
+                tot[(t * R + r) * 2] = active ? sgv[t] * a : 0.f;
+                tot[(t * R + r) * 2 + 1] = active ? suv[t] * b : 0.f;
+            }
         }
     }
     // thread q = (t * R + r) * 2 + {0 gate, 1 up}; the even thread finishes the pair
@@ -215,62 +221,83 @@ __global__ __launch_bounds__(512) void k_moe_gateup(MoeJobs jobs, ExpertLayout L
     h[(size_t)pair_out * inter + row0 + r] = f32_to_bf16_bits(__fdiv_rn(gv, 1.f + expf(-gv)) * uv * w_out);
 }
 
+template <WFmt F, int M, int R, bool DW>
+__global__ __launch_bounds__(512) void k_moe_gateup(MoeJobs jobs, ExpertLayout L, const uint16_t *__restrict__ x,
+                                                    uint16_t *__restrict__ h, int dim, int inter, float limit,
+                                                    int official) {
+    gateup_job<F, M, R, DW>(jobs.j[blockIdx.y], L, x, h, dim, inter, limit, official);
+}
+
+// Jobs of two formats in one launch (the reference's FP4 routed experts next to its FP8 E8M0 shared
+// expert, stbl/model.cu:536-547): each workgroup takes its job's format (wave-uniform), so the
+// shared expert costs no launches of its own.
+template <WFmt FA, WFmt FB, int M, int R, bool DWA, bool DWB>
+__global__ __launch_bounds__(512) void k_moe_gateup_mix(MoeJobs jobs, ExpertLayout LA, ExpertLayout LB,
+                                                        const uint16_t *__restrict__ x, uint16_t *__restrict__ h,
+                                                        int dim, int inter, float limit, int official, int fmt_a) {
+    const MoeJob &J = jobs.j[blockIdx.y];
+    if (J.fmt == fmt_a) gateup_job<FA, M, R, DWA>(J, LA, x, h, dim, inter, limit, official);
+    else gateup_job<FB, M, R, DWB>(J, LB, x, h, dim, inter, limit, official);
+}
+
 // ---- down ------------------------------------------------------------------------------------------
 
 // Job blockIdx.y, rows [row0, row0 + R) of down. h bf16 [P][inter] -> o [P][dim] (bf16, or fp32
 // holding the unrounded sum when out_f32). DW as in k_moe_gateup.
 template <WFmt F, int M, int R, bool DW>
-__global__ __launch_bounds__(512) void k_moe_down(MoeJobs jobs, ExpertLayout L, const uint16_t *__restrict__ h,
-                                                  void *__restrict__ o, int dim, int inter, int official, int out_f32) {
+__device__ __forceinline__ void down_job(const MoeJob &J, const ExpertLayout &L, const uint16_t *__restrict__ h,
+                                         void *__restrict__ o, int dim, int inter, int official, int out_f32) {
     constexpr int CH = WTraits<F>::CH;
-    const MoeJob &J = jobs.j[blockIdx.y];
     const SlotMat<F> D(J.slot, L, 2, dim, inter);
     const int lane = threadIdx.x & 63, c = (threadIdx.x >> 6) * 64 + lane, nch = inter / CH;
     const bool active = c < nch;
     const int cc = active ? c : 0;
     const int row0 = blockIdx.x * R;
     const int m = J.m;
-    const int pair_out = J.pair[min((int)threadIdx.x / R, M - 1)];  // read early, as in k_moe_gateup
-
-    uint32_t xw[M][CH / 2];
-#pragma unroll
-    for (int t = 0; t < M; t++) {
-        uint32_t tmp[1][CH / 2];
-        load_x_packed<1, CH>(tmp, h + (size_t)J.pair[t < m ? t : 0] * inter, inter, cc * CH);
-#pragma unroll
-        for (int i = 0; i < CH / 2; i++) xw[t][i] = tmp[0][i];
-    }
-    u32x4 wd[R];
-    uint32_t sd[R];
-    uint32_t sdw[(R + 3) / 4];
-    if constexpr (DW) {
-        const int wave = threadIdx.x >> 6, dwi = min(wave * 16 + (lane & 15), (nch >> 2) - 1);
-#pragma unroll
-        for (int q = 0; q < (R + 3) / 4; q++)
-            sdw[q] = D.load_scale_dword((size_t)min(row0 + min(4 * q + (lane >> 4), R - 1), dim - 1), dwi);
-#pragma unroll
-        for (int r = 0; r < R; r++) wd[r] = D.load_codes((size_t)min(row0 + r, dim - 1), cc);
-    } else {
-#pragma unroll
-        for (int r = 0; r < R; r++) D.load((size_t)min(row0 + r, dim - 1), cc, wd[r], sd[r]);
-    }
-    float ld = 1.f;
-    if constexpr (!WTraits<F>::fp4) ld = D.block_scale(row0, cc);
-    if (official) act_quant_packed<M, CH>(xw);
-    if constexpr (DW) {
-#pragma unroll
-        for (int r = 0; r < R; r++) sd[r] = dw_scale_byte(sdw, r, lane);
-    }
-
+    const int pair_out = J.pair[min((int)threadIdx.x / R, M - 1)];  // read early, as in gateup_job
     __shared__ float red[kMaxWaves][M * R];
     float tot[M * R];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        float s[M];
-        chunk_dot_packed<F, M, CH>(s, wd[r], xw, conv_scale<F>(sd[r], ld));
-        const float a = post_scale<F>(ld);
+    for (int i = 0; i < M * R; i++) tot[i] = 0.f;
+    if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * 64 < nch) {
+        uint32_t xw[M][CH / 2];
 #pragma unroll
-        for (int t = 0; t < M; t++) tot[t * R + r] = active ? s[t] * a : 0.f;
+        for (int t = 0; t < M; t++) {
+            uint32_t tmp[1][CH / 2];
+            load_x_packed<1, CH>(tmp, h + (size_t)J.pair[t < m ? t : 0] * inter, inter, cc * CH);
+#pragma unroll
+            for (int i = 0; i < CH / 2; i++) xw[t][i] = tmp[0][i];
+        }
+        u32x4 wd[R];
+        uint32_t sd[R];
+        uint32_t sdw[(R + 3) / 4];
+        if constexpr (DW) {
+            const int wave = threadIdx.x >> 6, dwi = min(wave * 16 + (lane & 15), (nch >> 2) - 1);
+#pragma unroll
+            for (int q = 0; q < (R + 3) / 4; q++)
+                sdw[q] = D.load_scale_dword((size_t)min(row0 + min(4 * q + (lane >> 4), R - 1), dim - 1), dwi);
+#pragma unroll
+            for (int r = 0; r < R; r++) wd[r] = D.load_codes((size_t)min(row0 + r, dim - 1), cc);
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; r++) D.load((size_t)min(row0 + r, dim - 1), cc, wd[r], sd[r]);
+        }
+        float ld = 1.f;
+        if constexpr (!WTraits<F>::fp4) ld = D.block_scale(row0, cc);
+        if (official) act_quant_packed<M, CH>(xw);
+        if constexpr (DW) {
+#pragma unroll
+            for (int r = 0; r < R; r++) sd[r] = dw_scale_byte(sdw, r, lane);
+        }
+
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float s[M];
+            chunk_dot_packed<F, M, CH>(s, wd[r], xw, conv_scale<F>(sd[r], ld));
+            const float a = post_scale<F>(ld);
+#pragma unroll
+            for (int t = 0; t < M; t++) tot[t * R + r] = active ? s[t] * a : 0.f;
+        }
     }
     float v = 0.f;
     if (!wave_total<M * R>(tot, red, &v)) return;
@@ -279,6 +306,22 @@ __global__ __launch_bounds__(512) void k_moe_down(MoeJobs jobs, ExpertLayout L, 
     const size_t at = (size_t)pair_out * dim + row0 + r;
     if (out_f32) ((float *)o)[at] = v;
     else ((uint16_t *)o)[at] = f32_to_bf16_bits(v);
+}
+
+template <WFmt F, int M, int R, bool DW>
+__global__ __launch_bounds__(512) void k_moe_down(MoeJobs jobs, ExpertLayout L, const uint16_t *__restrict__ h,
+                                                  void *__restrict__ o, int dim, int inter, int official, int out_f32) {
+    down_job<F, M, R, DW>(jobs.j[blockIdx.y], L, h, o, dim, inter, official, out_f32);
+}
+
+// Down rows of jobs of two formats in one launch, as k_moe_gateup_mix.
+template <WFmt FA, WFmt FB, int M, int R, bool DWA, bool DWB>
+__global__ __launch_bounds__(512) void k_moe_down_mix(MoeJobs jobs, ExpertLayout LA, ExpertLayout LB,
+                                                      const uint16_t *__restrict__ h, void *__restrict__ o, int dim,
+                                                      int inter, int official, int out_f32, int fmt_a) {
+    const MoeJob &J = jobs.j[blockIdx.y];
+    if (J.fmt == fmt_a) down_job<FA, M, R, DWA>(J, LA, h, o, dim, inter, official, out_f32);
+    else down_job<FB, M, R, DWB>(J, LB, h, o, dim, inter, official, out_f32);
 }
 
 // ---- combine ------------------------------------------------------------------------------------
@@ -484,6 +527,100 @@ static hipError_t run_fmt(int fmt, const MoeJob *all, int njobs, int dim, int in
     return run_jobs<WFmt::FP8_E8M0>(all, njobs, L, x, h, o, dim, inter, limit, official, out_f32, st);
 }
 
+// Gate/up and down launches over jobs of two formats, FA (format fmt_a) and FB (each job's fmt
+// says which), with the same row tiles as the single-format launches (4 gate and 4 up rows, 8 down
+// rows, 4 with 4 tokens). A workgroup has as many waves as the format with the longer rows needs.
+template <WFmt FA, WFmt FB, int M>
+static hipError_t launch_mix(bool gateup, const MoeJobs &jobs, int n, int fmt_a, int fmt_b, const uint16_t *x,
+                             uint16_t *h, void *o, int dim, int inter, float limit, int official, int out_f32,
+                             hipStream_t st) {
+    const ExpertLayout LA = expert_layout(fmt_a, dim, inter), LB = expert_layout(fmt_b, dim, inter);
+    const int k = gateup ? dim : inter;
+    const int waves = std::max(ceil_div(k / WTraits<FA>::CH, 64), ceil_div(k / WTraits<FB>::CH, 64));
+    // FP4 tiles of 4+ rows whose scale rows are a multiple of 4 bytes fetch their scales as dwords
+    const bool dwa = WTraits<FA>::fp4 && (k / 32) % 4 == 0, dwb = WTraits<FB>::fp4 && (k / 32) % 4 == 0;
+    if (gateup) {
+        constexpr int R = 4;
+        const dim3 grid(ceil_div(inter, R), n), block(64 * waves);
+#define STBL_GU(DA, DB)                                                                                          \
+    hipLaunchKernelGGL((k_moe_gateup_mix<FA, FB, M, R, DA, DB>), grid, block, 0, st, jobs, LA, LB, x, h, dim, inter, \
+                       limit, official, fmt_a)
+        if (dwa && dwb) STBL_GU(WTraits<FA>::fp4, WTraits<FB>::fp4);
+        else if (dwa) STBL_GU(WTraits<FA>::fp4, false);
+        else if (dwb) STBL_GU(false, WTraits<FB>::fp4);
+        else STBL_GU(false, false);
+#undef STBL_GU
+    } else {
+        constexpr int R = M == 4 ? 4 : 8;
+        const dim3 grid(ceil_div(dim, R), n), block(64 * waves);
+#define STBL_DN(DA, DB)                                                                                             \
+    hipLaunchKernelGGL((k_moe_down_mix<FA, FB, M, R, DA, DB>), grid, block, 0, st, jobs, LA, LB, h, o, dim, inter, \
+                       official, out_f32, fmt_a)
+        if (dwa && dwb) STBL_DN(WTraits<FA>::fp4, WTraits<FB>::fp4);
+        else if (dwa) STBL_DN(WTraits<FA>::fp4, false);
+        else if (dwb) STBL_DN(false, WTraits<FB>::fp4);
+        else STBL_DN(false, false);
+#undef STBL_DN
+    }
+    return hipGetLastError();
+}
+
+// Runs jobs of formats fmt_a (FA) and fmt_b (FB) through gate/up and down as run_jobs does, a launch
+// holding both formats where its token class has both (the FB jobs first: their workgroups carry
+// more bytes, so they are dispatched before the others), else the single-format launches.
+template <WFmt FA, WFmt FB>
+static hipError_t run_jobs_mix(const MoeJob *all, int njobs, int fmt_a, int fmt_b, const uint16_t *x, uint16_t *h,
+                               void *o, int dim, int inter, float limit, int official, int out_f32, hipStream_t st) {
+    const ExpertLayout LA = expert_layout(fmt_a, dim, inter), LB = expert_layout(fmt_b, dim, inter);
+    for (int phase = 0; phase < 2; phase++) {
+        for (int mclass = 1; mclass <= 3; mclass++) {
+            MoeJobs batch;
+            int n = 0, na = 0, nb = 0;
+            auto flush = [&]() -> hipError_t {
+                if (n == 0) return hipSuccess;
+                hipError_t e;
+                const bool gu = phase == 0;
+                if (na > 0 && nb > 0) {
+                    e = mclass == 1 ? launch_mix<FA, FB, 1>(gu, batch, n, fmt_a, fmt_b, x, h, o, dim, inter, limit, official, out_f32, st)
+                        : mclass == 2 ? launch_mix<FA, FB, 2>(gu, batch, n, fmt_a, fmt_b, x, h, o, dim, inter, limit, official, out_f32, st)
+                                      : launch_mix<FA, FB, 4>(gu, batch, n, fmt_a, fmt_b, x, h, o, dim, inter, limit, official, out_f32, st);
+                } else if (na > 0) {
+                    e = gu ? (mclass == 1 ? launch_gateup<FA, 1>(batch, n, LA, x, h, dim, inter, limit, official, st)
+                              : mclass == 2 ? launch_gateup<FA, 2>(batch, n, LA, x, h, dim, inter, limit, official, st)
+                                            : launch_gateup<FA, 4>(batch, n, LA, x, h, dim, inter, limit, official, st))
+                           : (mclass == 1 ? launch_down<FA, 1>(batch, n, LA, h, o, dim, inter, official, out_f32, st)
+                              : mclass == 2 ? launch_down<FA, 2>(batch, n, LA, h, o, dim, inter, official, out_f32, st)
+                                            : launch_down<FA, 4>(batch, n, LA, h, o, dim, inter, official, out_f32, st));
+                } else {
+                    e = gu ? (mclass == 1 ? launch_gateup<FB, 1>(batch, n, LB, x, h, dim, inter, limit, official, st)
+                              : mclass == 2 ? launch_gateup<FB, 2>(batch, n, LB, x, h, dim, inter, limit, official, st)
+                                            : launch_gateup<FB, 4>(batch, n, LB, x, h, dim, inter, limit, official, st))
+                           : (mclass == 1 ? launch_down<FB, 1>(batch, n, LB, h, o, dim, inter, official, out_f32, st)
+                              : mclass == 2 ? launch_down<FB, 2>(batch, n, LB, h, o, dim, inter, official, out_f32, st)
+                                            : launch_down<FB, 4>(batch, n, LB, h, o, dim, inter, official, out_f32, st));
+                }
+                n = na = nb = 0;
+                return e;
+            };
+            for (int pass = 0; pass < 2; pass++) {  // the FB jobs, then the FA jobs
+                for (int j = 0; j < njobs; j++) {
+                    const int cls = all[j].m == 1 ? 1 : (all[j].m == 2 ? 2 : 3);
+                    if (cls != mclass || (all[j].fmt == fmt_a) != (pass == 1)) continue;
+                    batch.j[n++] = all[j];
+                    (pass == 1 ? na : nb)++;
+                    if (n == kMoeMaxJobs) {
+                        const hipError_t e = flush();
+                        if (e != hipSuccess) return e;
+                    }
+                }
+            }
+            const hipError_t e = flush();
+            if (e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
+}
+
 static bool fmt_ok(int fmt) { return fmt == EXPERT_FP4 || fmt == EXPERT_FP8 || fmt == EXPERT_FP8_E8M0; }
 
 static bool dims_ok(int fmt, int dim, int inter) {
@@ -574,9 +711,11 @@ static int moe_experts_impl(int fmt, void *y, const void *x, int t, int dim, int
                 table.pair[tt][p] = npairs;
                 if (run) {
                     if (!J || J->m == kMoeMaxTok) {
-                        J = s == shared && shared_fmt != fmt ? &sjobs[nsjobs++] : &jobs[njobs++];
+                        const bool other = s == shared && shared_fmt != fmt;
+                        J = other ? &sjobs[nsjobs++] : &jobs[njobs++];
                         *J = MoeJob{};
                         J->slot = (const uint8_t *)slots[s];
+                        J->fmt = other ? shared_fmt : fmt;
                     }
                     J->tok[J->m] = tt;
                     J->pair[J->m] = npairs;
@@ -588,9 +727,17 @@ static int moe_experts_impl(int fmt, void *y, const void *x, int t, int dim, int
     }
     uint16_t *h = (uint16_t *)work;
     uint16_t *o = h + (size_t)t * npick * inter;
-    hipError_t e = run_fmt(fmt, jobs, njobs, dim, inter, (const uint16_t *)x, h, o, limit, official, 0, st);
-    if (e == hipSuccess && nsjobs > 0)
-        e = run_fmt(shared_fmt, sjobs, nsjobs, dim, inter, (const uint16_t *)x, h, o, limit, official, 0, st);
+    hipError_t e;
+    if (nsjobs > 0 && fmt == EXPERT_FP4 && shared_fmt == EXPERT_FP8_E8M0) {
+        // the reference's pairing (FP4 routed, FP8 E8M0 shared): both formats in the same launches
+        for (int i = 0; i < nsjobs; i++) jobs[njobs + i] = sjobs[i];
+        e = run_jobs_mix<WFmt::FP4_OCP, WFmt::FP8_E8M0>(jobs, njobs + nsjobs, EXPERT_FP4, EXPERT_FP8_E8M0,
+                                                        (const uint16_t *)x, h, o, dim, inter, limit, official, 0, st);
+    } else {
+        e = run_fmt(fmt, jobs, njobs, dim, inter, (const uint16_t *)x, h, o, limit, official, 0, st);
+        if (e == hipSuccess && nsjobs > 0)
+            e = run_fmt(shared_fmt, sjobs, nsjobs, dim, inter, (const uint16_t *)x, h, o, limit, official, 0, st);
+    }
     if (e == hipSuccess && phase != 1) {
         hipLaunchKernelGGL(k_moe_combine, dim3(ceil_div(dim, 256), t), dim3(256), 0, st, table, npick, o, y, dim, y_f32);
         e = hipGetLastError();
