@@ -35,10 +35,23 @@ constexpr int kGemmMaxN = 1 << 20;
 
 // ---- activation quantization --------------------------------------------------------------------
 
+// Byte offset of activation code (m, k0) (k0 % 8 == 0; 8 codes from there) in MFMA operand order:
+// per group of 16 rows and 128-K step, 2 KB in which the 16-byte piece lane l = r + 16 g of the
+// operand loads (row r, bytes [16 g, 16 g + 16) of the step's first 64, then of its second 64)
+// sits at l * 16 of the first, then of the second kilobyte, so each operand load reads one
+// contiguous kilobyte. ks = k / 128.
+__host__ __device__ __forceinline__ size_t arranged_offset(int m, int k0, int ks) {
+    const int s = k0 >> 7, o = k0 & 127, h = o >> 6, g = (o & 63) >> 4;
+    return (((size_t)(m >> 4) * ks + s) * 2 + h) * 1024 + (size_t)((m & 15) + 16 * g) * 16 + (o & 15);
+}
+
 // x bf16 [rows][k] -> codes e4m3 [rows][k], scales E8M0 bytes [rows][k / block]. Each thread takes 8
-// consecutive values; block / 8 threads share a block (8 or 16 lanes of one wave).
+// consecutive values; block / 8 threads share a block (8 or 16 lanes of one wave). With `arranged`
+// (k % 128 == 0) the codes go out in MFMA operand order instead (arranged_offset below), for
+// k_gemm_one's contiguous activation loads.
 __global__ __launch_bounds__(256) void k_act_quant_e4m3(const uint16_t *__restrict__ x, int n8, int block,
-                                                        uint8_t *__restrict__ codes, uint8_t *__restrict__ scales) {
+                                                        uint8_t *__restrict__ codes, uint8_t *__restrict__ scales,
+                                                        int k, int arranged) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     const bool ok = i < n8;
     const u32x4 v = *(const u32x4 *)(x + (size_t)(ok ? i : 0) * 8);
@@ -64,7 +77,12 @@ __global__ __launch_bounds__(256) void k_act_quant_e4m3(const uint16_t *__restri
         w[j] = (uint32_t)p;
     }
     if (!ok) return;
-    *(u32x2 *)(codes + (size_t)i * 8) = u32x2{w[0], w[1]};
+    size_t at = (size_t)i * 8;
+    if (arranged) {
+        const int m = (int)(at / k), k0 = (int)(at % k);
+        at = arranged_offset(m, k0, k >> 7);
+    }
+    *(u32x2 *)(codes + at) = u32x2{w[0], w[1]};
     if ((threadIdx.x & (lanes - 1)) == 0) scales[(size_t)i * 8 / block] = (uint8_t)((__float_as_uint(s) >> 23) & 0xffu);
 }
 
@@ -250,7 +268,7 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const f32x4 *__restrict__ p
 //    act_block 128, 16 bytes per row or column for the per-32 scales), not one byte per step: a
 //    one-byte wave load costs the L1 as much as a 1 KB one. The MFMA reads the low byte of its scale
 //    operand, so each lane shifts its byte down.
-template <bool FP4W, int MT, int NT, int NW, int QW>
+template <bool FP4W, int MT, int NT, int NW, int QW, bool AARR>
 __global__ __launch_bounds__(NW * 64) void k_gemm_one(const uint8_t *__restrict__ wc, const void *__restrict__ ws,
                                                       const uint8_t *__restrict__ aq, const uint8_t *__restrict__ as_,
                                                       void *__restrict__ y, int y_f32, int M, int N, int K, int lda,
@@ -329,9 +347,15 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_one(const uint8_t *__restrict_
             const size_t kb = (size_t)(s < nst ? s0 + s : s0) * 128;
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                const uint8_t *row = aq + (size_t)min(m0 + 16 * mt + r, M - 1) * lda + kb;
-                av[s][mt][0] = *(const u32x4 *)(row + h0 + 16 * g);
-                av[s][mt][1] = *(const u32x4 *)(row + h1 + 16 * g);
+                if constexpr (AARR) {  // operand order (arranged_offset): two contiguous kilobytes
+                    const uint8_t *blk = aq + (((size_t)((m0 >> 4) + mt) * KS + (kb >> 7)) * 2) * 1024 + lane * 16;
+                    av[s][mt][0] = *(const u32x4 *)blk;
+                    av[s][mt][1] = *(const u32x4 *)(blk + 1024);
+                } else {
+                    const uint8_t *row = aq + (size_t)min(m0 + 16 * mt + r, M - 1) * lda + kb;
+                    av[s][mt][0] = *(const u32x4 *)(row + h0 + 16 * g);
+                    av[s][mt][1] = *(const u32x4 *)(row + h1 + 16 * g);
+                }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -359,7 +383,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_one(const uint8_t *__restrict_
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
                 const u32x4 x0 = av[s][mt][0], x1 = av[s][mt][1];
-                const u32x4 a0 = odd ? x1 : x0, a1 = odd ? x0 : x1;
+                const u32x4 a0 = odd && !AARR ? x1 : x0, a1 = odd && !AARR ? x0 : x1;
                 const i32x8 a = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
                 const uint32_t aw = asw[s / 4][mt][act32 ? s % 4 : 0];
                 const int ascale = (int)(act32 ? aw >> gsh : aw >> (8 * (s % 4)));
@@ -493,28 +517,36 @@ static hipError_t launch_gemm_t(const GemmPlan &p, int fmt, void *y, const void 
 
 // Requires p.steps <= the variant's steps per workgroup and p.slices * p.steps covering k / 128, and
 // split K (slices > 1) only in variant 0; A rows lda bytes apart.
+// arr: the activations are in operand order (arranged_offset; variants 3 and 4 only).
+template <bool ARR>
+static hipError_t launch_gemm_one(const GemmPlan &p, int fmt, void *y, const void *codes, const void *scales,
+                                  const uint8_t *aq, int lda, const uint8_t *as_, int m, int n, int k, int act_block,
+                                  int y_f32, hipStream_t st) {
+    const dim3 grid(p.ntiles * p.mgroups);
+    const int a32 = act_block == 32;
+    if (p.variant == 3 && fmt == 0)
+        hipLaunchKernelGGL((k_gemm_one<true, 1, 2, 8, 2, ARR>), grid, dim3(512), 0, st, (const uint8_t *)codes, scales, aq,
+                           as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
+    else if (p.variant == 3)
+        hipLaunchKernelGGL((k_gemm_one<false, 1, 2, 16, 1, ARR>), grid, dim3(1024), 0, st, (const uint8_t *)codes, scales,
+                           aq, as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
+    else if (fmt == 0)
+        hipLaunchKernelGGL((k_gemm_one<true, 2, 4, 4, 1, ARR>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales, aq,
+                           as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
+    else
+        hipLaunchKernelGGL((k_gemm_one<false, 2, 4, 4, 1, ARR>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales,
+                           aq, as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
+    return hipGetLastError();
+}
+
 static hipError_t launch_gemm_plan(const GemmPlan &p, int fmt, void *y, const void *codes, const void *scales,
                                    const uint8_t *aq, int lda, const uint8_t *as_, int m, int n, int k, int act_block,
-                                   int y_f32, void *work, hipStream_t st) {
+                                   int y_f32, void *work, hipStream_t st, bool arr = false) {
     f32x4 *part = (f32x4 *)work;
     const int shift = act_block == 32 ? 5 : 7;
-    if (p.variant >= 3) {
-        const dim3 grid(p.ntiles * p.mgroups);
-        const int a32 = act_block == 32;
-        if (p.variant == 3 && fmt == 0)
-            hipLaunchKernelGGL((k_gemm_one<true, 1, 2, 8, 2>), grid, dim3(512), 0, st, (const uint8_t *)codes, scales, aq,
-                               as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
-        else if (p.variant == 3)
-            hipLaunchKernelGGL((k_gemm_one<false, 1, 2, 16, 1>), grid, dim3(1024), 0, st, (const uint8_t *)codes, scales, aq,
-                               as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
-        else if (fmt == 0)
-            hipLaunchKernelGGL((k_gemm_one<true, 2, 4, 4, 1>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales, aq,
-                               as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
-        else
-            hipLaunchKernelGGL((k_gemm_one<false, 2, 4, 4, 1>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales, aq,
-                               as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
-        return hipGetLastError();
-    }
+    if (p.variant >= 3)
+        return arr ? launch_gemm_one<true>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, act_block, y_f32, st)
+                   : launch_gemm_one<false>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, act_block, y_f32, st);
     if (p.variant == 0)
         return launch_gemm_t<4, 4, 8>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
     if (p.variant == 1)
@@ -522,14 +554,20 @@ static hipError_t launch_gemm_plan(const GemmPlan &p, int fmt, void *y, const vo
     return launch_gemm_t<2, 4, 16>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
 }
 
+// variants 3 and 4 load scale words 16 bytes at a time; unaligned scale arrays take the other plans
+static GemmPlan plan_for(int fmt, const void *scales, const uint8_t *as_, int m, int n, int k) {
+    return gemm_plan(m, n, k, aligned16(as_) && (fmt != 0 || aligned16(scales)));
+}
+
 static hipError_t launch_gemm(int fmt, void *y, const void *codes, const void *scales, const uint8_t *aq,
                               const uint8_t *as_, int m, int n, int k, int act_block, int y_f32, void *work,
                               hipStream_t st) {
-    // variants 3 and 4 load scale words 16 bytes at a time; unaligned scale arrays take the other plans
-    const bool aligned = aligned16(as_) && (fmt != 0 || aligned16(scales));
-    return launch_gemm_plan(gemm_plan(m, n, k, aligned), fmt, y, codes, scales, aq, k, as_, m, n, k, act_block, y_f32,
-                            work, st);
+    return launch_gemm_plan(plan_for(fmt, scales, as_, m, n, k), fmt, y, codes, scales, aq, k, as_, m, n, k, act_block,
+                            y_f32, work, st);
 }
+
+// Rows of the activation codes in the workspace: a whole number of 16-row groups (operand order).
+static uint64_t aq_bytes(int m, int k) { return a256((uint64_t)(m + 15) / 16 * 16 * k); }
 
 static int check_gemm(const char *name, int fmt, const void *y, const void *codes, const void *scales, int m, int n,
                       int k, int act_block, const void *work) {
@@ -551,7 +589,7 @@ extern "C" {
 
 uint64_t stbl_amd_gemm_work_bytes(int m, int n, int k) {
     if (m < 1 || n < 1 || k < 128) return 256;
-    return part_reserve(m, n, k) + a256((uint64_t)m * k) + a256((uint64_t)m * (k / 32)) + 256;
+    return part_reserve(m, n, k) + aq_bytes(m, k) + a256((uint64_t)m * (k / 32)) + 256;
 }
 
 int stbl_amd_gemm_q(int fmt, void *y, const void *codes, const void *scales, const void *aq, const void *as, int m,
@@ -568,11 +606,17 @@ int stbl_amd_gemm(int fmt, void *y, const void *codes, const void *scales, const
     if (int e = check_gemm("gemm", fmt, y, codes, scales, m, n, k, act_block, work)) return e;
     if (!x || !aligned16(x)) return abi_fail(hipErrorInvalidValue, "gemm: x must be 16-byte aligned");
     uint8_t *aq = (uint8_t *)work + part_reserve(m, n, k);
-    uint8_t *as_ = aq + a256((uint64_t)m * k);
+    uint8_t *as_ = aq + aq_bytes(m, k);
+    // the one-launch plans read activations this call quantizes in operand order (one contiguous
+    // kilobyte per load instead of 16 rows x 64 bytes)
+    const GemmPlan p = plan_for(fmt, scales, as_, m, n, k);
+    const bool arr = p.variant >= 3;
     const int n8 = m * k / 8;
-    hipLaunchKernelGGL(k_act_quant_e4m3, dim3((n8 + 255) / 256), dim3(256), 0, st, (const uint16_t *)x, n8, act_block, aq, as_);
+    hipLaunchKernelGGL(k_act_quant_e4m3, dim3((n8 + 255) / 256), dim3(256), 0, st, (const uint16_t *)x, n8, act_block, aq,
+                       as_, k, (int)arr);
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess) e = launch_gemm(fmt, y, codes, scales, aq, as_, m, n, k, act_block, y_f32, work, st);
+    if (e == hipSuccess)
+        e = launch_gemm_plan(p, fmt, y, codes, scales, aq, k, as_, m, n, k, act_block, y_f32, work, st, arr);
     return abi_status(e, "gemm launch");
 }
 
@@ -584,7 +628,7 @@ int stbl_amd_act_quant_e4m3(const void *x, int rows, int k, int block, void *cod
     if (!aligned16(x) || ((uintptr_t)codes & 7)) return abi_fail(hipErrorInvalidValue, "act_quant_e4m3: x 16-byte, codes 8-byte aligned");
     const int n8 = rows * k / 8;
     hipLaunchKernelGGL(k_act_quant_e4m3, dim3((n8 + 255) / 256), dim3(256), 0, st, (const uint16_t *)x, n8, block,
-                       (uint8_t *)codes, (uint8_t *)scales);
+                       (uint8_t *)codes, (uint8_t *)scales, k, 0);
     return abi_status(hipGetLastError(), "act_quant_e4m3 launch");
 }
 
