@@ -50,6 +50,8 @@ def parse():
                     help="print the per-dispatch summary of a rocprofv3 kernel-trace CSV and exit (no GPU)")
     ap.add_argument("--trace-kernel", default=r"k_gemv<\(stbl::WFmt\)0, false, 1,",
                     help="kernel-name regex for --trace-summary (default: the headline FP4 GEMV kernel)")
+    ap.add_argument("--trace-by-grid", action="store_true",
+                    help="with --trace-summary: one line per (kernel, grid) with calls and median / mean duration")
     ap.add_argument("--copy-calib", action="store_true",
                     help="after the workloads, copy 64 MiB device to device 5 times (the reference transfer for "
                          "scaling HBM byte counters)")
@@ -1011,10 +1013,33 @@ def trace_summary(path, kernel_regex):
             "spacing_mean_ns": avg(sp), "gap_median_ns": med(gap), "pairs": len(nxt)}
 
 
+def trace_table(path, kernel_regex):
+    """Per (kernel, grid) rows of a rocprofv3 --kernel-trace CSV for the kernels matching kernel_regex:
+    calls and median / mean duration (ns), so that rows of one run that share a kernel (by shape)
+    are told apart. Returns a list of dicts."""
+    import csv
+    import re
+    import statistics
+
+    pat = re.compile(kernel_regex)
+    groups = {}
+    for r in csv.DictReader(open(path)):
+        if not pat.search(r["Kernel_Name"]):
+            continue
+        key = (r["Kernel_Name"], r["Grid_Size_X"], r["Grid_Size_Y"], r["Workgroup_Size_X"])
+        groups.setdefault(key, []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    return [{"kernel": k[0], "grid": f"{k[1]}x{k[2]}", "workgroup": int(k[3]), "calls": len(v),
+             "median_ns": statistics.median(v), "mean_ns": round(statistics.mean(v))} for k, v in groups.items()]
+
+
 def main():
     args = parse()
     if args.trace_summary:
-        print(json.dumps(trace_summary(args.trace_summary, args.trace_kernel)))
+        if args.trace_by_grid:
+            for row in trace_table(args.trace_summary, args.trace_kernel):
+                print(json.dumps(row))
+        else:
+            print(json.dumps(trace_summary(args.trace_summary, args.trace_kernel)))
         return
     if args.steps < 1 or args.warmup < 0:
         print(f"bench.py needs --steps >= 1 and --warmup >= 0 (got {args.steps}, {args.warmup})", file=sys.stderr)

@@ -131,3 +131,16 @@ def test_trace_summary_reads_a_kernel_trace(tmp_path):
     s = bench.trace_summary(str(p), r"k_gemv<")
     assert s["calls"] == 4 and s["pairs"] == 2
     assert s["dur_median_ns"] == 30 and s["spacing_median_ns"] == 50 and s["gap_median_ns"] == 20
+
+
+def test_trace_table_groups_by_grid(tmp_path):
+    import bench
+
+    p = tmp_path / "t_kernel_trace.csv"
+    hdr = '"Kind","Kernel_Name","Start_Timestamp","End_Timestamp","Grid_Size_X","Grid_Size_Y","Workgroup_Size_X"\n'
+    rows = [("k_a", 0, 10, 64, 1), ("k_a", 20, 40, 64, 1), ("k_a", 50, 55, 128, 2), ("k_b", 60, 90, 64, 1)]
+    p.write_text(hdr + "".join(f'"KERNEL_DISPATCH","{n}",{s},{e},{gx},{gy},64\n' for n, s, e, gx, gy in rows))
+    t = {(r["kernel"], r["grid"]): r for r in bench.trace_table(str(p), r"k_a")}
+    assert set(t) == {("k_a", "64x1"), ("k_a", "128x2")}
+    assert t[("k_a", "64x1")]["calls"] == 2 and t[("k_a", "64x1")]["median_ns"] == 15
+    assert t[("k_a", "128x2")]["mean_ns"] == 5
