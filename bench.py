@@ -50,6 +50,8 @@ def parse():
                     help="print the per-dispatch summary of a rocprofv3 kernel-trace CSV and exit (no GPU)")
     ap.add_argument("--trace-kernel", default=r"k_gemv<\(stbl::WFmt\)0, false, 1,",
                     help="kernel-name regex for --trace-summary (default: the headline FP4 GEMV kernel)")
+    ap.add_argument("--counter-summary", default=None, metavar="CSV",
+                    help="print per (kernel, grid, counter) medians of a rocprofv3 --pmc counter_collection CSV and exit")
     ap.add_argument("--trace-by-grid", action="store_true",
                     help="with --trace-summary: one line per (kernel, grid) with calls and median / mean duration")
     ap.add_argument("--copy-calib", action="store_true",
@@ -1032,8 +1034,30 @@ def trace_table(path, kernel_regex):
              "median_ns": statistics.median(v), "mean_ns": round(statistics.mean(v))} for k, v in groups.items()]
 
 
+def counter_table(path, kernel_regex):
+    """Per (kernel, grid, counter) medians of a rocprofv3 --pmc counter_collection CSV for the kernels
+    matching kernel_regex. Returns a list of dicts."""
+    import csv
+    import re
+    import statistics
+
+    pat = re.compile(kernel_regex)
+    groups = {}
+    for r in csv.DictReader(open(path)):
+        if not pat.search(r["Kernel_Name"]):
+            continue
+        key = (r["Kernel_Name"], r["Grid_Size"], r["Counter_Name"])
+        groups.setdefault(key, []).append(float(r["Counter_Value"]))
+    return [{"kernel": k[0], "grid": k[1], "counter": k[2], "dispatches": len(v), "median": statistics.median(v)}
+            for k, v in sorted(groups.items())]
+
+
 def main():
     args = parse()
+    if args.counter_summary:
+        for row in counter_table(args.counter_summary, args.trace_kernel):
+            print(json.dumps(row))
+        return
     if args.trace_summary:
         if args.trace_by_grid:
             for row in trace_table(args.trace_summary, args.trace_kernel):

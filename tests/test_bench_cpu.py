@@ -144,3 +144,16 @@ def test_trace_table_groups_by_grid(tmp_path):
     assert set(t) == {("k_a", "64x1"), ("k_a", "128x2")}
     assert t[("k_a", "64x1")]["calls"] == 2 and t[("k_a", "64x1")]["median_ns"] == 15
     assert t[("k_a", "128x2")]["mean_ns"] == 5
+
+
+def test_counter_table_medians(tmp_path):
+    import bench
+
+    p = tmp_path / "p_counter_collection.csv"
+    hdr = '"Dispatch_Id","Grid_Size","Kernel_Name","Counter_Name","Counter_Value"\n'
+    rows = [(1, 64, "k_a", "FETCH_SIZE", 10.0), (2, 64, "k_a", "FETCH_SIZE", 30.0), (3, 64, "k_a", "FETCH_SIZE", 20.0),
+            (4, 128, "k_a", "FETCH_SIZE", 5.0), (5, 64, "k_b", "FETCH_SIZE", 7.0)]
+    p.write_text(hdr + "".join(f'{d},{g},"{n}","{c}",{v}\n' for d, g, n, c, v in rows))
+    t = {(r["grid"], r["counter"]): r for r in bench.counter_table(str(p), r"k_a")}
+    assert t[("64", "FETCH_SIZE")]["median"] == 20.0 and t[("64", "FETCH_SIZE")]["dispatches"] == 3
+    assert t[("128", "FETCH_SIZE")]["median"] == 5.0 and len(t) == 2
