@@ -16,18 +16,39 @@ namespace stbl {
 
 // The reference engine's form: per 32 values in place, s = pow2_ceil(max(amax, 1e-4) * (1/448)),
 // x = bf16(e4m3(clamp(x / s, +-448)) * s). One 32-lane half-wave per block of 32.
+// The block's amax comes from its 32 lanes (half a wave) by four DPP moves and one lane shuffle
+// (instead of five shuffles, each an LDS round trip); x / s is x times the exact inverse of the power of two s; the e4m3 rounding is the
+// hardware v_cvt_pk_fp8_f32 (round to nearest even, equal to the software encoder f32_to_e4m3 on
+// fp32 inputs), and e4m3 * s is exact.
+__device__ __forceinline__ float dpp_max(float a, int ctrl_sel) {
+    int m;
+    switch (ctrl_sel) {  // compile-time after inlining
+        case 0: m = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0xB1, 0xF, 0xF, false); break;   // lane ^ 1
+        case 1: m = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x4E, 0xF, 0xF, false); break;   // lane ^ 2
+        case 2: m = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x141, 0xF, 0xF, false); break;  // 7 - lane in 8
+        default: m = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x140, 0xF, 0xF, false); break; // 15 - lane in 16
+    }
+    return fmaxf(a, __builtin_bit_cast(float, m));
+}
+
 __global__ void k_act_quant_fp8_inplace(float *x, int n_blocks) {
     const int b = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
     const int i = (blockIdx.x * blockDim.x + threadIdx.x) & 31;
     const bool ok = b < n_blocks;
     const float v = ok ? x[(size_t)b * 32 + i] : 0.f;
     float a = fabsf(v);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, kWave));
+    a = dpp_max(a, 0);
+    a = dpp_max(a, 1);
+    a = dpp_max(a, 2);
+    a = dpp_max(a, 3);
+    a = fmaxf(a, __shfl_xor(a, 16, kWave));  // lanes l and l ^ 16
     const float s = pow2_ceil(fmaxf(a, 1e-4f) * (1.0f / 448.0f));
+    const float inv = __uint_as_float((254u - ((__float_as_uint(s) >> 23) & 0xffu)) << 23);
     if (ok) {
-        const float q = fminf(fmaxf(v / s, -448.f), 448.f);  // exact: s is a power of two
-        x[(size_t)b * 32 + i] = bf16_round(e4m3_to_f32(f32_to_e4m3(q)) * s);
+        // (a block holding an infinity has s = +Inf, whose inverse is not a power of two: divide)
+        const float q = fminf(fmaxf(__builtin_isinf(s) ? v / s : v * inv, -448.f), 448.f);
+        const uint32_t c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q, q, 0, false) & 0xffu;
+        x[(size_t)b * 32 + i] = bf16_round(e4m3_to_f32(c) * s);
     }
 }
 

@@ -104,6 +104,20 @@ def test_stbl_act_quant_fp8_inplace(gpu):
     assert bits_equal(np_(got), want)
 
 
+@pytest.mark.parametrize("n", [13824, 13824 + 96, 32])
+def test_stbl_act_quant_fp8_inplace_fp32_scales(gpu, n):
+    # any fp32 values (not only bf16 ones), blocks spread over 2^-30 .. 2^40, an all-zero block and a
+    # block below the 1e-4 floor, at the engine's SwiGLU-output size and with a partial workgroup
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * np.repeat(2.0 ** rng.integers(-30, 41, n // 32), 32)).astype(np.float32)
+    if n >= 96:
+        x[32:64] = 0
+        x[64:96] *= 1e-12
+    got = ops.stbl_act_quant_fp8(torch.from_numpy(x.copy()).to(gpu))
+    want = oracle.act_quant(x[None], 32, True)[2][0]
+    assert bits_equal(np_(got), want)
+
+
 def test_round_bf16_axpy(gpu):
     x = data.normal((5000,), 10.0, seed=8)
     got = ops.stbl_round_bf16(x.clone().to(gpu))
