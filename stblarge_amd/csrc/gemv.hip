@@ -448,6 +448,11 @@ static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int o
         if constexpr (XF32) return launch_r<F, XF32, M, 1>(jobs, njobs, rows, k, out_mode, st);
         else {
             if (k / WTraits<F>::CH <= 64) return launch_r<F, XF32, M, 2>(jobs, njobs, rows, k, out_mode, st);
+            // rows of 4+ waves: 8 rows share the lane's x chunks (M x the weight bytes it reads) while
+            // the tiles still fill every CU (2048x7168: FP4 M=4 5.53 -> 5.23 us, M=3 4.80 -> 4.76,
+            // FP8 M=3 5.62 -> 5.38; FP8 M=4 unchanged)
+            if (k / WTraits<F>::CH > 3 * 64 && (long)ceil_div(rows, 8) * njobs >= device_cus())
+                return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
             return launch_r<F, XF32, M, 4>(jobs, njobs, rows, k, out_mode, st);
         }
     }
@@ -489,10 +494,10 @@ static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int o
             return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
         }
         const int cus = device_cus();
-        // one token of FP4 over rows of 4+ waves: 8-row tiles when they still fill every CU, halving the x
-        // reads per weight byte again (2048x7168: 3.85 -> 3.80 us; rows of one wave lose: 7168x2048
-        // 3.73 -> 4.62 us)
-        if constexpr (F == WFmt::FP4_OCP && M == 1)
+        // one token of FP4, or two tokens, over rows of 4+ waves: 8-row tiles when they still fill every
+        // CU, halving the x reads per weight byte again (2048x7168: FP4 M=1 3.85 -> 3.80 us, M=2 4.24 ->
+        // 4.18, FP8 M=2 5.08 -> 4.78; rows of one wave lose: 7168x2048 3.73 -> 4.62 us)
+        if constexpr (M == 2 || (F == WFmt::FP4_OCP && M == 1))
             if (k / WTraits<F>::CH > 3 * 64 && (long)ceil_div(rows, 8) * njobs >= cus)
                 return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
         const long busiest2 = ceil_div(ceil_div(rows, 2) * njobs, cus) * 2L;
