@@ -559,3 +559,20 @@ def test_random_shapes_every_gemv_entry_point(gpu, seed):
             ops.stbl_gemv_fp8(y, torch.from_numpy(codes).to(gpu), torch.from_numpy(sc).to(gpu),
                               torch.from_numpy(x).to(gpu), rows, k, 1)
             assert_gemv(np_(y), np_(y), want, tol=2.0 ** -8)
+
+
+@pytest.mark.parametrize("fmt,rows,k", [(0, 2052, 7168), (1, 2060, 4096)])
+@pytest.mark.parametrize("m", [2, 3, 4])
+def test_gemv_multi_token_8_row_tiles(gpu, fmt, rows, k, m):
+    # 2-4 tokens over rows of 4+ waves take 8-row tiles when those fill every CU; a ragged last tile
+    # (4 of 8 rows, FP8 12 of 8 + 4) against the oracle
+    q, ref = (oracle.quant_fp4, oracle.gemv_fp4) if fmt == 0 else (oracle.quant_fp8_b128, oracle.gemv_fp8_b128)
+    codes, scales = q(data.weight(rows, k, seed=rows + m).numpy())
+    x = data.activation(m, k, seed=k + m)
+    want = ref(codes, scales, x.float().numpy())
+    fn = ops.gemv_fp4 if fmt == 0 else ops.gemv_fp8
+    dc, ds = torch.from_numpy(codes).to(gpu), torch.from_numpy(scales).to(gpu)
+    y32 = fn(dc, ds, x.to(gpu), out_f32=True)
+    y16 = fn(dc, ds, x.to(gpu))
+    assert tuple(y16.shape) == (m, rows)
+    assert_gemv(np_(y32), np_(y16), want)
