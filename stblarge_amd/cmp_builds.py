@@ -144,25 +144,32 @@ def _cases(dev, seed):
     # expert FFN and MoE (official numerics, the engine's shared expert format)
     dim, inter = 5120, 2304
     experts = [ops.quant_expert(data.weight(inter, dim, 10 * seed + i, dev), data.weight(inter, dim, 10 * seed + i + 1, dev),
-                                data.weight(dim, inter, 10 * seed + i + 2, dev), ops.FP4) for i in range(0, 21, 3)]
+                                data.weight(dim, inter, 10 * seed + i + 2, dev), ops.FP4) for i in range(0, 42, 3)]
     shared = ops.quant_expert(data.weight(inter, dim, 3, dev), data.weight(inter, dim, 4, dev),
                               data.weight(dim, inter, 5, dev), ops.FP8_E8M0)
-    for t in (1, 4):
+    # picks (j + 2i) % 7 give every expert three or four tokens; the explicit table gives experts of
+    # one, two and four tokens, so the step's jobs span every token class (with the FP8 E8M0 shared
+    # expert, or with expert 13 as an FP4 shared one)
+    mixed = [[0, 1, 2, 3, 4, 5], [0, 1, 7, 8, 9, 10], [0, 11, 12, 6, 2, 3], [0, 7, 11, 12, 8, 9]]
+    for name, t, table, sfmt in (("v41 t=1", 1, None, ops.FP8_E8M0), ("v41 t=4", 4, None, ops.FP8_E8M0),
+                                 ("v41 t=4 token classes", 4, mixed, ops.FP8_E8M0),
+                                 ("fp4 t=4 token classes", 4, mixed, -1)):
         x = bf((t, dim))
 
-        def moe(lib, x=x, t=t):
-            pick = [[(j + 2 * i) % 7 for j in range(6)] for i in range(t)]
+        def moe(lib, x=x, t=t, table=table, sfmt=sfmt):
+            pick = table or [[(j + 2 * i) % 7 for j in range(6)] for i in range(t)]
             wts = [[0.3, 0.2, 0.15, 0.15, 0.1, 0.1]] * t
-            slots = experts + [shared]
+            slots = experts + [shared] if sfmt >= 0 else experts
+            sh = 14 if sfmt >= 0 else 13
             y = _out((t, dim), dev, torch.bfloat16)
             work = torch.empty(ops.moe_work_bytes(t, 6, dim, inter), dtype=torch.uint8, device=dev)
             arr = (ctypes.c_void_p * len(slots))(*[s.data_ptr() for s in slots])
             pk = (ctypes.c_int * (6 * t))(*[v for row in pick for v in row])
             wt = (ctypes.c_float * (6 * t))(*[v for row in wts for v in row])
-            assert lib.stbl_amd_moe_experts(ops.FP4, _p(y), _p(x), t, dim, inter, arr, len(slots), pk, wt, 6, 7,
-                                            ops.FP8_E8M0, 10.0, 1, 0, _p(work), st) == 0
+            assert lib.stbl_amd_moe_experts(ops.FP4, _p(y), _p(x), t, dim, inter, arr, len(slots), pk, wt, 6, sh,
+                                            sfmt, 10.0, 1, 0, _p(work), st) == 0
             return [y]
-        cases.append((f"moe_experts v41 t={t}", moe))
+        cases.append((f"moe_experts {name}", moe))
     logits = torch.randn((4, 256), device=dev, generator=g) * 3
 
     def route(lib):

@@ -13,6 +13,10 @@
 //   k_moe_down    down rows of a job; output rounded to bf16 as the reference's GEMV does;
 //   k_moe_combine per token, the fp32 sum of its experts' outputs in top-k order plus the shared
 //                 expert's, rounded to bf16 (stbl/model.cu:589-592).
+// Jobs are compiled per token class (1, 2 or 3-4 tokens). A step whose jobs of one format span
+// several classes runs them all in one gate/up and one down launch (k_moe_gateup_any /
+// k_moe_down_any); otherwise each class has its launches, one launch holding both formats where a
+// class has FP4 and FP8 E8M0 jobs (k_moe_gateup_mix / k_moe_down_mix).
 // In the reference's "official" numerics the expert input and the SwiGLU output are quantized to FP8
 // per 32 first (stbl/model.cu:510, :538); both kernels do that quantization in registers on the
 // lane's own chunk of the activation, so it costs no launch and no memory traffic.
@@ -122,6 +126,32 @@ __device__ __forceinline__ bool wave_total(float (&vals)[N], float (*red)[N], fl
     return true;
 }
 
+// The lane's products over its CPL chunks of 16 bytes (x words of chunk i: i * CH / 2 on), chunk by
+// chunk.
+template <WFmt F, int M, int CPL>
+__device__ __forceinline__ void chunk_dot_lane(float (&s)[M], const u32x4 (&w)[CPL],
+                                               const uint32_t (&xw)[M][WTraits<F>::CH * CPL / 2], float cs) {
+    constexpr int CH = WTraits<F>::CH;
+    if constexpr (CPL == 1) {
+        chunk_dot_packed<F, M, CH>(s, w[0], xw, cs);
+    } else {
+#pragma unroll
+        for (int t = 0; t < M; t++) s[t] = 0.f;
+#pragma unroll
+        for (int i = 0; i < CPL; i++) {
+            uint32_t part[M][CH / 2];
+#pragma unroll
+            for (int t = 0; t < M; t++)
+#pragma unroll
+                for (int j = 0; j < CH / 2; j++) part[t][j] = xw[t][i * CH / 2 + j];
+            float si[M];
+            chunk_dot_packed<F, M, CH>(si, w[i], part, cs);
+#pragma unroll
+            for (int t = 0; t < M; t++) s[t] += si[t];
+        }
+    }
+}
+
 // ---- gate/up + SwiGLU ----------------------------------------------------------------------------
 
 // Job blockIdx.y, rows [row0, row0 + R) of gate and of up. x bf16 [T][dim] -> h bf16 [P][inter].
@@ -131,10 +161,11 @@ __device__ __forceinline__ bool wave_total(float (&vals)[N], float (*red)[N], fl
 // The body runs in any workgroup of at least ceil(dim / CH / 64) waves: waves past the job's K (in
 // the mixed-format launches, whose workgroups are sized for the format with the most waves) load
 // nothing and add zeros.
-template <WFmt F, int M, int R, bool DW>
+template <WFmt F, int M, int R, bool DW, int CPL = 1>
 __device__ __forceinline__ void gateup_job(const MoeJob &J, const ExpertLayout &L, const uint16_t *__restrict__ x,
                                            uint16_t *__restrict__ h, int dim, int inter, float limit, int official) {
-    constexpr int CH = WTraits<F>::CH;
+    static_assert(CPL == 1 || !WTraits<F>::fp4, "two chunks per lane: FP8 rows");
+    constexpr int CH = WTraits<F>::CH * CPL;  // elements per lane
     const SlotMat<F> G(J.slot, L, 0, dim, inter), U(J.slot, L, 1, dim, inter);
     const int lane = threadIdx.x & 63, c = (threadIdx.x >> 6) * 64 + lane, nch = dim / CH;
     const bool active = c < nch;
@@ -159,7 +190,7 @@ __device__ __forceinline__ void gateup_job(const MoeJob &J, const ExpertLayout &
 #pragma unroll
             for (int i = 0; i < CH / 2; i++) xw[t][i] = tmp[0][i];
         }
-        u32x4 wg[R], wu[R];
+        u32x4 wg[R][CPL], wu[R][CPL];
         uint32_t sg[R], su[R];
         uint32_t sdw[(2 * R + 3) / 4];
         if constexpr (DW) {
@@ -174,19 +205,22 @@ __device__ __forceinline__ void gateup_job(const MoeJob &J, const ExpertLayout &
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const size_t row = (size_t)min(row0 + r, inter - 1);
-                wg[r] = G.load_codes(row, cc);
-                wu[r] = U.load_codes(row, cc);
+                wg[r][0] = G.load_codes(row, cc);
+                wu[r][0] = U.load_codes(row, cc);
             }
         } else {
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const size_t row = (size_t)min(row0 + r, inter - 1);
-                G.load(row, cc, wg[r], sg[r]);
-                U.load(row, cc, wu[r], su[r]);
+#pragma unroll
+                for (int i = 0; i < CPL; i++) {
+                    G.load(row, cc * CPL + i, wg[r][i], sg[r]);
+                    U.load(row, cc * CPL + i, wu[r][i], su[r]);
+                }
             }
         }
         float lg = 1.f, lu = 1.f;
-        if constexpr (!WTraits<F>::fp4) lg = G.block_scale(row0, cc), lu = U.block_scale(row0, cc);
+        if constexpr (!WTraits<F>::fp4) lg = G.block_scale(row0, cc * CPL), lu = U.block_scale(row0, cc * CPL);
         if (official) act_quant_packed<M, CH>(xw);
         if constexpr (DW) {
 #pragma unroll
@@ -196,8 +230,8 @@ __device__ __forceinline__ void gateup_job(const MoeJob &J, const ExpertLayout &
 #pragma unroll
         for (int r = 0; r < R; r++) {
             float sgv[M], suv[M];
-            chunk_dot_packed<F, M, CH>(sgv, wg[r], xw, conv_scale<F>(sg[r], lg));
-            chunk_dot_packed<F, M, CH>(suv, wu[r], xw, conv_scale<F>(su[r], lu));
+            chunk_dot_lane<F, M, CPL>(sgv, wg[r], xw, conv_scale<F>(sg[r], lg));
+            chunk_dot_lane<F, M, CPL>(suv, wu[r], xw, conv_scale<F>(su[r], lu));
             const float a = post_scale<F>(lg), b = post_scale<F>(lu);
 #pragma unroll
             for (int t = 0; t < M; t++) {
@@ -230,24 +264,31 @@ __global__ __launch_bounds__(512) void k_moe_gateup(MoeJobs jobs, ExpertLayout L
 
 // Jobs of two formats in one launch (the reference's FP4 routed experts next to its FP8 E8M0 shared
 // expert, stbl/model.cu:536-547): each workgroup takes its job's format (wave-uniform), so the
-// shared expert costs no launches of its own.
+// shared expert costs no launches of its own. FP8 rows next to FP4 ones take two 16-byte chunks per
+// lane (mix_cpl), so both formats' rows span the same lanes and no wave of a workgroup idles.
+template <WFmt FA, WFmt FB>
+constexpr int mix_cpl() {
+    return WTraits<FB>::fp4 ? 1 : WTraits<FA>::CH / WTraits<FB>::CH;
+}
+
 template <WFmt FA, WFmt FB, int M, int R, bool DWA, bool DWB>
 __global__ __launch_bounds__(512) void k_moe_gateup_mix(MoeJobs jobs, ExpertLayout LA, ExpertLayout LB,
                                                         const uint16_t *__restrict__ x, uint16_t *__restrict__ h,
                                                         int dim, int inter, float limit, int official, int fmt_a) {
     const MoeJob &J = jobs.j[blockIdx.y];
     if (J.fmt == fmt_a) gateup_job<FA, M, R, DWA>(J, LA, x, h, dim, inter, limit, official);
-    else gateup_job<FB, M, R, DWB>(J, LB, x, h, dim, inter, limit, official);
+    else gateup_job<FB, M, R, DWB, mix_cpl<FA, FB>()>(J, LB, x, h, dim, inter, limit, official);
 }
 
 // ---- down ------------------------------------------------------------------------------------------
 
 // Job blockIdx.y, rows [row0, row0 + R) of down. h bf16 [P][inter] -> o [P][dim] (bf16, or fp32
 // holding the unrounded sum when out_f32). DW as in k_moe_gateup.
-template <WFmt F, int M, int R, bool DW>
+template <WFmt F, int M, int R, bool DW, int CPL = 1>
 __device__ __forceinline__ void down_job(const MoeJob &J, const ExpertLayout &L, const uint16_t *__restrict__ h,
                                          void *__restrict__ o, int dim, int inter, int official, int out_f32) {
-    constexpr int CH = WTraits<F>::CH;
+    static_assert(CPL == 1 || !WTraits<F>::fp4, "two chunks per lane: FP8 rows");
+    constexpr int CH = WTraits<F>::CH * CPL;  // elements per lane
     const SlotMat<F> D(J.slot, L, 2, dim, inter);
     const int lane = threadIdx.x & 63, c = (threadIdx.x >> 6) * 64 + lane, nch = inter / CH;
     const bool active = c < nch;
@@ -268,7 +309,7 @@ __device__ __forceinline__ void down_job(const MoeJob &J, const ExpertLayout &L,
 #pragma unroll
             for (int i = 0; i < CH / 2; i++) xw[t][i] = tmp[0][i];
         }
-        u32x4 wd[R];
+        u32x4 wd[R][CPL];
         uint32_t sd[R];
         uint32_t sdw[(R + 3) / 4];
         if constexpr (DW) {
@@ -277,13 +318,15 @@ __device__ __forceinline__ void down_job(const MoeJob &J, const ExpertLayout &L,
             for (int q = 0; q < (R + 3) / 4; q++)
                 sdw[q] = D.load_scale_dword((size_t)min(row0 + min(4 * q + (lane >> 4), R - 1), dim - 1), dwi);
 #pragma unroll
-            for (int r = 0; r < R; r++) wd[r] = D.load_codes((size_t)min(row0 + r, dim - 1), cc);
+            for (int r = 0; r < R; r++) wd[r][0] = D.load_codes((size_t)min(row0 + r, dim - 1), cc);
         } else {
 #pragma unroll
-            for (int r = 0; r < R; r++) D.load((size_t)min(row0 + r, dim - 1), cc, wd[r], sd[r]);
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int i = 0; i < CPL; i++) D.load((size_t)min(row0 + r, dim - 1), cc * CPL + i, wd[r][i], sd[r]);
         }
         float ld = 1.f;
-        if constexpr (!WTraits<F>::fp4) ld = D.block_scale(row0, cc);
+        if constexpr (!WTraits<F>::fp4) ld = D.block_scale(row0, cc * CPL);
         if (official) act_quant_packed<M, CH>(xw);
         if constexpr (DW) {
 #pragma unroll
@@ -293,7 +336,7 @@ __device__ __forceinline__ void down_job(const MoeJob &J, const ExpertLayout &L,
 #pragma unroll
         for (int r = 0; r < R; r++) {
             float s[M];
-            chunk_dot_packed<F, M, CH>(s, wd[r], xw, conv_scale<F>(sd[r], ld));
+            chunk_dot_lane<F, M, CPL>(s, wd[r], xw, conv_scale<F>(sd[r], ld));
             const float a = post_scale<F>(ld);
 #pragma unroll
             for (int t = 0; t < M; t++) tot[t * R + r] = active ? s[t] * a : 0.f;
@@ -321,7 +364,35 @@ __global__ __launch_bounds__(512) void k_moe_down_mix(MoeJobs jobs, ExpertLayout
                                                       int inter, int official, int out_f32, int fmt_a) {
     const MoeJob &J = jobs.j[blockIdx.y];
     if (J.fmt == fmt_a) down_job<FA, M, R, DWA>(J, LA, h, o, dim, inter, official, out_f32);
-    else down_job<FB, M, R, DWB>(J, LB, h, o, dim, inter, official, out_f32);
+    else down_job<FB, M, R, DWB, mix_cpl<FA, FB>()>(J, LB, h, o, dim, inter, official, out_f32);
+}
+
+// ---- jobs of every token class in one launch --------------------------------------------------------
+
+// Jobs of 1, 2 and 3-4 tokens of one format in one gate/up and one down launch: each workgroup
+// takes its job's token class (workgroup-uniform). The few multi-token jobs of a step (the shared
+// expert, which every token takes; experts two tokens picked) then compute while the one-token jobs
+// stream, instead of running in launches of their own at a fraction of the bandwidth. The kernel's
+// registers are those of the 4-token body, so a launch of one-token jobs only keeps k_moe_gateup /
+// k_moe_down.
+template <WFmt F, int R, bool DW>
+__global__ __launch_bounds__(512) void k_moe_gateup_any(MoeJobs jobs, ExpertLayout L, const uint16_t *__restrict__ x,
+                                                        uint16_t *__restrict__ h, int dim, int inter, float limit,
+                                                        int official) {
+    const MoeJob &J = jobs.j[blockIdx.y];
+    if (J.m == 1) gateup_job<F, 1, R, DW>(J, L, x, h, dim, inter, limit, official);
+    else if (J.m == 2) gateup_job<F, 2, R, DW>(J, L, x, h, dim, inter, limit, official);
+    else gateup_job<F, 4, R, DW>(J, L, x, h, dim, inter, limit, official);
+}
+
+template <WFmt F, int R, bool DW>
+__global__ __launch_bounds__(512) void k_moe_down_any(MoeJobs jobs, ExpertLayout L, const uint16_t *__restrict__ h,
+                                                      void *__restrict__ o, int dim, int inter, int official,
+                                                      int out_f32) {
+    const MoeJob &J = jobs.j[blockIdx.y];
+    if (J.m == 1) down_job<F, 1, R, DW>(J, L, h, o, dim, inter, official, out_f32);
+    else if (J.m == 2) down_job<F, 2, R, DW>(J, L, h, o, dim, inter, official, out_f32);
+    else down_job<F, 4, R, DW>(J, L, h, o, dim, inter, official, out_f32);
 }
 
 // ---- combine ------------------------------------------------------------------------------------
@@ -477,10 +548,80 @@ static hipError_t launch_down(const MoeJobs &jobs, int n, const ExpertLayout &L,
     return launch_down_r<F, M, M == 4 ? 4 : 8>(jobs, n, L, h, o, dim, inter, official, out_f32, st);
 }
 
-// Runs the jobs (sorted into launches by token count) through gate/up and down.
+// Token class of a job: 1 (one token), 2 (two) or 3 (three or four: the M = 4 templates).
+static int token_class(const MoeJob &J) { return J.m == 1 ? 1 : (J.m == 2 ? 2 : 3); }
+
+static bool several_classes(const MoeJob *all, int njobs) {
+    for (int j = 1; j < njobs; j++)
+        if (token_class(all[j]) != token_class(all[0])) return true;
+    return false;
+}
+
+// One gate/up (4 gate and 4 up rows per workgroup) or down (8 rows) launch over jobs of every token
+// class (k_moe_gateup_any, k_moe_down_any).
 template <WFmt F>
-static hipError_t run_jobs(const MoeJob *all, int njobs, const ExpertLayout &L, const uint16_t *x, uint16_t *h,
-                           void *o, int dim, int inter, float limit, int official, int out_f32, hipStream_t st) {
+static hipError_t launch_any(bool gateup, const MoeJobs &jobs, int n, const ExpertLayout &L, const uint16_t *x,
+                             uint16_t *h, void *o, int dim, int inter, float limit, int official, int out_f32,
+                             hipStream_t st) {
+    const int k = gateup ? dim : inter;
+    const dim3 block(64 * ceil_div(k / WTraits<F>::CH, 64));
+    // FP4 tiles whose scale rows are a multiple of 4 bytes fetch their scales as dwords
+    const bool dw = WTraits<F>::fp4 && (k / 32) % 4 == 0;
+    if (gateup) {
+        const dim3 grid(ceil_div(inter, 4), n);
+        if (dw)
+            hipLaunchKernelGGL((k_moe_gateup_any<F, 4, WTraits<F>::fp4>), grid, block, 0, st, jobs, L, x, h, dim, inter,
+                               limit, official);
+        else
+            hipLaunchKernelGGL((k_moe_gateup_any<F, 4, false>), grid, block, 0, st, jobs, L, x, h, dim, inter, limit,
+                               official);
+    } else {
+        const dim3 grid(ceil_div(dim, 8), n);
+        if (dw)
+            hipLaunchKernelGGL((k_moe_down_any<F, 8, WTraits<F>::fp4>), grid, block, 0, st, jobs, L, h, o, dim, inter,
+                               official, out_f32);
+        else
+            hipLaunchKernelGGL((k_moe_down_any<F, 8, false>), grid, block, 0, st, jobs, L, h, o, dim, inter, official,
+                               out_f32);
+    }
+    return hipGetLastError();
+}
+
+// Runs jobs of one format and several token classes through one gate/up and one down launch (per
+// kMoeMaxJobs jobs), in order of falling token class: the workgroups with the most arithmetic per
+// byte are dispatched first, so it overlaps the one-token jobs' streaming.
+template <WFmt F>
+static hipError_t run_jobs_any(const MoeJob *all, int njobs, const ExpertLayout &L, const uint16_t *x, uint16_t *h,
+                               void *o, int dim, int inter, float limit, int official, int out_f32, hipStream_t st) {
+    for (int phase = 0; phase < 2; phase++) {
+        MoeJobs batch;
+        int n = 0;
+        auto flush = [&]() -> hipError_t {
+            if (n == 0) return hipSuccess;
+            const hipError_t e = launch_any<F>(phase == 0, batch, n, L, x, h, o, dim, inter, limit, official, out_f32, st);
+            n = 0;
+            return e;
+        };
+        for (int cls = 3; cls >= 1; cls--)
+            for (int j = 0; j < njobs; j++) {
+                if (token_class(all[j]) != cls) continue;
+                batch.j[n++] = all[j];
+                if (n == kMoeMaxJobs) {
+                    const hipError_t e = flush();
+                    if (e != hipSuccess) return e;
+                }
+            }
+        const hipError_t e = flush();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// Runs the jobs through gate/up and down in launches of one token class each.
+template <WFmt F>
+static hipError_t run_jobs_by_class(const MoeJob *all, int njobs, const ExpertLayout &L, const uint16_t *x,
+                                    uint16_t *h, void *o, int dim, int inter, float limit, int official, int out_f32,
+                                    hipStream_t st) {
     for (int phase = 0; phase < 2; phase++) {
         for (int mclass = 1; mclass <= 3; mclass++) {  // M = 1, 2, 4 templates
             MoeJobs batch;
@@ -516,17 +657,6 @@ static hipError_t run_jobs(const MoeJob *all, int njobs, const ExpertLayout &L, 
     return hipSuccess;
 }
 
-// Runs jobs whose slots hold format fmt.
-static hipError_t run_fmt(int fmt, const MoeJob *all, int njobs, int dim, int inter, const uint16_t *x, uint16_t *h,
-                          void *o, float limit, int official, int out_f32, hipStream_t st) {
-    const ExpertLayout L = expert_layout(fmt, dim, inter);
-    if (fmt == EXPERT_FP4)
-        return run_jobs<WFmt::FP4_OCP>(all, njobs, L, x, h, o, dim, inter, limit, official, out_f32, st);
-    if (fmt == EXPERT_FP8)
-        return run_jobs<WFmt::FP8_B128>(all, njobs, L, x, h, o, dim, inter, limit, official, out_f32, st);
-    return run_jobs<WFmt::FP8_E8M0>(all, njobs, L, x, h, o, dim, inter, limit, official, out_f32, st);
-}
-
 // Gate/up and down launches over jobs of two formats, FA (format fmt_a) and FB (each job's fmt
 // says which), with the same row tiles as the single-format launches (4 gate and 4 up rows, 8 down
 // rows, 4 with 4 tokens). A workgroup has as many waves as the format with the longer rows needs.
@@ -536,7 +666,7 @@ static hipError_t launch_mix(bool gateup, const MoeJobs &jobs, int n, int fmt_a,
                              hipStream_t st) {
     const ExpertLayout LA = expert_layout(fmt_a, dim, inter), LB = expert_layout(fmt_b, dim, inter);
     const int k = gateup ? dim : inter;
-    const int waves = std::max(ceil_div(k / WTraits<FA>::CH, 64), ceil_div(k / WTraits<FB>::CH, 64));
+    const int waves = std::max(ceil_div(k / WTraits<FA>::CH, 64), ceil_div(k / (WTraits<FB>::CH * mix_cpl<FA, FB>()), 64));
     // FP4 tiles of 4+ rows whose scale rows are a multiple of 4 bytes fetch their scales as dwords
     const bool dwa = WTraits<FA>::fp4 && (k / 32) % 4 == 0, dwb = WTraits<FB>::fp4 && (k / 32) % 4 == 0;
     if (gateup) {
@@ -565,12 +695,14 @@ static hipError_t launch_mix(bool gateup, const MoeJobs &jobs, int n, int fmt_a,
     return hipGetLastError();
 }
 
-// Runs jobs of formats fmt_a (FA) and fmt_b (FB) through gate/up and down as run_jobs does, a launch
-// holding both formats where its token class has both (the FB jobs first: their workgroups carry
-// more bytes, so they are dispatched before the others), else the single-format launches.
+// Runs jobs of formats fmt_a (FA) and fmt_b (FB) through gate/up and down in launches of one token
+// class each, a launch holding both formats where its class has both (the FB jobs first: their
+// workgroups carry more bytes, so they are dispatched before the others), else the single-format
+// launches.
 template <WFmt FA, WFmt FB>
-static hipError_t run_jobs_mix(const MoeJob *all, int njobs, int fmt_a, int fmt_b, const uint16_t *x, uint16_t *h,
-                               void *o, int dim, int inter, float limit, int official, int out_f32, hipStream_t st) {
+static hipError_t run_jobs_mix_by_class(const MoeJob *all, int njobs, int fmt_a, int fmt_b, const uint16_t *x,
+                                        uint16_t *h, void *o, int dim, int inter, float limit, int official,
+                                        int out_f32, hipStream_t st) {
     const ExpertLayout LA = expert_layout(fmt_a, dim, inter), LB = expert_layout(fmt_b, dim, inter);
     for (int phase = 0; phase < 2; phase++) {
         for (int mclass = 1; mclass <= 3; mclass++) {
@@ -619,6 +751,47 @@ static hipError_t run_jobs_mix(const MoeJob *all, int njobs, int fmt_a, int fmt_
         }
     }
     return hipSuccess;
+}
+
+// The launch plan of a set of jobs: when the jobs of format fmt_a (every job, with one format) span
+// several token classes, they go through run_jobs_any and the others (format fmt_b) through the
+// launches per class; otherwise every job goes through the launches per class. The formats stay
+// apart: in one launch with both, each workgroup holds the registers of the widest of six bodies
+// (measured with FP8 E8M0 jobs of two chunks per lane: C4 T=4 122 -> 137 us, V4.1 T=4 108 -> 115 us).
+template <WFmt FA, WFmt FB>
+static hipError_t run_jobs_split(const MoeJob *all, int njobs, int fmt_a, int fmt_b, const uint16_t *x, uint16_t *h,
+                                 void *o, int dim, int inter, float limit, int official, int out_f32, hipStream_t st) {
+    const ExpertLayout LA = expert_layout(fmt_a, dim, inter);
+    static thread_local MoeJob lo[kMoeMaxT * kMoeMaxPick], hi[kMoeMaxT * kMoeMaxPick];
+    int nlo = 0, nhi = 0;
+    for (int j = 0; j < njobs; j++) {
+        if (FA == FB || all[j].fmt == fmt_a) lo[nlo++] = all[j];
+        else hi[nhi++] = all[j];
+    }
+    if (!several_classes(lo, nlo)) {
+        if constexpr (FA == FB) return run_jobs_by_class<FA>(all, njobs, LA, x, h, o, dim, inter, limit, official, out_f32, st);
+        else return run_jobs_mix_by_class<FA, FB>(all, njobs, fmt_a, fmt_b, x, h, o, dim, inter, limit, official, out_f32, st);
+    }
+    hipError_t e = run_jobs_any<FA>(lo, nlo, LA, x, h, o, dim, inter, limit, official, out_f32, st);
+    if constexpr (FA != FB) {
+        if (e == hipSuccess && nhi > 0)
+            e = run_jobs_by_class<FB>(hi, nhi, expert_layout(fmt_b, dim, inter), x, h, o, dim, inter, limit, official,
+                                      out_f32, st);
+    }
+    return e;
+}
+
+// Runs jobs whose slots hold format fmt.
+static hipError_t run_fmt(int fmt, const MoeJob *all, int njobs, int dim, int inter, const uint16_t *x, uint16_t *h,
+                          void *o, float limit, int official, int out_f32, hipStream_t st) {
+    if (fmt == EXPERT_FP4)
+        return run_jobs_split<WFmt::FP4_OCP, WFmt::FP4_OCP>(all, njobs, fmt, fmt, x, h, o, dim, inter, limit, official,
+                                                            out_f32, st);
+    if (fmt == EXPERT_FP8)
+        return run_jobs_split<WFmt::FP8_B128, WFmt::FP8_B128>(all, njobs, fmt, fmt, x, h, o, dim, inter, limit, official,
+                                                              out_f32, st);
+    return run_jobs_split<WFmt::FP8_E8M0, WFmt::FP8_E8M0>(all, njobs, fmt, fmt, x, h, o, dim, inter, limit, official,
+                                                          out_f32, st);
 }
 
 static bool fmt_ok(int fmt) { return fmt == EXPERT_FP4 || fmt == EXPERT_FP8 || fmt == EXPERT_FP8_E8M0; }
@@ -731,8 +904,8 @@ static int moe_experts_impl(int fmt, void *y, const void *x, int t, int dim, int
     if (nsjobs > 0 && fmt == EXPERT_FP4 && shared_fmt == EXPERT_FP8_E8M0) {
         // the reference's pairing (FP4 routed, FP8 E8M0 shared): both formats in the same launches
         for (int i = 0; i < nsjobs; i++) jobs[njobs + i] = sjobs[i];
-        e = run_jobs_mix<WFmt::FP4_OCP, WFmt::FP8_E8M0>(jobs, njobs + nsjobs, EXPERT_FP4, EXPERT_FP8_E8M0,
-                                                        (const uint16_t *)x, h, o, dim, inter, limit, official, 0, st);
+        e = run_jobs_split<WFmt::FP4_OCP, WFmt::FP8_E8M0>(jobs, njobs + nsjobs, EXPERT_FP4, EXPERT_FP8_E8M0,
+                                                          (const uint16_t *)x, h, o, dim, inter, limit, official, 0, st);
     } else {
         e = run_fmt(fmt, jobs, njobs, dim, inter, (const uint16_t *)x, h, o, limit, official, 0, st);
         if (e == hipSuccess && nsjobs > 0)

@@ -144,6 +144,35 @@ def test_moe_one_token_one_call_matches_two_phases(gpu, fmt, dim, inter, topk, o
         assert u.max() <= 1 and u.mean() < 0.02, (u.max(), u.mean())
 
 
+@pytest.mark.parametrize("dim,inter", [(1024, 512), (7168, 2048)])
+def test_moe_token_classes_in_one_launch_match_one_token_calls(gpu, dim, inter):
+    # four tokens whose experts take one, two and four tokens (the shared expert every token): the
+    # jobs of all three classes share one gate/up and one down launch, and each token's output must
+    # equal, bit for bit, a call with that token alone (one-token kernels; each token's sums use the
+    # same lanes in the same order); the first shape is also checked against the oracle
+    topk, n = 6, 14
+    experts = [make_expert(ops.FP4, dim, inter, seed=1300 + 3 * i, gpu=gpu) for i in range(n)]
+    slots = [e[0] for e in experts]
+    pick = [[0, 1, 2, 3, 4, 5], [0, 1, 7, 8, 9, 10], [0, 11, 12, 6, 2, 3], [0, 7, 11, 12, 8, 9]]
+    w = [[0.3, 0.2, 0.15, 0.15, 0.1, 0.1]] * 4
+    x = data.activation(4, dim, seed=131).to(gpu)
+    kw = dict(shared=n - 1, limit=10.0)
+    y = ops.moe_experts(x, slots, pick, w, ops.FP4, dim, inter, **kw)
+    for t in range(4):
+        y1 = ops.moe_experts(x[t:t + 1], slots, pick[t:t + 1], w[t:t + 1], ops.FP4, dim, inter, **kw)
+        assert torch.equal(y[t], y1[0]), f"token {t}"
+    if dim == 1024:
+        packed = [np.concatenate([p.ravel() for p in e[1]]) for e in experts]
+        wn, xf = np.array(w, np.float32), x.float().cpu().numpy()
+        want = oracle.moe_fp4([[packed[i] for i in row] for row in pick], wn, packed[n - 1], dim, inter, xf, limit=10.0)
+        terms = np.zeros((4, dim))
+        for i, row in enumerate(pick):
+            for p, e in enumerate(row + [n - 1]):
+                terms[i] += np.abs(oracle.expert_ffn_fp4(packed[e], dim, inter, xf[i], wn[i, p] if p < topk else 1.0,
+                                                         limit=10.0))
+        assert_moe_sum(np_(y), want, terms)
+
+
 def test_moe_experts_shared_token_groups(gpu):
     # six tokens all routed to the same two experts: jobs of <= 4 tokens are split (4 + 2)
     dim, inter, topk = 256, 128, 2
