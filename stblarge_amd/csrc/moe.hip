@@ -163,14 +163,15 @@ __device__ __forceinline__ void chunk_dot_lane(float (&s)[M], const u32x4 (&w)[C
 // nothing and add zeros.
 template <WFmt F, int M, int R, bool DW, int CPL = 1>
 __device__ __forceinline__ void gateup_job(const MoeJob &J, const ExpertLayout &L, const uint16_t *__restrict__ x,
-                                           uint16_t *__restrict__ h, int dim, int inter, float limit, int official) {
+                                           uint16_t *__restrict__ h, int dim, int inter, float limit, int official,
+                                           int tile0 = -1) {
     static_assert(CPL == 1 || !WTraits<F>::fp4, "two chunks per lane: FP8 rows");
     constexpr int CH = WTraits<F>::CH * CPL;  // elements per lane
     const SlotMat<F> G(J.slot, L, 0, dim, inter), U(J.slot, L, 1, dim, inter);
     const int lane = threadIdx.x & 63, c = (threadIdx.x >> 6) * 64 + lane, nch = dim / CH;
     const bool active = c < nch;
     const int cc = active ? c : 0;
-    const int row0 = blockIdx.x * R;
+    const int row0 = tile0 < 0 ? (int)blockIdx.x * R : tile0;  // the tile's first row
     const int m = J.m;
     // the output row and route weight of the (token, row) this thread may finish, read now: indexed
     // by thread they are memory loads, which at the end would add a round trip to every workgroup
@@ -286,14 +287,15 @@ __global__ __launch_bounds__(512) void k_moe_gateup_mix(MoeJobs jobs, ExpertLayo
 // holding the unrounded sum when out_f32). DW as in k_moe_gateup.
 template <WFmt F, int M, int R, bool DW, int CPL = 1>
 __device__ __forceinline__ void down_job(const MoeJob &J, const ExpertLayout &L, const uint16_t *__restrict__ h,
-                                         void *__restrict__ o, int dim, int inter, int official, int out_f32) {
+                                         void *__restrict__ o, int dim, int inter, int official, int out_f32,
+                                         int tile0 = -1) {
     static_assert(CPL == 1 || !WTraits<F>::fp4, "two chunks per lane: FP8 rows");
     constexpr int CH = WTraits<F>::CH * CPL;  // elements per lane
     const SlotMat<F> D(J.slot, L, 2, dim, inter);
     const int lane = threadIdx.x & 63, c = (threadIdx.x >> 6) * 64 + lane, nch = inter / CH;
     const bool active = c < nch;
     const int cc = active ? c : 0;
-    const int row0 = blockIdx.x * R;
+    const int row0 = tile0 < 0 ? (int)blockIdx.x * R : tile0;  // the tile's first row
     const int m = J.m;
     const int pair_out = J.pair[min((int)threadIdx.x / R, M - 1)];  // read early, as in gateup_job
     __shared__ float red[kMaxWaves][M * R];
@@ -380,9 +382,18 @@ __global__ __launch_bounds__(512) void k_moe_gateup_any(MoeJobs jobs, ExpertLayo
                                                         uint16_t *__restrict__ h, int dim, int inter, float limit,
                                                         int official) {
     const MoeJob &J = jobs.j[blockIdx.y];
-    if (J.m == 1) gateup_job<F, 1, R, DW>(J, L, x, h, dim, inter, limit, official);
-    else if (J.m == 2) gateup_job<F, 2, R, DW>(J, L, x, h, dim, inter, limit, official);
-    else gateup_job<F, 4, R, DW>(J, L, x, h, dim, inter, limit, official);
+    if (J.m == 1) {
+        gateup_job<F, 1, R, DW>(J, L, x, h, dim, inter, limit, official);
+    } else if (J.m == 2) {
+        gateup_job<F, 2, R, DW>(J, L, x, h, dim, inter, limit, official);
+    } else {
+        // the 4-token body in passes of 2 rows, so that it needs no more registers than the others
+#pragma unroll 1
+        for (int p = 0; p < R; p++) {
+            if (p > 0) __syncthreads();  // the pass before has read its sums out of LDS
+            gateup_job<F, 4, 1, DW>(J, L, x, h, dim, inter, limit, official, (int)blockIdx.x * R + p);
+        }
+    }
 }
 
 template <WFmt F, int R, bool DW>
@@ -390,9 +401,17 @@ __global__ __launch_bounds__(512) void k_moe_down_any(MoeJobs jobs, ExpertLayout
                                                       void *__restrict__ o, int dim, int inter, int official,
                                                       int out_f32) {
     const MoeJob &J = jobs.j[blockIdx.y];
-    if (J.m == 1) down_job<F, 1, R, DW>(J, L, h, o, dim, inter, official, out_f32);
-    else if (J.m == 2) down_job<F, 2, R, DW>(J, L, h, o, dim, inter, official, out_f32);
-    else down_job<F, 4, R, DW>(J, L, h, o, dim, inter, official, out_f32);
+    if (J.m == 1) {
+        down_job<F, 1, R, DW>(J, L, h, o, dim, inter, official, out_f32);
+    } else if (J.m == 2) {
+        down_job<F, 2, R, DW>(J, L, h, o, dim, inter, official, out_f32);
+    } else {
+#pragma unroll 1
+        for (int p = 0; p < R / 2; p++) {
+            if (p > 0) __syncthreads();
+            down_job<F, 4, 2, DW>(J, L, h, o, dim, inter, official, out_f32, (int)blockIdx.x * R + 2 * p);
+        }
+    }
 }
 
 // ---- combine ------------------------------------------------------------------------------------
