@@ -374,9 +374,9 @@ __global__ __launch_bounds__(512) void k_moe_down_mix(MoeJobs jobs, ExpertLayout
 // Jobs of 1, 2 and 3-4 tokens of one format in one gate/up and one down launch: each workgroup
 // takes its job's token class (workgroup-uniform). The few multi-token jobs of a step (the shared
 // expert, which every token takes; experts two tokens picked) then compute while the one-token jobs
-// stream, instead of running in launches of their own at a fraction of the bandwidth. The kernel's
-// registers are those of the 4-token body, so a launch of one-token jobs only keeps k_moe_gateup /
-// k_moe_down.
+// stream, instead of running in launches of their own at a fraction of the bandwidth. The kernel
+// needs more registers than the one-token body alone, so a launch of one-token jobs only keeps
+// k_moe_gateup / k_moe_down.
 template <WFmt F, int R, bool DW>
 __global__ __launch_bounds__(512) void k_moe_gateup_any(MoeJobs jobs, ExpertLayout L, const uint16_t *__restrict__ x,
                                                         uint16_t *__restrict__ h, int dim, int inter, float limit,
@@ -387,7 +387,8 @@ __global__ __launch_bounds__(512) void k_moe_gateup_any(MoeJobs jobs, ExpertLayo
     } else if (J.m == 2) {
         gateup_job<F, 2, R, DW>(J, L, x, h, dim, inter, limit, official);
     } else {
-        // the 4-token body in passes of 2 rows, so that it needs no more registers than the others
+        // the 4-token body in passes of one row (down: two rows), so that the kernel needs no more
+        // registers than for the 2-token body
 #pragma unroll 1
         for (int p = 0; p < R; p++) {
             if (p > 0) __syncthreads();  // the pass before has read its sums out of LDS
