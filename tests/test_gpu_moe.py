@@ -579,6 +579,31 @@ def test_moe_experts_byte_scales_fallback(gpu):
         assert bf16_ulps(y, want).max() <= 1
 
 
+def test_moe_random_steps_match_one_token_calls(gpu):
+    # random steps of one expert format (2-16 tokens, top-1..8 of up to 12 experts, with or without a
+    # shared expert): whatever launches a step's jobs take (per token class, or every class in one
+    # launch), each token's output equals a call with that token alone bit for bit, since every
+    # (token, expert) sum uses the same lanes in the same order
+    rng = np.random.default_rng(77)
+    for case in range(9):
+        fmt = (ops.FP4, ops.FP8, ops.FP8_E8M0)[case % 3]
+        dim, inter = int(256 * rng.integers(1, 5)), int(128 * rng.integers(1, 5))
+        t, topk = int(rng.integers(2, 17)), int(rng.integers(1, 9))
+        nr = int(rng.integers(topk, topk + 5))
+        slots = [make_expert(fmt, dim, inter, seed=7000 + 100 * case + 3 * i, gpu=gpu)[0] for i in range(nr + 1)]
+        sh = nr if rng.random() < 0.7 else -1
+        pick = [[int(v) for v in rng.choice(nr, size=topk, replace=False)] for _ in range(t)]
+        w = (rng.random((t, topk)) / topk).astype(np.float32).tolist()
+        official = bool(rng.integers(0, 2))
+        x = data.activation(t, dim, seed=700 + case).to(gpu)
+        kw = dict(shared=sh, limit=7.0, official=official)
+        print(f"case {case}: fmt {fmt} {dim}x{inter} t={t} topk={topk} experts={nr} shared={sh}", flush=True)
+        y = ops.moe_experts(x, slots, pick, w, fmt, dim, inter, **kw)
+        for ti in range(t):
+            y1 = ops.moe_experts(x[ti:ti + 1], slots, pick[ti:ti + 1], w[ti:ti + 1], fmt, dim, inter, **kw)
+            assert torch.equal(y[ti], y1[0]), f"case {case} token {ti}"
+
+
 def test_moe_random_configurations(gpu):
     # 24 random expert steps over the three expert formats, a shared expert of the routed format or
     # of the engine's FP8 E8M0 one, raw and official numerics, SwiGLU limit or none, 1-16 tokens,
