@@ -251,8 +251,11 @@ def ffn_workload(torch, fmt, steps, warmup, use_graph=True):
     alg = wbytes + 2 * dim + 2 * dim
     gbs = alg / (ms * 1e-3) / 1e9
     name = "fp4" if fmt == ops.FP4 else "fp8"
+    # the weight bytes of its two launches (gate + up, then down): the bare reads of those byte counts,
+    # one launch each, are the floor of a plan whose second launch needs the first's output
+    launch_bytes = [2 * ops._mat_bytes(fmt, inter, dim), ops._mat_bytes(fmt, dim, inter)]
     return {"workload": f"{name}_expert_ffn_7168x2048_m1", "ms_per_step": ms, "steps": n, "alg_bytes": alg,
-            "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS, "slot_copies": copies}
+            "GB_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS, "slot_copies": copies, "launch_bytes": launch_bytes}
 
 
 def moe_workload(torch, tokens, steps, warmup_steps):
@@ -772,11 +775,18 @@ def read_floor_workload(torch, nbytes, steps, warmup):
 
 def attach_floor(row, floors):
     """Adds the row's fraction of the bare-read floor for its byte count (the same bytes in one
-    launch, timed the same way) next to its fraction of peak."""
+    launch, timed the same way) next to its fraction of peak; for a row of several dependent launches
+    (launch_bytes), also the sum of the bare reads of each launch's bytes and the row's time against
+    it."""
     f = floors.get(int(row["alg_bytes"]))
     if f:
         row["read_floor_GB_s"] = f["GB_s"]
         row["frac_of_read_floor"] = row["GB_s"] / f["GB_s"]
+    parts = [floors.get(int(b)) for b in row.get("launch_bytes", ())]
+    if parts and all(parts):
+        t = sum(p["ms_per_step"] for p in parts)
+        row["launch_floors_us"] = 1e3 * t
+        row["frac_of_launch_floors"] = t / row["ms_per_step"]
     return row
 
 
@@ -1145,15 +1155,20 @@ def main():
         report(r)
     if args.only in ("all", "fp4", "gemv", "batch", "ffn", "floor"):
         # bare-read floors at the single-launch rows' byte counts: FP4 / FP8 GEMV, FP4 / FP8 expert
-        # FFN, 16 FP4 / FP8 GEMVs per launch, 64 FP4 / FP8 GEMVs per launch
+        # FFN, 16 FP4 / FP8 GEMVs per launch, 64 FP4 / FP8 GEMVs per launch; then the FFN launches'
+        # own (FP4 gate + up, down; FP8 gate + up, down)
         floors = {}
-        for nbytes in (7817216, 14702080, 23425024, 44079616, 125075456, 235233280, 500301824, 940933120):
+        for nbytes in (7817216, 14702080, 23425024, 44079616, 125075456, 235233280, 500301824, 940933120,
+                       15597568, 7798784, 29367296, 14683648):
             r = read_floor_workload(torch, nbytes, K, W)
             floors[nbytes] = r
             report(r)
         for row in [head] + list(extra.values()):
             if "alg_bytes" in row and not row["workload"].startswith("read_floor"):
                 attach_floor(row, floors)
+                if "frac_of_launch_floors" in row:
+                    print(f"# {row['workload']}: {100 * row['frac_of_launch_floors']:.0f}% of its launches' bare reads "
+                          f"({row['launch_floors_us']:.2f} us)", file=sys.stderr, flush=True)
         if "frac_of_read_floor" in head:
             print(f"# headline: {100 * head['frac_of_read_floor']:.1f}% of the bare read of its bytes",
                   file=sys.stderr, flush=True)
