@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import oracle
-from stblarge_amd import data, ops
+from stblarge_amd import _lib, data, ops
 from stblarge_amd.moe import ExpertCache, MoELayer
 from util import assert_gemv, assert_moe_sum, bf16_ulps, np_, read_device
 
@@ -229,6 +229,87 @@ def test_expert_ffn_fp8_e8m0(gpu, dim, inter, official):
     for t in range(2):
         o, raw = oracle.expert_ffn_deq(*mats, x[t].float().numpy(), 0.6, 10.0, official, raw=True)
         assert_gemv(y32[t], y16[t], raw)
+
+
+def _ffn_with_h(slot, x, fmt, dim, inter, w, limit, official, out_f32):
+    """stbl_amd_expert_ffn through the C-ABI with a work buffer of the test's own, which holds the
+    SwiGLU intermediates h (bf16 [m][inter], before the official act_quant) after the call."""
+    m = x.shape[0]
+    y = torch.empty((m, dim), dtype=torch.float32 if out_f32 else torch.bfloat16, device=x.device)
+    work = torch.zeros(m * inter, dtype=torch.bfloat16, device=x.device)
+    _lib.check(_lib.load().stbl_amd_expert_ffn(fmt, ops._ptr(y), ops._ptr(slot), ops._ptr(x), m, dim, inter, float(w),
+                                               float(limit), int(official), int(out_f32), ops._ptr(work),
+                                               ops._stream()), "expert_ffn")
+    return np_(y), np_(work).reshape(m, inter)
+
+
+def _h_candidates(g, u, abs_g, abs_u, w, limit):
+    """Every value the SwiGLU intermediate bf16(silu(g) * u * w) may take when the gate and up sums
+    carry the rounding of an fp32 accumulation in some order: each exact sum (double) moves by up to
+    2^-17 of its sum of absolute terms (128 fp32 rounding units; a kernel's sum of one output passes
+    through fewer than 50 fp32 additions), so it rounds to either bf16 neighbour where a rounding
+    midpoint lies that close; and the product moves by 2^-20 of itself (expf is a library routine on
+    either side). That worst-case band admits both neighbours for about half the elements at K = 5120
+    to 7168 (a sixth at K = 256), so it only bounds where a difference may sit; the test also caps
+    the elements that differ from the exact oracle's h. Returns the candidate arrays (the exact
+    oracle's first)."""
+    cands = [oracle.swiglu(oracle.bf16_round(g.astype(np.float32)), oracle.bf16_round(u.astype(np.float32)), w, limit)]
+    for gs in (-1.0, 1.0):
+        for us in (-1.0, 1.0):
+            gb = oracle.bf16_round((g + gs * 2.0 ** -17 * abs_g).astype(np.float32))
+            ub = oracle.bf16_round((u + us * 2.0 ** -17 * abs_u).astype(np.float32))
+            for ws in (1 - 2.0 ** -20, 1 + 2.0 ** -20):
+                cands.append(oracle.swiglu(gb, ub, w * ws, limit))
+    return cands
+
+
+# (format, dim, inter, tokens, route weight, limit, official, weight seed, x seed, x row): random
+# configurations, and two that a longer randomized run found, where one gate sum lies at a bf16
+# rounding midpoint (0 and 19 fp32 units from it) and the GPU's h takes the other neighbour, which
+# moves a few percent of the outputs by up to 6 bf16 steps through the down product
+_STAGE_CASES = [
+    (ops.FP8, 256, 512, 1, 1.0, 7.0, True, 9001, 1, 0),
+    (ops.FP4, 768, 384, 1, 0.5595918297767639, 0.0, False, 6203, 12, 1),
+    (ops.FP4, 7168, 2048, 1, 1.0, 0.0, False, 11, 11, 0),
+    (ops.FP4, 1024, 512, 4, 0.37, 7.0, True, 12, 12, 0),
+    (ops.FP8, 2048, 1024, 3, 0.8, 0.0, True, 13, 13, 0),
+    (ops.FP8_E8M0, 5120, 2304, 1, 1.0, 10.0, True, 14, 14, 0),
+    (ops.FP8_E8M0, 768, 256, 2, 0.25, 0.0, False, 15, 15, 0),
+    (ops.FP4, 512, 128, 3, 0.6, 10.0, False, 16, 16, 0),
+]
+
+
+@pytest.mark.parametrize("case", range(len(_STAGE_CASES)))
+def test_expert_ffn_stage_by_stage(gpu, case):
+    # The FFN checked one stage at a time, so that no intermediate rounding can hide in a tolerance:
+    # (1) h (read from the work buffer) equals the exact oracle's h except in at most 1% of its
+    # elements, each of which is one of the values the gate/up sums admit under fp32 accumulation
+    # (_h_candidates: a gate sum one bf16 step over moves h by one or two steps); (2) the down product
+    # of the GPU's own h (act_quant'ed as the official numerics do) meets the GEMV bar, fp32 within
+    # 1e-3 and bf16 outputs at most one step from the exact product. (stbl/model.cu:516-547,
+    # stbl/kernels.cu:444-464)
+    fmt, dim, inter, m, w, limit, official, wseed, xseed, row = _STAGE_CASES[case]
+    slot, parts = make_expert(fmt, dim, inter, seed=wseed, gpu=gpu)
+    gw, uw, dw = deq_parts(fmt, parts)
+    x = data.activation(max(m, row + 1), dim, seed=xseed)[row:row + m]
+    y16, h = _ffn_with_h(slot, x.to(gpu), fmt, dim, inter, w, limit, official, False)
+    y32, h2 = _ffn_with_h(slot, x.to(gpu), fmt, dim, inter, w, limit, official, True)
+    assert np.array_equal(h, h2)
+    xs = x.float().numpy()
+    xb = oracle.act_quant(xs, 32, True)[2] if official else xs
+    g, u = oracle.gemm(xb, gw), oracle.gemm(xb, uw)
+    abs_g, abs_u = oracle.gemm(np.abs(xb), np.abs(gw)), oracle.gemm(np.abs(xb), np.abs(uw))
+    cands = _h_candidates(g, u, abs_g, abs_u, w, limit)
+    diff = h != cands[0]
+    assert diff.mean() <= 0.01, f"{diff.mean():.4f} of h values differ from the oracle's"
+    ok = np.zeros(h.shape, bool)
+    for c in cands:
+        ok |= h == c
+    assert ok.all(), f"{int((~ok).sum())} h values outside what the gate/up sums admit"
+    hq = oracle.act_quant(h, 32, True)[2] if official else h
+    raw = oracle.gemm(hq, dw)
+    for t in range(m):
+        assert_gemv(y32[t], y16[t], raw[t])
 
 
 def test_moe_experts_routed_picks_of_the_shared_slot_and_phases(gpu):
