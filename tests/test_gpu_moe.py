@@ -379,6 +379,21 @@ def test_route_sqrt_softplus(gpu):
     assert np.allclose(np_(w), ow, rtol=8 * 2.0 ** -24, atol=0)
 
 
+def test_route_scores_over_the_logit_range(gpu):
+    # both score functions at 4001 logits over fp32's whole exp range [-87, 87]: the device scores
+    # within 3 fp32 ulps of the oracle's (host libm, within 1 ulp of exact; the device's are within
+    # 1.6). The library is built so that the compiler's expf / log1pf expansions keep their range
+    # reduction as written; with x * log2(e) - n fused into one FMA the device sigmoid was 43 ulps
+    # off at |logit| ~ 70 and 5 ulps within |logit| < 10
+    lg = torch.linspace(-87, 87, 4001)
+    for fn in (ops.SCORE_SIGMOID, ops.SCORE_SQRT_SOFTPLUS):
+        _, _, sc = ops.route(lg[:, None].contiguous().to(gpu), 1, want_scores=True, score_fn=fn)
+        osc, _, _ = oracle.route(lg[:, None].numpy(), 1, score_fn=fn)
+        got, want = np_(sc)[:, 0], osc[:, 0]
+        ulps = np.abs(got.astype(np.float64) - want) / np.spacing(np.abs(want)).astype(np.float64)
+        assert ulps.max() <= 3, f"score_fn {fn}: {ulps.max():.1f} ulps at logit {float(lg[int(ulps.argmax())])}"
+
+
 def test_stbl_sqrt_softplus(gpu):
     # the reference ABI's in-place scores (stbl/test_kernels.py:208-211: 384 values of N(0, 8), bar
     # 1e-6 of max |want|); also bit-identical to the scores stbl_amd_route reports for the same logits
@@ -469,6 +484,49 @@ def test_cache_lookup_begin_end(gpu):
     cache.mark_used()
     assert cache.lookahead()["misses"] == 2
     cache.close()
+
+
+def check_route(gids, gw, scores, oids, ow, bias):
+    """Device router output against the oracle's. The scores' exp / log1p are library routines on
+    either side and may differ in the last fp32 bit, so where the ids differ the two keys (score +
+    bias, as the oracle computes them) must be a near tie, within 4 fp32 ulps: an equal pair in the
+    other order, or the other one of a tie at the k-th place. Every other id matches exactly, and
+    where the ids match the weights are within 8 fp32 ulps of the row's largest weight (NaN where
+    the oracle's are)."""
+    key = (scores + (bias if bias is not None else np.float32(0))).astype(np.float32)
+    for r in range(gids.shape[0]):
+        for j in np.nonzero(gids[r] != oids[r])[0]:
+            a, b = key[r, gids[r, j]], key[r, oids[r, j]]
+            assert abs(float(a) - float(b)) <= 4 * float(np.spacing(np.float32(max(abs(a), abs(b))))), \
+                f"row {r} place {j}: id {gids[r, j]} (key {a}) against {oids[r, j]} (key {b})"
+    same = gids == oids
+    assert np.array_equal(np.isnan(gw)[same], np.isnan(ow)[same])
+    tol = 8 * 2.0 ** -24 * np.nanmax(np.abs(ow), axis=1, keepdims=True, initial=0)
+    fin = same & ~np.isnan(ow)
+    assert np.all(np.abs(gw - ow)[fin] <= np.broadcast_to(tol, ow.shape)[fin])
+
+
+def test_route_random(gpu):
+    # 300 random routers (stbl/model.cu:430-452): 1-32 tokens, 1-1024 experts, top-1..32, both score
+    # functions, bias or none, route scales; logits normal, quantized to quarters (ties), 5% NaN, or
+    # far in the tails (saturated sigmoids, softplus past its threshold) -- checked by check_route
+    rng = np.random.default_rng(31337)
+    for case in range(300):
+        t, e = int(rng.integers(1, 33)), int(rng.integers(1, 1025))
+        topk, fn = int(rng.integers(1, min(32, e) + 1)), int(rng.integers(0, 2))
+        scale = float(rng.choice([1.0, 2.5, 0.3]))
+        lg = rng.normal(0, float(rng.choice([0.5, 3.0, 12.0])), (t, e)).astype(np.float32)
+        if case % 4 == 1:
+            lg = np.round(lg * 4) / 4
+        elif case % 4 == 2:
+            lg[rng.random((t, e)) < 0.05] = np.nan
+        elif case % 4 == 3:
+            lg = lg * np.float32(10)
+        bias = rng.normal(0, 0.01, e).astype(np.float32) if rng.random() < 0.5 else None
+        ids, w = ops.route(torch.from_numpy(lg).to(gpu), topk, None if bias is None else torch.from_numpy(bias).to(gpu),
+                           route_scale=scale, score_fn=fn)
+        sc, oids, ow = oracle.route(lg, topk, bias, scale, score_fn=fn)
+        check_route(np_(ids), np_(w), sc, oids, ow, bias)
 
 
 def test_route_nan_logits(gpu):
