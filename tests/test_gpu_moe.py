@@ -456,6 +456,33 @@ def test_cache_lru_matches_oracle(gpu):
     cache.close()
 
 
+def test_cache_lru_random_configurations(gpu):
+    # 10 random caches (2-199 experts, 1-48 slots, 1-16 distinct ids a lookup, uniform or Zipf(1.1)
+    # picks, 200 lookups each): hits equal oracle.lru_simulate's (stbl/model.cu:347-422) and every
+    # looked-up slot holds its expert's bytes
+    rng = np.random.default_rng(3)
+    for case in range(10):
+        n, slots, sb = int(rng.integers(2, 200)), int(rng.integers(1, 49)), 256 * int(rng.integers(16, 64))
+        width = int(rng.integers(1, min(slots, n, 16) + 1))
+        p = None
+        if case % 2:
+            p = 1.0 / np.arange(1, n + 1) ** 1.1
+            p /= p.sum()
+        steps = [[int(v) for v in rng.choice(n, size=int(rng.integers(1, width + 1)), replace=False, p=p)]
+                 for _ in range(200)]
+        cache = ExpertCache(slots, sb, pinned_pool(n, sb), n)
+        for si, (ids, (hits, _, _)) in enumerate(zip(steps, oracle.lru_simulate(steps, slots))):
+            ptrs, got_hits, nmiss = cache.lookup(ids)
+            cache.mark_used()
+            torch.cuda.synchronize()
+            assert list(got_hits) == hits and nmiss == hits.count(False), f"case {case} step {si}"
+            for e, q in zip(ids, ptrs):
+                assert read_device(q, 8).tolist()[:4] == [e, 255 - e, 7, 9], f"case {case} step {si} expert {e}"
+        st = cache.stats()
+        assert st["hits"] + st["misses"] == sum(len(s) for s in steps)
+        cache.close()
+
+
 def test_cache_lookup_begin_end(gpu):
     # the lookup in two calls: begin maps and queues the refills and says which slots may be read at
     # once (pool tier: the hits), end makes the compute stream wait for the refills
