@@ -770,6 +770,54 @@ def test_moe_random_steps_match_one_token_calls(gpu):
             assert torch.equal(y[ti], y1[0]), f"case {case} token {ti}"
 
 
+def test_moe_and_gemm_from_concurrent_threads_and_streams(gpu):
+    # four host threads, each on its own stream, run MoE steps (FP4 routed + FP8 E8M0 shared, one and
+    # four tokens: the mixed and merged launches, whose job tables are built in per-thread host
+    # arrays) and M = 64 GEMMs with their own work buffers, 10 times each; every result is
+    # bit-identical to the same call made alone
+    import threading
+
+    dim, inter, n, topk = 1024, 512, 8, 4
+    slots = [make_expert(ops.FP4, dim, inter, seed=3100 + 3 * i, gpu=gpu)[0] for i in range(n)]
+    slots.append(make_expert(ops.FP8_E8M0, dim, inter, seed=3190, gpu=gpu)[0])
+    gw = data.weight(2048, 1024, seed=3200)
+    gc, gs = (torch.from_numpy(a).to(gpu) for a in oracle.quant_fp4(gw.numpy()))
+    rng = np.random.default_rng(31)
+    jobs = []
+    for i in range(4):
+        t = 1 if i % 2 == 0 else 4
+        pick = [[int(v) for v in rng.choice(n, size=topk, replace=False)] for _ in range(t)]
+        w = (rng.random((t, topk)) / topk).astype(np.float32).tolist()
+        jobs.append((data.activation(t, dim, seed=3300 + i).to(gpu), pick, w, data.activation(64, 1024, seed=3400 + i).to(gpu)))
+    kw = dict(shared=n, limit=10.0, official=True, shared_fmt=ops.FP8_E8M0)
+    run = lambda x, pick, w, xg: (ops.moe_experts(x, slots, pick, w, ops.FP4, dim, inter, **kw),
+                                  ops.gemm(gc, gs, xg, ops.FP4, 32))
+    alone = [run(*j) for j in jobs]
+    torch.cuda.synchronize()
+    got, errors = [None] * 4, []
+
+    def work(i):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                out = None
+                for _ in range(10):
+                    out = run(*jobs[i])
+            s.synchronize()
+            got[i] = out
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    ts = [threading.Thread(target=work, args=(i,)) for i in range(4)]
+    for th in ts:
+        th.start()
+    for th in ts:
+        th.join()
+    assert not errors, errors
+    for (am, ag), (gm, gg) in zip(alone, got):
+        assert torch.equal(am, gm) and torch.equal(ag, gg)
+
+
 def test_moe_random_configurations(gpu):
     # 24 random expert steps over the three expert formats, a shared expert of the routed format or
     # of the engine's FP8 E8M0 one, raw and official numerics, SwiGLU limit or none, 1-16 tokens,
