@@ -23,6 +23,10 @@ pytestmark = pytest.mark.gpu
 def test_act_quant_e4m3_bit_exact(gpu, block):
     x = (data.normal((64, 7168), 1.0, seed=block) * torch.logspace(-2, 2, 7168)).to(torch.bfloat16)
     x[3, :block] = 0
+    # non-finite values: a block holding an infinity takes the scale +Inf (its codes are x / Inf: 0,
+    # and NaN clamped to -448 for the infinity itself); a NaN is skipped by the block's maximum and
+    # clamps to -448 (fmaxf, as the engine's stbl/kernels.cu:56-63 and the oracle do)
+    x[5, 10], x[6, block + 3], x[7, 2 * block + 1] = float("inf"), float("-inf"), float("nan")
     codes, sc = ops.act_quant_e4m3(x.to(gpu), block)
     oc, os_, _ = oracle.act_quant(x.float().numpy(), block, True)
     assert np.array_equal(np_(codes), oc)
