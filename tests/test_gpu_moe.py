@@ -535,8 +535,9 @@ def check_route(gids, gw, scores, oids, ow, bias):
 
 def test_route_random(gpu):
     # 300 random routers (stbl/model.cu:430-452): 1-32 tokens, 1-1024 experts, top-1..32, both score
-    # functions, bias or none, route scales; logits normal, quantized to quarters (ties), 5% NaN, or
-    # far in the tails (saturated sigmoids, softplus past its threshold) -- checked by check_route
+    # functions, bias or none, route scales; logits normal, quantized to quarters (ties), 5% NaN with
+    # 2% +Inf and 2% -Inf, or far in the tails (saturated sigmoids, softplus past its threshold) --
+    # checked by check_route
     rng = np.random.default_rng(31337)
     for case in range(300):
         t, e = int(rng.integers(1, 33)), int(rng.integers(1, 1025))
@@ -547,6 +548,8 @@ def test_route_random(gpu):
             lg = np.round(lg * 4) / 4
         elif case % 4 == 2:
             lg[rng.random((t, e)) < 0.05] = np.nan
+            lg[rng.random((t, e)) < 0.02] = np.inf
+            lg[rng.random((t, e)) < 0.02] = -np.inf
         elif case % 4 == 3:
             lg = lg * np.float32(10)
         bias = rng.normal(0, 0.01, e).astype(np.float32) if rng.random() < 0.5 else None
