@@ -946,7 +946,8 @@ def make_line(head, extra, cpu, timing, warmup, traffic=None, profiled=None):
     gbs = head["GB_s"]
     target = {}
     for key, name in (("fp4", "fp4_gemv_7168x2048_m1"), ("fp8", "fp8_gemv_7168x2048_m1"),
-                      ("fp4_batch16", "fp4_gemv_batch16_7168x2048_m1"), ("fp8_batch16", "fp8_gemv_batch16_7168x2048_m1")):
+                      ("fp4_batch16", "fp4_gemv_batch16_7168x2048_m1"), ("fp8_batch16", "fp8_gemv_batch16_7168x2048_m1"),
+                      ("fp4_batch64", "fp4_gemv_batch64_7168x2048_m1"), ("fp8_batch64", "fp8_gemv_batch64_7168x2048_m1")):
         if name in extra:
             target[key] = {"us": _r(extra[name]["ms_per_step"] * 1e3), "GB_s": _r(extra[name]["GB_s"]),
                            "frac": _r(extra[name]["frac_hbm_peak"])}

@@ -96,7 +96,7 @@ def test_stdout_line_is_compact_and_parses():
     assert d["roofline"]["traffic"] == 7982353 and d["roofline"]["profiled"] == prof
     assert abs(d["roofline"]["isolated_frac"] - 7817216 / 3.81234567e-6 / 1e9 / 8000.0) < 1e-4
     assert d["cpu_baseline"]["kind"] == "port" and d["cpu_baseline"]["cores"] == 16
-    assert set(d["target_7168x2048"]) == {"fp4", "fp8", "fp4_batch16", "fp8_batch16"}
+    assert set(d["target_7168x2048"]) == {"fp4", "fp8", "fp4_batch16", "fp8_batch16", "fp4_batch64", "fp8_batch64"}
     assert set(d["extra"]) == set(bench.LINE_ROWS)
     assert d["extra"]["fp4_gemm_q_m64_2048x7168"][3] == 240.0  # TFLOP/s, 3 significant digits
     assert d["extra"]["moe_layer_t1_fp4_256x_top8_lru64"]["hit"] == 0.679
