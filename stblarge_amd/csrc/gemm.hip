@@ -52,15 +52,16 @@ __global__ __launch_bounds__(256) void k_act_quant_e4m3(const uint16_t *__restri
     const int lanes = block >> 3;  // 4 or 16, a power of two
     for (int o = 1; o < lanes; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, kWave));
     const float s = pow2_ceil(fmaxf(a, 1e-4f) * (1.0f / 448.0f));
-    const float inv = __uint_as_float((uint32_t)(254 - ((__float_as_uint(s) >> 23) & 0xffu)) << 23);  // 1/s, exact
-    const bool s_inf = __builtin_isinf(s);  // a block holding an infinity: 1/s is no power of two, so divide
+    // 1/s, exact; 0 for s = +Inf (a block holding an infinity), where x * 0 is x / s: a signed zero for
+    // a finite x, NaN for an infinite one
+    const float inv = __builtin_isinf(s) ? 0.f : __uint_as_float((uint32_t)(254 - ((__float_as_uint(s) >> 23) & 0xffu)) << 23);
     uint32_t w[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         // x / s is exact (s is a power of two); the clamp is ref/kernel.py:41's
         float q[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) q[e] = fminf(fmaxf(s_inf ? f[4 * j + e] / s : f[4 * j + e] * inv, -448.f), 448.f);
+        for (int e = 0; e < 4; e++) q[e] = fminf(fmaxf(f[4 * j + e] * inv, -448.f), 448.f);
         int p = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
         p = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], p, true);
         w[j] = (uint32_t)p;
@@ -113,16 +114,16 @@ __global__ __launch_bounds__(64) void k_act_quant_e4m3_ops(const uint16_t *__res
 #pragma unroll
     for (int h = 0; h < 2; h++) {
         const float sc = pow2_ceil(fmaxf(a[h], 1e-4f) * (1.0f / 448.0f));
-        const float inv = __uint_as_float((uint32_t)(254 - ((__float_as_uint(sc) >> 23) & 0xffu)) << 23);  // 1/sc, exact
-        const bool sc_inf = __builtin_isinf(sc);  // as in k_act_quant_e4m3
+        // 1/sc, exact, or 0 for sc = +Inf, as in k_act_quant_e4m3
+        const float inv =
+            __builtin_isinf(sc) ? 0.f : __uint_as_float((uint32_t)(254 - ((__float_as_uint(sc) >> 23) & 0xffu)) << 23);
         u32x4 out;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             // x / sc is exact (sc is a power of two); the clamp is ref/kernel.py:41's
             float q[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                q[e] = fminf(fmaxf(sc_inf ? f[h][4 * j + e] / sc : f[h][4 * j + e] * inv, -448.f), 448.f);
+            for (int e = 0; e < 4; e++) q[e] = fminf(fmaxf(f[h][4 * j + e] * inv, -448.f), 448.f);
             int p = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
             p = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], p, true);
             out[j] = ok ? (uint32_t)p : 0u;

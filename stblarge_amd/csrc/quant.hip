@@ -43,10 +43,11 @@ __global__ void k_act_quant_fp8_inplace(float *x, int n_blocks) {
     a = dpp_max(a, 3);
     a = fmaxf(a, __shfl_xor(a, 16, kWave));  // lanes l and l ^ 16
     const float s = pow2_ceil(fmaxf(a, 1e-4f) * (1.0f / 448.0f));
-    const float inv = __uint_as_float((254u - ((__float_as_uint(s) >> 23) & 0xffu)) << 23);
+    // 1/s, exact; 0 for s = +Inf (a block holding an infinity), where v * 0 is v / s: a signed zero for
+    // a finite v, NaN for an infinite one
+    const float inv = __builtin_isinf(s) ? 0.f : __uint_as_float((254u - ((__float_as_uint(s) >> 23) & 0xffu)) << 23);
     if (ok) {
-        // (a block holding an infinity has s = +Inf, whose inverse is not a power of two: divide)
-        const float q = fminf(fmaxf(__builtin_isinf(s) ? v / s : v * inv, -448.f), 448.f);
+        const float q = fminf(fmaxf(v * inv, -448.f), 448.f);
         const uint32_t c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q, q, 0, false) & 0xffu;
         x[(size_t)b * 32 + i] = bf16_round(e4m3_to_f32(c) * s);
     }
