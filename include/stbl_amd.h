@@ -236,7 +236,10 @@ int stbl_amd_gemm_q(int fmt, void *y, const void *codes, const void *scales, con
 uint64_t stbl_amd_gemm_work_bytes(int m, int n, int k);
 
 /* act_quant(x, block, "ue8m0") (ref/kernel.py:35-45) as the GEMM consumes it: x bf16 [rows][k] ->
- * e4m3 codes [rows][k] and E8M0 scale bytes [rows][k/block]; block 32 or 128. */
+ * e4m3 codes [rows][k] and E8M0 scale bytes [rows][k/block]; block 32 or 128. Non-finite values as
+ * the engine's act_quant treats them (stbl/kernels.cu:56-63): a NaN is left out of its block's
+ * maximum and clamps to -448; a block holding an infinity gets scale byte 255 (+Inf) and codes
+ * x / Inf (0, and -448 for the infinity). stbl_amd_act_quant follows the same rules. */
 int stbl_amd_act_quant_e4m3(const void *x, int rows, int k, int block, void *codes, void *scales, hipStream_t st);
 
 /* ---- v2: HBM expert cache (stbl/model.cu:99-106, 347-422 ExpertCache / expert() / take_slot) -------- */
