@@ -89,6 +89,9 @@ def test_quant_fp8_e8m0_matches_oracle(gpu, rows, k):
 def test_act_quant_matches_oracle(gpu, block, pow2):
     x = (data.normal((5, 1024), 1.0, seed=block) * torch.logspace(-3, 3, 1024)).to(torch.bfloat16)
     x[0, :block] = 0
+    # non-finite values (the engine's rules, stbl/kernels.cu:56-63): a block holding an infinity has
+    # scale +Inf, codes x / Inf and a NaN in-place form; a NaN is skipped by its block's maximum
+    x[1, 3], x[2, block + 5], x[3, 2 * block] = float("inf"), float("-inf"), float("nan")
     codes, scales, deq = ops.act_quant(x.to(gpu), block, pow2, want_deq=True)
     oc, os_, od = oracle.act_quant(x.float().numpy(), block, pow2)
     assert np.array_equal(np_(scales), os_)
@@ -99,6 +102,7 @@ def test_act_quant_matches_oracle(gpu, block, pow2):
 def test_stbl_act_quant_fp8_inplace(gpu):
     # the reference engine's form (stbl/kernels.cu:54-63): fp32 buffer of bf16 values, block 32
     x = (data.normal((4, 256), 3.0, seed=7)).to(torch.bfloat16).float()
+    x[1, 40], x[2, 70], x[3, 100] = float("inf"), float("-inf"), float("nan")  # NaN blocks, NaN skipped
     got = ops.stbl_act_quant_fp8(x.clone().to(gpu))
     want = oracle.act_quant(x.numpy(), 32, True)[2]
     assert bits_equal(np_(got), want)
