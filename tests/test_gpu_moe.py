@@ -217,6 +217,29 @@ def deq_parts(fmt, parts):
     return out
 
 
+@pytest.mark.parametrize("fmt", [ops.FP4, ops.FP8])
+@pytest.mark.parametrize("limit", [10.0, 0.0])
+def test_expert_ffn_official_non_finite_inputs(gpu, fmt, limit):
+    # the official numerics quantize x and h in registers with the engine's rules
+    # (stbl/kernels.cu:56-63): in a token whose x holds an infinity, that block's values become
+    # 0 * Inf = NaN and so do its gate and up sums; the SwiGLU clamps turn NaN into the limits
+    # (fminf / fmaxf, stbl/kernels.cu:452-458), and without a limit the NaN h is left out of its
+    # blocks' maxima and each NaN clamps to -448 times the smallest scale in h's act_quant. Either
+    # way the token comes out finite, as the oracle's does; a NaN element of x only clamps to -448
+    # times its block's scale. Every token meets the oracle's bar.
+    dim, inter = 1024, 512
+    slot, parts = make_expert(fmt, dim, inter, seed=333 + fmt, gpu=gpu)
+    x = data.activation(3, dim, seed=334)
+    x[0, 100] = float("inf")
+    x[1, 200] = float("nan")
+    y16 = np_(ops.expert_ffn(slot, x.to(gpu), fmt, dim, inter, 0.5, limit, True))
+    y32 = np_(ops.expert_ffn(slot, x.to(gpu), fmt, dim, inter, 0.5, limit, True, out_f32=True))
+    for t in range(3):
+        _, raw = oracle_ffn(fmt, parts, dim, inter, x[t].float().numpy(), 0.5, limit, True)
+        assert np.isfinite(raw).all()
+        assert_gemv(y32[t], y16[t], raw)
+
+
 @pytest.mark.parametrize("dim,inter", [(512, 256), (5120, 2304)])
 @pytest.mark.parametrize("official", [False, True])
 def test_expert_ffn_fp8_e8m0(gpu, dim, inter, official):
