@@ -494,6 +494,13 @@ static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int o
             return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
         }
         const int cus = device_cus();
+        // rows of at most 32 chunks (FP4 K <= 1024) use half the lanes of their one-wave workgroup,
+        // so a 2-row tile has little in flight: 8-row tiles wherever each CU still gets two (M = 1,
+        // us, 2 -> 8 rows: 32768x1024 7.12 -> 5.49, 16384x1024 4.69 -> 3.87, 7168x1024 3.27 -> 3.03,
+        // 4096x1024 2.83 -> 2.75; at 3072x1024, 1.5 tiles per CU, 2.63 -> 2.67)
+        if constexpr (F == WFmt::FP4_OCP && M == 1)
+            if (k / WTraits<F>::CH <= 32 && (long)ceil_div(rows, 8) * njobs >= 2L * cus)
+                return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
         // one token of FP4, or two tokens, over rows of 4+ waves: 8-row tiles when they still fill every
         // CU, halving the x reads per weight byte again (2048x7168: FP4 M=1 3.85 -> 3.80 us, M=2 4.24 ->
         // 4.18, FP8 M=2 5.08 -> 4.78; rows of one wave lose: 7168x2048 3.73 -> 4.62 us)

@@ -16,7 +16,7 @@ from util import assert_gemv, np_
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(8, 32), (13, 96), (64, 2048), (100, 2080), (2048, 7168), (7168, 2048)]
+SHAPES = [(8, 32), (13, 96), (64, 2048), (100, 2080), (4100, 1024), (2048, 7168), (7168, 2048)]
 
 
 def _fp4(gpu, rows, k, seed):
