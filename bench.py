@@ -54,9 +54,10 @@ def parse():
                     help="print per (kernel, grid, counter) medians of a rocprofv3 --pmc counter_collection CSV and exit")
     ap.add_argument("--trace-by-grid", action="store_true",
                     help="with --trace-summary: one line per (kernel, grid) with calls and median / mean duration")
-    ap.add_argument("--sweep", default=None, choices=["gemv"],
+    ap.add_argument("--sweep", default=None, choices=["gemv", "gemv-tokens"],
                     help="gemv: FP4 and FP8 single GEMVs (one token) over a grid of shapes, each against the "
-                         "bare read of its bytes; one JSON line per shape on stdout, and exit")
+                         "bare read of its bytes; gemv-tokens: the same with 2, 3 and 4 tokens; one JSON line "
+                         "per shape on stdout, and exit")
     ap.add_argument("--copy-calib", action="store_true",
                     help="after the workloads, copy 64 MiB device to device 5 times (the reference transfer for "
                          "scaling HBM byte counters)")
@@ -1070,19 +1071,21 @@ SWEEP_ROWS = (512, 1024, 2048, 4096, 7168, 16384)
 SWEEP_K = (1024, 2048, 4096, 7168)
 
 
-def gemv_sweep(torch, steps, warmup):
-    """The single-GEMV tile plans over a grid of shapes (rows x K, one token): per shape the GEMV's
-    time and its bare-read floor (the same bytes in one launch), both graph-timed as the rows are."""
-    for fmt in ("fp4", "fp8"):
-        for rows in SWEEP_ROWS:
-            for k in SWEEP_K:
-                r = gemv_workload(torch, fmt, rows, k, 1, steps, warmup)
-                f = read_floor_workload(torch, int(r["alg_bytes"]) // 16 * 16, steps, warmup)
-                print(json.dumps({"fmt": fmt, "rows": rows, "k": k, "us": _r(r["ms_per_step"] * 1e3, 4),
-                                  "GB_s": _r(r["GB_s"]), "frac_hbm_peak": _r(r["frac_hbm_peak"]),
-                                  "floor_us": _r(f["ms_per_step"] * 1e3, 4),
-                                  "frac_of_read_floor": _r(f["ms_per_step"] / r["ms_per_step"])}), flush=True)
-                torch.cuda.empty_cache()
+def gemv_sweep(torch, steps, warmup, tokens=(1,)):
+    """The single-GEMV tile plans over a grid of shapes (rows x K, each token count): per shape the
+    GEMV's time and its bare-read floor (the same bytes in one launch), both graph-timed as the rows
+    are."""
+    for m in tokens:
+        for fmt in ("fp4", "fp8"):
+            for rows in SWEEP_ROWS:
+                for k in SWEEP_K:
+                    r = gemv_workload(torch, fmt, rows, k, m, steps, warmup)
+                    f = read_floor_workload(torch, int(r["alg_bytes"]) // 16 * 16, steps, warmup)
+                    print(json.dumps({"fmt": fmt, "m": m, "rows": rows, "k": k, "us": _r(r["ms_per_step"] * 1e3, 4),
+                                      "GB_s": _r(r["GB_s"]), "frac_hbm_peak": _r(r["frac_hbm_peak"]),
+                                      "floor_us": _r(f["ms_per_step"] * 1e3, 4),
+                                      "frac_of_read_floor": _r(f["ms_per_step"] / r["ms_per_step"])}), flush=True)
+                    torch.cuda.empty_cache()
 
 
 def main():
@@ -1114,8 +1117,8 @@ def main():
 
     _lib.load()  # fails loudly when the library was not built
     K, W, graph = args.steps, args.warmup, not args.no_graph
-    if args.sweep == "gemv":
-        gemv_sweep(torch, K, W)
+    if args.sweep:
+        gemv_sweep(torch, K, W, (1,) if args.sweep == "gemv" else (2, 3, 4))
         return
     extra = {}
 

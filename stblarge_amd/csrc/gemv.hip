@@ -429,7 +429,44 @@ static int device_cus() {
     return n;
 }
 
-// Rows per workgroup (M <= 2). A launch with much more work (batched matrices) takes 8 rows per
+// Rows per workgroup for 2-4 tokens of bf16 x (FP4 and FP8 with 128x128 scales). A lane's x chunk
+// is M times one token's and every row of the tile reuses it, so taller tiles cut the x bytes the
+// vector L1 takes in per weight byte (4 M / R for FP4, 2 M / R for FP8), while shorter ones keep
+// more waves in flight per CU. Chosen from a sweep that forced each height in turn (rows 512-16384,
+// K 1024-7168, M = 2-4): the tallest tile that still gives each CU a number of tiles depending on
+// the format and the waves per row (us at M = 4 for 2 / 4 / 8 rows):
+//   FP4, rows of 4+ waves, and FP8 of 5+: 8 or 4 rows while every CU gets one (FP4 2048x7168 6.70 /
+//     5.54 / 5.21, 512x7168 3.37 / 3.73 / 4.63; FP8 2048x7168 7.09 / 6.14 / 6.08);
+//   FP4, rows of 1-3 waves: while every CU gets four (7168x2048 5.75 / 4.74 / 4.82, 16384x2048
+//     10.31 / 7.98 / 7.73, 16384x1024 8.88 / 7.05 / 6.32, 4096x4096 6.44 / 5.33 / 6.16);
+//   FP8, rows of 3-4 waves, 3-4 tokens: 8 rows while every CU gets two, 4 while it gets one
+//     (2048x4096 4.77 / 4.29 / 4.65, 4096x4096 7.31 / 6.34 / 6.22; with 2 tokens 8 rows win at
+//     2048x4096: 3.91 / 3.89 / 3.76);
+//   FP8, rows of 1-2 waves: never 8 rows; 4 while every CU gets four, or six for rows of one wave
+//     or 2 tokens (7168x2048 6.18 / 5.67 / 6.05, 2048x2048 3.27 / 3.62 / 3.88; 4096x1024 3.19 /
+//     3.21, 2 tokens 4096x2048 3.59 / 3.66).
+// A height of 16 was slower everywhere at M = 2 (no gain for FP8, 2-4x slower for FP4).
+template <WFmt F, int M>
+static int multi_token_rows(int rows, int njobs, int k) {
+    static_assert(F == WFmt::FP4_OCP || F == WFmt::FP8_B128, "bf16-x formats only");
+    const long cus = device_cus();
+    const int waves = ceil_div(k / WTraits<F>::CH, 64);
+    const long tiles8 = (long)ceil_div(rows, 8) * njobs, tiles4 = (long)ceil_div(rows, 4) * njobs;
+    long per_cu8 = 1, per_cu4 = 1;  // tiles each CU must get for the height (0: never)
+    if constexpr (F == WFmt::FP4_OCP) {
+        if (waves < 4) per_cu8 = per_cu4 = 4;
+    } else if (waves < 3) {
+        per_cu8 = 0;
+        per_cu4 = waves == 1 || M == 2 ? 6 : 4;
+    } else if (waves < 5 && M > 2) {
+        per_cu8 = 2;
+    }
+    if (per_cu8 > 0 && tiles8 >= per_cu8 * cus) return 8;
+    if (tiles4 >= per_cu4 * cus) return 4;
+    return 2;
+}
+
+// Rows per workgroup for one token. A launch with much more work (batched matrices) takes 8 rows per
 // workgroup, so the fixed per-workgroup cost (x chunk, prologue, reduction) is spread over 4x the
 // weight bytes while still leaving thousands of workgroups. Otherwise 4 rows halve the x loads per
 // weight byte, unless that leaves the busiest CU more rows than 2-row tiles would (workgroups come
@@ -437,23 +474,16 @@ static int device_cus() {
 // or a row takes too few waves: one wave (FP4 K <= 2048) or, for FP8, whose x chunk per weight
 // byte is half FP4's, two. Measured (M = 1, us, 2 -> 4 rows): FP4 2048x7168 4.01 -> 3.84,
 // 5120x2304 3.98 -> 3.84, 7168x2048 3.71 -> 3.99, 2304x5120 3.64 -> 3.84; FP8 2048x7168 4.73 ->
-// 4.66, 7168x2048 4.52 -> 4.58; M = 2 FP4 2048x7168 5.09 -> 4.51.
+// 4.66, 7168x2048 4.52 -> 4.58.
 template <WFmt F, bool XF32, int M>
 static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int out_mode, hipStream_t st) {
-    if constexpr (M > 2) {
-        // 3-4 tokens: a lane's x chunk is M times larger, so 4 rows share it (measured at 2048x7168:
-        // 6.5 us against 10.7 us with 1 row per workgroup for FP4, 6.8 against 11.8 for FP8), except
-        // where a row spans one wave: there 2 rows keep twice the workgroups in flight (M = 4: FP4
-        // 7168x2048 7.33 -> 6.81 us, 4096x1024 5.70 -> 5.08; FP8 4096x1024 5.45 -> 4.40)
-        if constexpr (XF32) return launch_r<F, XF32, M, 1>(jobs, njobs, rows, k, out_mode, st);
-        else {
-            if (k / WTraits<F>::CH <= 64) return launch_r<F, XF32, M, 2>(jobs, njobs, rows, k, out_mode, st);
-            // rows of 4+ waves: 8 rows share the lane's x chunks (M x the weight bytes it reads) while
-            // the tiles still fill every CU (2048x7168: FP4 M=4 5.53 -> 5.23 us, M=3 4.80 -> 4.76,
-            // FP8 M=3 5.62 -> 5.38; FP8 M=4 unchanged)
-            if (k / WTraits<F>::CH > 3 * 64 && (long)ceil_div(rows, 8) * njobs >= device_cus())
-                return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
-            return launch_r<F, XF32, M, 4>(jobs, njobs, rows, k, out_mode, st);
+    if constexpr (M > 2 && XF32) {
+        return launch_r<F, XF32, M, 1>(jobs, njobs, rows, k, out_mode, st);
+    } else if constexpr (M >= 2 && !XF32) {
+        switch (multi_token_rows<F, M>(rows, njobs, k)) {
+            case 8: return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
+            case 4: return launch_r<F, XF32, M, 4>(jobs, njobs, rows, k, out_mode, st);
+            default: return launch_r<F, XF32, M, 2>(jobs, njobs, rows, k, out_mode, st);
         }
     }
     else if constexpr (XF32) {
@@ -501,10 +531,10 @@ static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int o
         if constexpr (F == WFmt::FP4_OCP && M == 1)
             if (k / WTraits<F>::CH <= 32 && (long)ceil_div(rows, 8) * njobs >= 2L * cus)
                 return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
-        // one token of FP4, or two tokens, over rows of 4+ waves: 8-row tiles when they still fill every
-        // CU, halving the x reads per weight byte again (2048x7168: FP4 M=1 3.85 -> 3.80 us, M=2 4.24 ->
-        // 4.18, FP8 M=2 5.08 -> 4.78; rows of one wave lose: 7168x2048 3.73 -> 4.62 us)
-        if constexpr (M == 2 || (F == WFmt::FP4_OCP && M == 1))
+        // one token of FP4 over rows of 4+ waves: 8-row tiles when they still fill every CU, halving the
+        // x reads per weight byte again (2048x7168 3.85 -> 3.80 us; rows of one wave lose: 7168x2048
+        // 3.73 -> 4.62 us)
+        if constexpr (F == WFmt::FP4_OCP)
             if (k / WTraits<F>::CH > 3 * 64 && (long)ceil_div(rows, 8) * njobs >= cus)
                 return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
         const long busiest2 = ceil_div(ceil_div(rows, 2) * njobs, cus) * 2L;

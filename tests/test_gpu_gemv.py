@@ -58,6 +58,23 @@ def test_gemv_fp8(gpu, rows, k, m):
     assert_gemv(np_(y32), np_(y16), want)
 
 
+@pytest.mark.parametrize("fmt,rows,k,m", [(0, 8195, 1024, 2), (0, 8195, 1024, 3), (0, 8195, 1024, 4), (0, 4100, 2048, 4),
+                                          (0, 1030, 7168, 3), (0, 514, 4096, 4), (1, 7170, 1024, 3), (1, 4100, 4096, 4),
+                                          (1, 2050, 4096, 3), (1, 2050, 7168, 2), (1, 6150, 2048, 2)])
+def test_gemv_multi_token_tile_heights(gpu, fmt, rows, k, m):
+    # 2-4 tokens take tiles of 8, 4 or 2 rows by format, waves per row and tiles per CU; these shapes
+    # reach each height with a partial last tile (8195 rows of FP4 K = 1024: 8-row tiles, 3 rows in
+    # the last; 514 x 4096: 2-row tiles; 7170 x 1024 FP8: 4-row tiles; 4100 x 4096 FP8: 8-row tiles)
+    q = oracle.quant_fp4 if fmt == 0 else oracle.quant_fp8_b128
+    ref = oracle.gemv_fp4 if fmt == 0 else oracle.gemv_fp8_b128
+    run = ops.gemv_fp4 if fmt == 0 else ops.gemv_fp8
+    c, sc = q(data.weight(rows, k, seed=rows + k + m).numpy())
+    x = data.activation(m, k, seed=rows + m)
+    want = ref(c, sc, x.float().numpy())
+    dc, ds = torch.from_numpy(c).to(gpu), torch.from_numpy(sc).to(gpu)
+    assert_gemv(np_(run(dc, ds, x.to(gpu), out_f32=True)), np_(run(dc, ds, x.to(gpu))), want)
+
+
 @pytest.mark.parametrize("fmt,k", [(0, 16384), (1, 8192)])
 @pytest.mark.parametrize("m", [1, 4])
 def test_gemv_maximum_k_and_ragged_rows(gpu, fmt, k, m):
