@@ -517,20 +517,29 @@ static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int o
     } else {
         const long wgs8 = (long)ceil_div(rows, 8) * njobs * ceil_div(k / WTraits<F>::CH, 64);
         if (wgs8 >= 8192) {
-            // one FP4 token over rows of 4+ waves: 16 rows (16 x 2048x7168: 21.4 -> 21.0 us, 64 x 76.4
-            // -> 73.6; rows of one wave lose: 16 x 7168x2048 20.3 -> 21.1)
-            if constexpr (F == WFmt::FP4_OCP && M == 1)
-                if (k / WTraits<F>::CH > 3 * 64) return launch_r<F, XF32, M, 16>(jobs, njobs, rows, k, out_mode, st);
+            // FP4 rows of 2+ waves: 16 rows (16 x 2048x7168: 21.4 -> 21.0 us, 64 x 76.4 -> 73.6; 64 x
+            // 5120x2304, whose second wave has 8 chunks, 93.7 -> 82.8; 2304x5120 within the spread
+            // between runs); rows of one wave lose (16 x 7168x2048 20.3 -> 21.1). FP8 rows of 1-2
+            // waves take 4 rows (16 x 7168x2048 36.1 -> 35.3 us, 64 x 140.8 -> 137.1), longer ones 8
+            // (64 x 2048x7168 137.0, 140.6 with 4).
+            if constexpr (F == WFmt::FP4_OCP)
+                if (k / WTraits<F>::CH > 64) return launch_r<F, XF32, M, 16>(jobs, njobs, rows, k, out_mode, st);
+            if constexpr (F == WFmt::FP8_B128)
+                if (k / WTraits<F>::CH <= 128) return launch_r<F, XF32, M, 4>(jobs, njobs, rows, k, out_mode, st);
             return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
         }
         const int cus = device_cus();
-        // rows of at most 32 chunks (FP4 K <= 1024) use half the lanes of their one-wave workgroup,
-        // so a 2-row tile has little in flight: 8-row tiles wherever each CU still gets two (M = 1,
-        // us, 2 -> 8 rows: 32768x1024 7.12 -> 5.49, 16384x1024 4.69 -> 3.87, 7168x1024 3.27 -> 3.03,
-        // 4096x1024 2.83 -> 2.75; at 3072x1024, 1.5 tiles per CU, 2.63 -> 2.67)
-        if constexpr (F == WFmt::FP4_OCP && M == 1)
-            if (k / WTraits<F>::CH <= 32 && (long)ceil_div(rows, 8) * njobs >= 2L * cus)
+        // FP4 rows of one wave: rows of at most 32 chunks (K <= 1024) use half the lanes of their
+        // workgroup, so a 2-row tile has little in flight: 8-row tiles wherever each CU still gets two
+        // (us, 2 -> 8 rows: 32768x1024 7.12 -> 5.49, 16384x1024 4.69 -> 3.87, 7168x1024 3.27 -> 3.03,
+        // 4096x1024 2.83 -> 2.75; at 3072x1024, 1.5 tiles per CU, 2.63 -> 2.67); rows of 33-64 chunks
+        // wherever each CU gets four (16384x2048 5.22 -> 4.70; 7168x2048, 3.5 per CU: 3.51 -> 3.48)
+        if constexpr (F == WFmt::FP4_OCP) {
+            const long tiles8 = (long)ceil_div(rows, 8) * njobs;
+            const int nch = k / WTraits<F>::CH;
+            if ((nch <= 32 && tiles8 >= 2L * cus) || (nch <= 64 && tiles8 >= 4L * cus))
                 return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
+        }
         // one token of FP4 over rows of 4+ waves: 8-row tiles when they still fill every CU, halving the
         // x reads per weight byte again (2048x7168 3.85 -> 3.80 us; rows of one wave lose: 7168x2048
         // 3.73 -> 4.62 us)

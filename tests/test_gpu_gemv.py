@@ -419,21 +419,26 @@ def test_gemv_batch(gpu, fmt, rows, k, n):
         assert_gemv(np_(y), np_(y16), want)
 
 
-@pytest.mark.parametrize("rows,k", [(1100, 7168), (4100, 2048)])
-def test_gemv_batch_ragged_rows_eight_row_tiles(gpu, rows, k):
-    # 16 x 1100 rows at K = 7168 take 16-row tiles (rows of 4 waves), 16 x 4100 at K = 2048 8-row
-    # tiles; 1100 = 68 x 16 + 12 and 4100 = 512 x 8 + 4 leave the last tile partly past the matrix
+@pytest.mark.parametrize("fmt,rows,k", [(0, 1100, 7168), (0, 4100, 2048), (0, 5130, 2304), (1, 4102, 2048), (1, 2052, 7168)])
+def test_gemv_batch_ragged_rows_eight_row_tiles(gpu, fmt, rows, k):
+    # one-token batches of 16 large matrices: FP4 16 x 1100 rows at K = 7168 and 16 x 5130 at K = 2304
+    # (a second wave of 8 chunks) take 16-row tiles, 16 x 4100 at K = 2048 8-row tiles; FP8 16 x 4102
+    # at K = 2048 4-row tiles, 16 x 2052 at K = 7168 8-row tiles. Each row count leaves the last tile
+    # partly past the matrix (1100 = 68 x 16 + 12, 5130 = 320 x 16 + 10, 4100 = 512 x 8 + 4, 4102 =
+    # 1025 x 4 + 2, 2052 = 256 x 8 + 4)
     n = 16
+    q = oracle.quant_fp4 if fmt == 0 else oracle.quant_fp8_b128
+    ref = oracle.gemv_fp4 if fmt == 0 else oracle.gemv_fp8_b128
     cs, ss, xs, wants = [], [], [], []
     for j in range(n):
-        c, s = oracle.quant_fp4(data.weight(rows, k, seed=700 + j).numpy())
+        c, s = q(data.weight(rows, k, seed=700 + j).numpy())
         x = data.activation(1, k, seed=800 + j)
-        wants.append(oracle.gemv_fp4(c, s, x.float().numpy()))
+        wants.append(ref(c, s, x.float().numpy()))
         cs.append(torch.from_numpy(c).to(gpu))
         ss.append(torch.from_numpy(s).to(gpu))
         xs.append(x.to(gpu))
-    ys = ops.gemv_batch(cs, ss, xs, 0, out_f32=True)
-    ys16 = ops.gemv_batch(cs, ss, xs, 0)
+    ys = ops.gemv_batch(cs, ss, xs, fmt, out_f32=True)
+    ys16 = ops.gemv_batch(cs, ss, xs, fmt)
     for y, y16, want in zip(ys, ys16, wants):
         assert_gemv(np_(y), np_(y16), want)
 
