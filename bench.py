@@ -52,6 +52,9 @@ def parse():
                     help="kernel-name regex for --trace-summary (default: the headline FP4 GEMV kernel)")
     ap.add_argument("--counter-summary", default=None, metavar="CSV",
                     help="print per (kernel, grid, counter) medians of a rocprofv3 --pmc counter_collection CSV and exit")
+    ap.add_argument("--counter-last", type=int, default=0, metavar="N",
+                    help="with --counter-summary: instead of medians, the values of the last N matching dispatches "
+                         "(by dispatch id), e.g. the calibration copies --copy-calib issues at the end of a run")
     ap.add_argument("--trace-by-grid", action="store_true",
                     help="with --trace-summary: one line per (kernel, grid) with calls and median / mean duration")
     ap.add_argument("--sweep", default=None, choices=["gemv", "gemv-tokens"],
@@ -1067,6 +1070,21 @@ def counter_table(path, kernel_regex):
             for k, v in sorted(groups.items())]
 
 
+def counter_last(path, kernel_regex, n):
+    """The last n dispatches (by dispatch id) of the kernels matching kernel_regex in a rocprofv3 --pmc
+    counter_collection CSV, one dict per (dispatch, counter)."""
+    import csv
+    import re
+
+    pat = re.compile(kernel_regex)
+    rows = [r for r in csv.DictReader(open(path)) if pat.search(r["Kernel_Name"])]
+    ids = sorted({int(r["Dispatch_Id"]) for r in rows})[-n:]
+    keep = set(ids)
+    return [{"dispatch": int(r["Dispatch_Id"]), "kernel": r["Kernel_Name"], "grid": r["Grid_Size"],
+             "counter": r["Counter_Name"], "value": float(r["Counter_Value"])}
+            for r in sorted(rows, key=lambda r: int(r["Dispatch_Id"])) if int(r["Dispatch_Id"]) in keep]
+
+
 SWEEP_ROWS = (512, 1024, 2048, 4096, 7168, 16384)
 SWEEP_K = (1024, 2048, 4096, 7168)
 
@@ -1091,7 +1109,9 @@ def gemv_sweep(torch, steps, warmup, tokens=(1,)):
 def main():
     args = parse()
     if args.counter_summary:
-        for row in counter_table(args.counter_summary, args.trace_kernel):
+        rows = (counter_last(args.counter_summary, args.trace_kernel, args.counter_last) if args.counter_last > 0
+                else counter_table(args.counter_summary, args.trace_kernel))
+        for row in rows:
             print(json.dumps(row))
         return
     if args.trace_summary:

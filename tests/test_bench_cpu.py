@@ -157,3 +157,15 @@ def test_counter_table_medians(tmp_path):
     t = {(r["grid"], r["counter"]): r for r in bench.counter_table(str(p), r"k_a")}
     assert t[("64", "FETCH_SIZE")]["median"] == 20.0 and t[("64", "FETCH_SIZE")]["dispatches"] == 3
     assert t[("128", "FETCH_SIZE")]["median"] == 5.0 and len(t) == 2
+
+
+def test_counter_last_dispatches(tmp_path):
+    import bench
+
+    p = tmp_path / "p_counter_collection.csv"
+    hdr = '"Dispatch_Id","Grid_Size","Kernel_Name","Counter_Name","Counter_Value"\n'
+    rows = [(3, 64, "copy", "FETCH_SIZE", 7.0), (1, 64, "copy", "FETCH_SIZE", 5.0), (9, 64, "copy", "FETCH_SIZE", 32.0),
+            (7, 64, "copy", "FETCH_SIZE", 31.0), (8, 64, "k_a", "FETCH_SIZE", 1.0)]
+    p.write_text(hdr + "".join(f'{d},{g},"{n}","{c}",{v}\n' for d, g, n, c, v in rows))
+    got = bench.counter_last(str(p), r"copy", 2)
+    assert [(r["dispatch"], r["value"]) for r in got] == [(7, 31.0), (9, 32.0)]
