@@ -532,13 +532,17 @@ static hipError_t launch(const GemvJobs &jobs, int njobs, int rows, int k, int o
         // FP4 rows of one wave: rows of at most 32 chunks (K <= 1024) use half the lanes of their
         // workgroup, so a 2-row tile has little in flight: 8-row tiles wherever each CU still gets two
         // (us, 2 -> 8 rows: 32768x1024 7.12 -> 5.49, 16384x1024 4.69 -> 3.87, 7168x1024 3.27 -> 3.03,
-        // 4096x1024 2.83 -> 2.75; at 3072x1024, 1.5 tiles per CU, 2.63 -> 2.67); rows of 33-64 chunks
-        // wherever each CU gets four (16384x2048 5.22 -> 4.70; 7168x2048, 3.5 per CU: 3.51 -> 3.48)
+        // 4096x1024 2.83 -> 2.75; at 3072x1024, 1.5 tiles per CU, 2.63 -> 2.67). Rows of 33-64 chunks
+        // take 8 rows wherever each CU gets eight tiles (16384x2048 5.22 -> 4.70), else 4 wherever it
+        // gets four (7168x2048 3.55 -> 3.46, 7168x1536 3.43 -> 3.30, 9216x2048 with 8 rows 3.86 ->
+        // 3.80; 5120x2048 and 4096x2048 within 0.01 us)
         if constexpr (F == WFmt::FP4_OCP) {
-            const long tiles8 = (long)ceil_div(rows, 8) * njobs;
+            const long tiles8 = (long)ceil_div(rows, 8) * njobs, tiles4 = (long)ceil_div(rows, 4) * njobs;
             const int nch = k / WTraits<F>::CH;
-            if ((nch <= 32 && tiles8 >= 2L * cus) || (nch <= 64 && tiles8 >= 4L * cus))
+            if ((nch <= 32 && tiles8 >= 2L * cus) || (nch <= 64 && tiles8 >= 8L * cus))
                 return launch_r<F, XF32, M, 8>(jobs, njobs, rows, k, out_mode, st);
+            if (nch > 32 && nch <= 64 && tiles4 >= 4L * cus)
+                return launch_r<F, XF32, M, 4>(jobs, njobs, rows, k, out_mode, st);
         }
         // one token of FP4 over rows of 4+ waves: 8-row tiles when they still fill every CU, halving the
         // x reads per weight byte again (2048x7168 3.85 -> 3.80 us; rows of one wave lose: 7168x2048
