@@ -61,12 +61,13 @@ def test_gemv_fp8(gpu, rows, k, m):
 @pytest.mark.parametrize("fmt,rows,k,m", [(0, 8195, 1024, 2), (0, 8195, 1024, 3), (0, 8195, 1024, 4), (0, 4100, 2048, 4),
                                           (0, 1030, 7168, 3), (0, 514, 4096, 4), (1, 7170, 1024, 3), (1, 4100, 4096, 4),
                                           (1, 2050, 4096, 3), (1, 2050, 7168, 2), (1, 6150, 2048, 2),
-                                          (0, 4102, 2048, 1), (0, 16390, 2048, 1)])
+                                          (0, 4102, 2048, 1), (0, 16390, 2048, 1), (0, 2046, 4096, 1), (0, 8190, 3072, 1)])
 def test_gemv_multi_token_tile_heights(gpu, fmt, rows, k, m):
     # 2-4 tokens take tiles of 8, 4 or 2 rows by format, waves per row and tiles per CU; these shapes
     # reach each height with a partial last tile (8195 rows of FP4 K = 1024: 8-row tiles, 3 rows in
     # the last; 514 x 4096: 2-row tiles; 7170 x 1024 FP8: 4-row tiles; 4100 x 4096 FP8: 8-row tiles).
-    # One token of FP4 rows of one wave: 4-row tiles at 4102 x 2048, 8-row ones at 16390 x 2048
+    # One token of FP4 rows of one wave: 4-row tiles at 4102 x 2048, 8-row ones at 16390 x 2048; of
+    # two or three waves: 8-row tiles at 2046 x 4096 (one round over the CUs) and 8190 x 3072 (four)
     q = oracle.quant_fp4 if fmt == 0 else oracle.quant_fp8_b128
     ref = oracle.gemv_fp4 if fmt == 0 else oracle.gemv_fp8_b128
     run = ops.gemv_fp4 if fmt == 0 else ops.gemv_fp8
