@@ -403,8 +403,8 @@ def test_stbl_gemv_fp8_engine_scale_bytes(gpu, rows, k):
 @pytest.mark.parametrize("rows,k,n", [(256, 1024, 16), (2048, 7168, 3), (128, 1024, 64)])
 def test_gemv_batch(gpu, fmt, rows, k, n):
     # same-shape GEMVs in one launch (stbl_gemv_mxfp4_batch's batching, v2 formats), M = 2: 16 small
-    # matrices (2-row tiles), 3 large ones (4-row tiles, FP4 scales as dwords from each matrix), and
-    # the largest v2 batch, 64 matrices
+    # matrices (4-row tiles for FP4, its scales as dwords from each matrix; 2-row tiles for FP8), 3
+    # large ones (8-row tiles), and the largest v2 batch, 64 matrices (8-row tiles for FP4, 4 for FP8)
     m = 2
     q = oracle.quant_fp4 if fmt == 0 else oracle.quant_fp8_b128
     ref = oracle.gemv_fp4 if fmt == 0 else oracle.gemv_fp8_b128
@@ -589,8 +589,9 @@ def test_random_shapes_every_gemv_entry_point(gpu, seed):
 @pytest.mark.parametrize("fmt,rows,k", [(0, 2052, 7168), (1, 2060, 4096)])
 @pytest.mark.parametrize("m", [2, 3, 4])
 def test_gemv_multi_token_8_row_tiles(gpu, fmt, rows, k, m):
-    # 2-4 tokens over rows of 4+ waves take 8-row tiles when those fill every CU; a ragged last tile
-    # (4 of 8 rows, FP8 12 of 8 + 4) against the oracle
+    # 2-4 tokens over FP4 rows of 4+ waves take 8-row tiles when those fill every CU (2052 x 7168: the
+    # last tile holds 4 rows); FP8 rows of 4 waves take 8-row tiles at 2 tokens (2060 x 4096: 4 rows
+    # in the last) and 4-row tiles at 3-4 tokens, where 8 rows would give a CU fewer than two
     q, ref = (oracle.quant_fp4, oracle.gemv_fp4) if fmt == 0 else (oracle.quant_fp8_b128, oracle.gemv_fp8_b128)
     codes, scales = q(data.weight(rows, k, seed=rows + m).numpy())
     x = data.activation(m, k, seed=k + m)
