@@ -117,6 +117,39 @@ def test_gemv_fp4_zero_and_extreme_inputs(gpu):
     assert_gemv(np_(ops.gemv_fp4(dc, ds, x.to(gpu), out_f32=True)), None, want)
 
 
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("m", [1, 4])
+def test_gemv_non_finite_activations(gpu, fmt, m):
+    # x with an infinity (token 0), a NaN (token 1) and both infinities (token 2): every output is
+    # NaN or the same infinity exactly where the oracle's IEEE double sum puts them (an infinity
+    # times a zero weight is NaN, +Inf plus -Inf is NaN), in fp32 and bf16; token 3, all finite,
+    # meets the GEMV bar, so a non-finite token leaves the others alone
+    rows, k = 300, 2048
+    q = oracle.quant_fp4 if fmt == 0 else oracle.quant_fp8_b128
+    ref = oracle.gemv_fp4 if fmt == 0 else oracle.gemv_fp8_b128
+    run = ops.gemv_fp4 if fmt == 0 else ops.gemv_fp8
+    codes, scales = q(data.weight(rows, k, seed=41 + fmt).numpy())
+    x = data.activation(m, k, seed=42)
+    x[0, 100] = float("inf")
+    if m > 1:
+        x[1, 5] = float("nan")
+        x[2, 700], x[2, 1500] = float("-inf"), float("inf")
+    with np.errstate(invalid="ignore"):
+        want = ref(codes, scales, x.float().numpy())
+    assert np.isinf(want[0]).any() and (np.isnan(want[0]).any() or fmt == 1)
+    dc, ds = torch.from_numpy(codes).to(gpu), torch.from_numpy(scales).to(gpu)
+    y32 = np_(run(dc, ds, x.to(gpu), out_f32=True)).astype(np.float64)
+    y16 = np_(run(dc, ds, x.to(gpu)).float()).astype(np.float64)
+    bad = slice(0, min(m, 3))
+    for got in (y32, y16):
+        assert np.array_equal(np.isnan(got[bad]), np.isnan(want[bad]))
+        inf = np.isinf(want[bad])
+        assert np.array_equal(got[bad][inf], want[bad][inf])
+        assert not np.isfinite(got[bad]).any()
+    if m == 4:
+        assert_gemv(y32[3:], y16[3:], want[3:])
+
+
 # ---- the reference engine's ABI ------------------------------------------------------------------
 
 @pytest.mark.parametrize("rows,k,round_out", [(1000, 1280, 1), (2048, 7168, 0), (64, 96, 1),
