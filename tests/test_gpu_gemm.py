@@ -182,3 +182,27 @@ def test_gemm_tile_plans(gpu, fmt, block, m, n, k, shift):
     y32 = np_(ops.gemm_q(dc, ds, aq, a_s, fmt, block, out_f32=True))
     y16 = np_(ops.gemm_q(dc, ds, aq, a_s, fmt, block))
     _check(y32, y16, want)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_gemm_non_finite_activations(gpu, fmt):
+    # an infinity in a row's activations makes its block scale +Inf (E8M0 byte 255, NaN to the scaled
+    # MFMA; the oracle's codes x / Inf and the infinity's own clamped code times +Inf give NaN), so
+    # that row is NaN in every output, as the oracle's; a NaN is skipped by the block maximum and
+    # clamps to -448 (the engine's fmaxf), so its row stays finite and meets the GEMM bar with the rest
+    m, n, k = 16, 256, 512
+    q, deq = (oracle.quant_fp4, oracle.dequant_fp4) if fmt == 0 else (oracle.quant_fp8_b128, oracle.dequant_fp8_b128)
+    codes, scales = q(data.weight(n, k, seed=5 + fmt).numpy())
+    x = data.activation(m, k, seed=6)
+    x[3, 10], x[5, 20], x[7, 300] = float("inf"), float("nan"), float("-inf")
+    with np.errstate(invalid="ignore"):
+        want = _oracle_gemm(x, deq(codes, scales), 128)
+    nan_rows = [3, 7]
+    assert np.isnan(want[nan_rows]).all() and np.isfinite(np.delete(want, nan_rows, axis=0)).all()
+    dc, ds, xg = torch.from_numpy(codes).to(gpu), torch.from_numpy(scales).to(gpu), x.to(gpu)
+    aq, a_s = ops.act_quant_e4m3(xg, 128)
+    for y32, y16 in ((np_(ops.gemm(dc, ds, xg, fmt, 128, out_f32=True)), np_(ops.gemm(dc, ds, xg, fmt, 128))),
+                     (np_(ops.gemm_q(dc, ds, aq, a_s, fmt, 128, out_f32=True)), np_(ops.gemm_q(dc, ds, aq, a_s, fmt, 128)))):
+        assert np.isnan(y32[nan_rows]).all() and np.isnan(y16.astype(np.float32)[nan_rows]).all()
+        keep = np.delete(np.arange(m), nan_rows)
+        _check(y32[keep], y16[keep], want[keep])
