@@ -23,8 +23,8 @@
 
 namespace stbl {
 
-// DW: OCP FP4 scales fetched as dwords and handed to the lanes by ds_bpermute (tiles of 4 rows
-// whose scale rows are dword-aligned: k % 128 == 0 and 4-byte aligned scales).
+// DW: OCP FP4 scales fetched as dwords and handed to the lanes by ds_bpermute (tiles of 4 rows and
+// 2-4 tokens whose scale rows are dword-aligned: k % 128 == 0 and 4-byte aligned scales).
 template <WFmt F, bool XF32, int M, int R, bool DW>
 __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, int out_mode) {
     using T = WTraits<F>;
@@ -44,15 +44,18 @@ __global__ __launch_bounds__(512) void k_gemv(GemvJobs jobs, int rows, int k, in
     //    Otherwise tiles of 4 or more rows stage them: the tile's rows hold one contiguous
     //    block of R * nch scale bytes, fetched with one 16-byte load per thread (from the block's
     //    16-byte units; such a load never crosses a page, so the bytes around the block are safe to
-    //    read) and handed out through LDS, instead of one byte load per row per lane. With 8 rows
-    //    (batched matrices) the block is loaded before the weights, so each row's products start as
-    //    soon as that row arrives; with 4 rows it is loaded after them and the tile waits for all
-    //    its loads at once; tiles of 1-2 rows load each lane's scale bytes directly.
-    //    (Measured: dwords beat the LDS block by 5% at 4 rows x 4 tokens; at 2 rows they are up to
-    //    1.6% slower than bytes; the early LDS block is the fastest at 8 rows.)
+    //    read) and handed out through LDS, instead of one byte load per row per lane. With 8 rows,
+    //    and with 4 rows of one token, the block is loaded before the weights, so each row's
+    //    products start as soon as that row arrives; with 4 rows of 2-4 tokens (scale rows that are
+    //    not dword-aligned) it is loaded after them and the tile waits for all its loads at once;
+    //    tiles of 1-2 rows load each lane's scale bytes directly.
+    //    (Measured: dwords beat the LDS block by 5% at 4 rows x 4 tokens (4096x4096: 13%), but with
+    //    one token the early LDS block is 2-4% faster at 4 rows (7168x2048 3.46 -> 3.38 us, 4096x4096
+    //    3.74 -> 3.62, 3072x3072 3.26 -> 3.15; loaded after the weights it gained 0-3%); at 2 rows
+    //    dwords are up to 1.6% slower than bytes; the early LDS block is the fastest at 8 rows.)
     static_assert(!DW || (F == WFmt::FP4_OCP && R <= 4), "dword scale loads: FP4 tiles of at most 4 rows");
     constexpr bool kStageScales = F == WFmt::FP4_OCP && R >= 4 && !DW;
-    constexpr bool kScalesEarly = R >= 8;
+    constexpr bool kScalesEarly = R >= 8 || (R >= 4 && M == 1);
     static_assert(!kStageScales || R <= kMaxStageRows, "the staged scale block holds at most kMaxStageRows rows");
     constexpr int kScaleLoads = R > 8 ? 2 : 1;  // units <= R nch / 16 + 2 <= kScaleLoads * threads
     // One slot past the block takes the writes of threads without a unit, so the LDS write is
@@ -404,7 +407,7 @@ template <WFmt F, bool XF32, int M, int R>
 static hipError_t launch_r(const GemvJobs &jobs, int njobs, int rows, int k, int out_mode, hipStream_t st) {
     const int nch = k / WTraits<F>::CH, waves = ceil_div(nch, 64);
     const dim3 grid(ceil_div(rows, R), njobs), block(64 * waves);
-    if constexpr (F == WFmt::FP4_OCP && R == 4) {
+    if constexpr (F == WFmt::FP4_OCP && R == 4 && M >= 2) {
         bool dw = nch % 4 == 0;
         for (int j = 0; j < njobs; j++) dw = dw && ((uintptr_t)jobs.j[j].s & 3) == 0;
         if (dw) {
