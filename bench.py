@@ -592,10 +592,12 @@ def ref_method_workload(torch, kind, rows, k, group_rows=0, reps=200):
     return {"workload": name, "us": us, "GB_s": nbytes / us / 1e3, "bytes": nbytes, "reps": reps}
 
 
-def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168, prequant=False, use_graph=True):
+def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168, prequant=False, use_graph=True, packed=False):
     """C5: multi-token expert GEMM, M = 64 tokens, W [2048 x 7168] FP4 or FP8 (scaled f8f6f4 MFMA).
     prequant: the activations are quantized outside the timed region and the GEMM proper is timed
-    (stbl_amd_gemm_q, fp8_gemm(a, a_s, b, b_s)'s form); otherwise act_quant + GEMM (stbl_amd_gemm)."""
+    (stbl_amd_gemm_q, fp8_gemm(a, a_s, b, b_s)'s form); otherwise act_quant + GEMM (stbl_amd_gemm).
+    packed: the weight codes packed once beforehand into operand order (stbl_amd_gemm_pack), the
+    calls stbl_amd_gemm_q_packed / stbl_amd_gemm_packed."""
     from stblarge_amd import _lib, data, ops
 
     dev = torch.device("cuda:0")
@@ -604,7 +606,7 @@ def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168, prequant=Fals
     del w
     wbytes = ops._mat_bytes(fmt, n, k)
     copies = max(2, math.ceil(ROTATE_BYTES / wbytes))
-    cs = [codes.clone() for _ in range(copies)]
+    cs = [ops.gemm_pack(codes, fmt) if packed else codes.clone() for _ in range(copies)]
     ss = [scales.clone() for _ in range(copies)]
     x = data.activation(m, k, seed=32, device=dev)
     aq, a_s = ops.act_quant_e4m3(x, 128)
@@ -614,18 +616,21 @@ def gemm_workload(torch, fmt, steps, warmup, m=64, n=2048, k=7168, prequant=Fals
 
     def launch(i):
         if prequant:
-            _lib.check(lib.stbl_amd_gemm_q(fmt, ops._ptr(y), ops._ptr(cs[i]), ops._ptr(ss[i]), ops._ptr(aq),
-                                           ops._ptr(a_s), m, n, k, 128, 0, ops._ptr(work), ops._stream()), "gemm_q")
+            fn = lib.stbl_amd_gemm_q_packed if packed else lib.stbl_amd_gemm_q
+            _lib.check(fn(fmt, ops._ptr(y), ops._ptr(cs[i]), ops._ptr(ss[i]), ops._ptr(aq), ops._ptr(a_s), m, n, k, 128, 0,
+                          ops._ptr(work), ops._stream()), "gemm_q")
         else:
-            _lib.check(lib.stbl_amd_gemm(fmt, ops._ptr(y), ops._ptr(cs[i]), ops._ptr(ss[i]), ops._ptr(x), m, n, k,
-                                         128, 0, ops._ptr(work), ops._stream()), "gemm")
+            fn = lib.stbl_amd_gemm_packed if packed else lib.stbl_amd_gemm
+            _lib.check(fn(fmt, ops._ptr(y), ops._ptr(cs[i]), ops._ptr(ss[i]), ops._ptr(x), m, n, k, 128, 0,
+                          ops._ptr(work), ops._stream()), "gemm")
 
     ms, nsteps = timed_steps(torch, launch, copies, steps, warmup, use_graph)
     alg = wbytes + (m * k + m * k // 128 if prequant else 2 * m * k) + 2 * m * n
     flops = 2.0 * m * n * k
     name = "fp4" if fmt == ops.FP4 else "fp8"
     peak_tf = 5000.0  # e4m3 activations: the MFMA runs at the fp8 rate for both weight formats
-    return {"workload": f"{name}_gemm{'_q' if prequant else ''}_m{m}_{n}x{k}", "ms_per_step": ms, "steps": nsteps,
+    return {"workload": f"{name}_gemm{'_q' if prequant else ''}{'_packed' if packed else ''}_m{m}_{n}x{k}",
+            "ms_per_step": ms, "steps": nsteps,
             "alg_bytes": alg, "GB_s": alg / (ms * 1e-3) / 1e9, "frac_hbm_peak": alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
             "TFLOP_s": flops / (ms * 1e-3) / 1e12, "frac_mfma_peak": flops / (ms * 1e-3) / 1e12 / peak_tf}
 
@@ -885,7 +890,9 @@ LINE_ROWS = (
     "fp8_gemv_2048x7168_m4", "fp4_gemv_batch16_7168x2048_m1", "fp8_gemv_batch16_7168x2048_m1",
     "fp4_gemv_batch64_7168x2048_m1", "fp8_gemv_batch64_7168x2048_m1", "fp4_expert_ffn_7168x2048_m1",
     "fp8_expert_ffn_7168x2048_m1", "fp4_gemm_q_m64_2048x7168", "fp8_gemm_q_m64_2048x7168", "fp4_gemm_m64_2048x7168",
-    "fp8_gemm_m64_2048x7168", "fp4_gemm_q_m64_7168x2048", "ref_abi_gemv_mxfp4_2304x5120",
+    "fp8_gemm_m64_2048x7168", "fp4_gemm_q_m64_7168x2048", "fp4_gemm_q_packed_m64_2048x7168",
+    "fp8_gemm_q_packed_m64_2048x7168", "fp4_gemm_packed_m64_2048x7168", "fp8_gemm_packed_m64_2048x7168",
+    "ref_abi_gemv_mxfp4_2304x5120",
     "ref_abi_gemv_mxfp4_5120x2304", "ref_abi_gemv_fp8_2304x5120", "ref_abi_gemv_mxfp4_batch12_2304x5120",
     "ref_abi_gemv_mxfp4_batch6_5120x2304", "ref_abi_moe_step_v41_t1", "moe_experts_allhit_t1_fp4",
     "moe_experts_allhit_t4_fp4", "moe_experts_allhit_t1_fp4_fp8e8m0_shared", "moe_v41_allhit_t1_fp4_top6_fp8e8m0_shared",
@@ -1169,6 +1176,10 @@ def main():
         for fmt, pq, n, k in [(ops.FP4, True, 2048, 7168), (ops.FP8, True, 2048, 7168), (ops.FP4, False, 2048, 7168),
                               (ops.FP8, False, 2048, 7168), (ops.FP4, True, 7168, 2048)]:
             report(gemm_workload(torch, fmt, K, W, n=n, k=k, prequant=pq, use_graph=graph))
+        # the same GEMMs on weights packed once into operand order (stbl_amd_gemm_pack)
+        for fmt, pq, n, k in [(ops.FP4, True, 2048, 7168), (ops.FP8, True, 2048, 7168), (ops.FP4, False, 2048, 7168),
+                              (ops.FP8, False, 2048, 7168), (ops.FP4, True, 7168, 2048)]:
+            report(gemm_workload(torch, fmt, K, W, n=n, k=k, prequant=pq, use_graph=graph, packed=True))
     if args.only in ("all", "refabi"):
         for kind, rows, k, grp in (("mxfp4", 2304, 5120, 0), ("mxfp4", 5120, 2304, 0), ("fp8", 2304, 5120, 0),
                                    ("fp8", 5120, 2304, 0), ("bf16", 4096, 5120, 0), ("fp8", 32768, 1280, 0),

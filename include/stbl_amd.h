@@ -232,8 +232,23 @@ int stbl_amd_gemm_q(int fmt, void *y, const void *codes, const void *scales, con
                     int n, int k, int act_block, int y_f32, void *work, hipStream_t st);
 
 /* Scratch bytes for stbl_amd_gemm and stbl_amd_gemm_q with m activation rows (n, k as in the call);
- * a workspace of that size also serves every call with fewer rows. */
+ * a workspace of that size also serves every call with fewer rows. The same bytes serve the packed
+ * variants below. */
 uint64_t stbl_amd_gemm_work_bytes(int m, int n, int k);
+
+/* No counterpart in the reference: for callers whose GEMM weights are static (an expert's matrices
+ * loaded once), the weight codes rearranged once into MFMA operand order, so each wave load of the
+ * GEMM reads one contiguous kilobyte instead of 16 columns x 64 bytes. packed receives as many bytes
+ * as codes holds (FP4 n * k / 2, FP8 n * k); n % 16 == 0, k % 128 == 0, both 16-byte aligned and
+ * distinct. The scales keep their layout. */
+int stbl_amd_gemm_pack(int fmt, void *packed, const void *codes, int n, int k, hipStream_t st);
+
+/* stbl_amd_gemm_q / stbl_amd_gemm with the weight codes from stbl_amd_gemm_pack (n % 16 == 0; every
+ * other argument and result as there, bit for bit). No counterpart in the reference. */
+int stbl_amd_gemm_q_packed(int fmt, void *y, const void *packed, const void *scales, const void *aq, const void *as,
+                           int m, int n, int k, int act_block, int y_f32, void *work, hipStream_t st);
+int stbl_amd_gemm_packed(int fmt, void *y, const void *packed, const void *scales, const void *x, int m, int n, int k,
+                         int act_block, int y_f32, void *work, hipStream_t st);
 
 /* act_quant(x, block, "ue8m0") (ref/kernel.py:35-45) as the GEMM consumes it: x bf16 [rows][k] ->
  * e4m3 codes [rows][k] and E8M0 scale bytes [rows][k/block]; block 32 or 128. Non-finite values as

@@ -56,6 +56,9 @@ SIGNATURES = {
     "stbl_amd_gemm": (I, [I, P, P, P, P, I, I, I, I, I, P, P]),
     "stbl_amd_gemm_q": (I, [I, P, P, P, P, P, I, I, I, I, I, P, P]),
     "stbl_amd_gemm_work_bytes": (U64, [I, I, I]),
+    "stbl_amd_gemm_pack": (I, [I, P, P, I, I, P]),
+    "stbl_amd_gemm_q_packed": (I, [I, P, P, P, P, P, I, I, I, I, I, P, P]),
+    "stbl_amd_gemm_packed": (I, [I, P, P, P, P, I, I, I, I, I, P, P]),
     "stbl_amd_act_quant_e4m3": (I, [P, I, I, I, P, P, P]),
     "stbl_amd_cache_create": (P, [I, U64, P, U64, I, I]),
     "stbl_amd_cache_create_gguf": (P, [I, ctypes.c_char_p, I, I, I, I]),

@@ -19,7 +19,9 @@
 //                     stbl_amd_gemm quantizes X first (one more launch).
 //   k_gemm_one        the same products in one launch over all of K, for m > 32 and K % 512 == 0
 //                     (the configurations' shapes): small tiles, half-line-balanced operand loads
-//                     and scales loaded four steps at a time.
+//                     and scales loaded four steps at a time;
+//   k_gemm_pack       the weight codes rearranged once into MFMA operand order (WOPS below), which
+//                     both GEMM kernels then read as one contiguous kilobyte per wave load.
 // Operand layout of the 16x16x128 f8f6f4 MFMA (probed on gfx950): lane l = r + 16 g holds row r of A
 // (column r of B); e4m3 operands hold K bytes [16g, 16g+16) and [64+16g, 64+16g+16) of the 128-K
 // step, e2m1 operands K elements [32g, 32g+32) (low nibble first); the lane's E8M0 scale covers K
@@ -137,6 +139,36 @@ __global__ __launch_bounds__(64) void k_act_quant_e4m3_ops(const uint16_t *__res
 
 // ---- GEMM ---------------------------------------------------------------------------------------
 
+// WOPS: weights in MFMA operand order. Per group G of 16 columns and 128-K step s, the 64 lanes'
+// 16-byte operand pieces lie in lane order: FP4 one kilobyte, lane r + 16 g holding bytes [16g,
+// 16g + 16) of column 16 G + r's 64-byte step; FP8 two kilobytes, the first holding bytes [16g, 16g
+// + 16) and the second [64 + 16g, 64 + 16g + 16) of the column's 128-byte step. Blocks run over the
+// steps of a group, then over the groups, so a column group's weights stay one contiguous run and
+// the packed array has the size of the codes. Byte offset of the block (G, s):
+__device__ __forceinline__ size_t ops_block(int G, int s, int KS, bool fp4) {
+    return ((size_t)G * KS + s) * (fp4 ? 1024 : 2048);
+}
+
+// codes [n][k / 2] (FP4) or [n][k] (FP8), n % 16 == 0, k % 128 == 0 -> the same codes in operand
+// order. Thread t moves the 16-byte piece t of the packed array.
+__global__ __launch_bounds__(256) void k_gemm_pack(const uint8_t *__restrict__ codes, uint8_t *__restrict__ packed,
+                                                   int n, int k, int fp4, size_t pieces) {
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= pieces) return;
+    const int KS = k >> 7, lane = (int)(t & 63), r = lane & 15, g = lane >> 4;
+    size_t src;
+    if (fp4) {
+        const size_t blk = t >> 6;  // G * KS + s
+        const size_t G = blk / KS, st = blk % KS;
+        src = (16 * G + r) * (size_t)(k >> 1) + st * 64 + 16 * g;
+    } else {
+        const size_t blk = t >> 7, half = (t >> 6) & 1;  // (G * KS + s) * 2 + half
+        const size_t G = blk / KS, st = blk % KS;
+        src = (16 * G + r) * (size_t)k + st * 128 + 64 * half + 16 * g;
+    }
+    *(u32x4 *)(packed + 16 * t) = *(const u32x4 *)(codes + src);
+}
+
 // One workgroup owns a 16 MT x 16 NT output tile (MT m-tiles x NT n-tiles of 16 x 16, rows m0 ..) and
 // a slice of up to NW * SW 128-K steps; wave w takes SW consecutive steps of the slice and accumulates
 // its MT * NT tiles in registers, loading its activations and weights straight from global memory
@@ -149,7 +181,7 @@ __global__ __launch_bounds__(64) void k_act_quant_e4m3_ops(const uint16_t *__res
 // at about 4x the whole GEMM, so the kernel boundary is the synchronization point.) The workgroup
 // order is gemm_plan's. A rows are lda bytes apart. Partial tiles and the LDS sum hold f32x4
 // q = t * 64 + lane with t = m-tile * NT + n-tile.
-template <bool FP4W, int MT, int NT, int NW, int SW>
+template <bool FP4W, int MT, int NT, int NW, int SW, bool WOPS>
 __global__ __launch_bounds__(NW * 64) void k_gemm(const uint8_t *__restrict__ wc, const void *__restrict__ ws,
                                                   const uint8_t *__restrict__ aq, const uint8_t *__restrict__ as_,
                                                   f32x4 *__restrict__ part, void *__restrict__ y, int y_f32, int M,
@@ -186,7 +218,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemm(const uint8_t *__restrict__ wc
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const int n = min(n0 + 16 * nt + r, N - 1);
-            if constexpr (FP4W) {
+            if constexpr (WOPS) {  // operand order: one contiguous kilobyte (two for FP8) per load
+                const uint8_t *blk = wc + ops_block(min((n0 >> 4) + nt, (N >> 4) - 1), (int)(kb >> 7), KS, FP4W) + 16 * lane;
+                bv[s][nt][0] = *(const u32x4 *)blk;
+                if constexpr (!FP4W) bv[s][nt][1] = *(const u32x4 *)(blk + 1024);
+                if constexpr (FP4W) bsc[s][nt] = ((const uint8_t *)ws)[(size_t)n * (K >> 5) + (kb >> 5) + g];
+            } else if constexpr (FP4W) {
                 bv[s][nt][0] = *(const u32x4 *)(wc + (size_t)n * (K >> 1) + (kb >> 1) + 16 * g);
                 bsc[s][nt] = ((const uint8_t *)ws)[(size_t)n * (K >> 5) + (kb >> 5) + g];
             } else {
@@ -317,7 +354,7 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const f32x4 *__restrict__ p
 //    act_block 128, 16 bytes per row or column for the per-32 scales), not one byte per step: a
 //    one-byte wave load costs the L1 as much as a 1 KB one. The MFMA reads the low byte of its scale
 //    operand, so each lane shifts its byte down.
-template <bool FP4W, int MT, int NT, int NW, int QW, bool AARR>
+template <bool FP4W, int MT, int NT, int NW, int QW, bool AARR, bool WOPS>
 __global__ __launch_bounds__(NW * 64) void k_gemm_one(const uint8_t *__restrict__ wc, const void *__restrict__ ws,
                                                       const uint8_t *__restrict__ aq, const uint8_t *__restrict__ as_,
                                                       void *__restrict__ y, int y_f32, int M, int N, int K, int lda,
@@ -372,7 +409,18 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_one(const uint8_t *__restrict_
 #pragma unroll
         for (int s = 0; s < SW; s++) {
             const size_t kb = (size_t)(s < nst ? s0 + s : s0) * 128;
-            if constexpr (FP4W) {
+            if constexpr (WOPS) {  // operand order: steps s and s + 1 of a group are adjacent blocks
+                if (!FP4W || s % 2 == 0) {
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++) {
+                        const uint8_t *blk = wc + ops_block(min((n0 >> 4) + nt, (N >> 4) - 1), (int)(kb >> 7), KS, FP4W) + 16 * lane;
+                        bv[s][nt][0] = *(const u32x4 *)blk;
+                        if constexpr (FP4W) bv[s + 1][nt][0] = *(const u32x4 *)(blk + 1024);
+                        else bv[s][nt][1] = *(const u32x4 *)(blk + 1024);
+                    }
+                }
+                if constexpr (!FP4W) wsc[s] = ((const float *)ws)[(size_t)(n0 >> 7) * KS + (kb >> 7)];
+            } else if constexpr (FP4W) {
                 if (s % 2 == 0) {
 #pragma unroll
                     for (int nt = 0; nt < NT; nt++) {
@@ -421,11 +469,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_one(const uint8_t *__restrict_
             for (int nt = 0; nt < NT; nt++) {
                 if constexpr (FP4W) {
                     const u32x4 x0 = bv[s & ~1][nt][0], x1 = bv[s | 1][nt][0];
-                    const u32x4 b0 = live ? ((odd == (s & 1)) ? x0 : x1) : z4;
+                    const u32x4 b0 = live ? (WOPS ? bv[s][nt][0] : (odd == (s & 1)) ? x0 : x1) : z4;
                     b[nt] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], 0, 0, 0, 0};
                 } else {
                     const u32x4 x0 = bv[s][nt][0], x1 = bv[s][nt][1];
-                    const u32x4 b0 = live ? (odd ? x1 : x0) : z4, b1 = live ? (odd ? x0 : x1) : z4;
+                    const bool sw = odd && !WOPS;  // operand-order weights need no half swap
+                    const u32x4 b0 = live ? (sw ? x1 : x0) : z4, b1 = live ? (sw ? x0 : x1) : z4;
                     b[nt] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
                 }
             }
@@ -543,17 +592,17 @@ static uint64_t part_reserve(int m, int n, int k) {
     return a256(std::max(part_bytes(gemm_plan(m, n, k, false)), part_bytes(gemm_plan(1, n, k, false))));
 }
 
-template <int MT, int NT, int NW>
+template <int MT, int NT, int NW, bool WOPS>
 static hipError_t launch_gemm_t(const GemmPlan &p, int fmt, void *y, const void *codes, const void *scales,
                                 const uint8_t *aq, int lda, const uint8_t *as_, int m, int n, int k, int shift,
                                 int y_f32, f32x4 *part, hipStream_t st) {
     static_assert(MT == 4 || NW == 16, "split K (the reduce kernel) takes 64-row tiles only");
     const dim3 grid(p.ntiles * p.mgroups * p.slices);
     if (fmt == 0)
-        hipLaunchKernelGGL((k_gemm<true, MT, NT, NW, 1>), grid, dim3(NW * 64), 0, st, (const uint8_t *)codes, scales, aq,
+        hipLaunchKernelGGL((k_gemm<true, MT, NT, NW, 1, WOPS>), grid, dim3(NW * 64), 0, st, (const uint8_t *)codes, scales, aq,
                            as_, part, y, y_f32, m, n, k, lda, shift, p.ntiles, p.mgroups, p.slices, p.steps);
     else
-        hipLaunchKernelGGL((k_gemm<false, MT, NT, NW, 1>), grid, dim3(NW * 64), 0, st, (const uint8_t *)codes, scales, aq,
+        hipLaunchKernelGGL((k_gemm<false, MT, NT, NW, 1, WOPS>), grid, dim3(NW * 64), 0, st, (const uint8_t *)codes, scales, aq,
                            as_, part, y, y_f32, m, n, k, lda, shift, p.ntiles, p.mgroups, p.slices, p.steps);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && p.slices > 1) {
@@ -567,40 +616,49 @@ static hipError_t launch_gemm_t(const GemmPlan &p, int fmt, void *y, const void 
 // Requires p.steps <= the variant's steps per workgroup and p.slices * p.steps covering k / 128, and
 // split K (slices > 1) only in variant 0; A rows lda bytes apart.
 // arr: the activations are in operand order (k_act_quant_e4m3_ops; variants 3 and 4 only).
-template <bool ARR>
+template <bool ARR, bool WOPS>
 static hipError_t launch_gemm_one(const GemmPlan &p, int fmt, void *y, const void *codes, const void *scales,
                                   const uint8_t *aq, int lda, const uint8_t *as_, int m, int n, int k, int act_block,
                                   int y_f32, hipStream_t st) {
     const dim3 grid(p.ntiles * p.mgroups);
     const int a32 = act_block == 32;
     if (p.variant == 3 && fmt == 0)
-        hipLaunchKernelGGL((k_gemm_one<true, 1, 2, 8, 2, ARR>), grid, dim3(512), 0, st, (const uint8_t *)codes, scales, aq,
+        hipLaunchKernelGGL((k_gemm_one<true, 1, 2, 8, 2, ARR, WOPS>), grid, dim3(512), 0, st, (const uint8_t *)codes, scales, aq,
                            as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
     else if (p.variant == 3)
-        hipLaunchKernelGGL((k_gemm_one<false, 1, 2, 16, 1, ARR>), grid, dim3(1024), 0, st, (const uint8_t *)codes, scales,
+        hipLaunchKernelGGL((k_gemm_one<false, 1, 2, 16, 1, ARR, WOPS>), grid, dim3(1024), 0, st, (const uint8_t *)codes, scales,
                            aq, as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
     else if (fmt == 0)
-        hipLaunchKernelGGL((k_gemm_one<true, 2, 4, 4, 1, ARR>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales, aq,
+        hipLaunchKernelGGL((k_gemm_one<true, 2, 4, 4, 1, ARR, WOPS>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales, aq,
                            as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
     else
-        hipLaunchKernelGGL((k_gemm_one<false, 2, 4, 4, 1, ARR>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales,
+        hipLaunchKernelGGL((k_gemm_one<false, 2, 4, 4, 1, ARR, WOPS>), grid, dim3(256), 0, st, (const uint8_t *)codes, scales,
                            aq, as_, y, y_f32, m, n, k, lda, a32, p.ntiles);
     return hipGetLastError();
 }
 
-static hipError_t launch_gemm_plan(const GemmPlan &p, int fmt, void *y, const void *codes, const void *scales,
-                                   const uint8_t *aq, int lda, const uint8_t *as_, int m, int n, int k, int act_block,
-                                   int y_f32, void *work, hipStream_t st, bool arr = false) {
+template <bool WOPS>
+static hipError_t launch_gemm_plan_w(const GemmPlan &p, int fmt, void *y, const void *codes, const void *scales,
+                                     const uint8_t *aq, int lda, const uint8_t *as_, int m, int n, int k, int act_block,
+                                     int y_f32, void *work, hipStream_t st, bool arr) {
     f32x4 *part = (f32x4 *)work;
     const int shift = act_block == 32 ? 5 : 7;
     if (p.variant >= 3)
-        return arr ? launch_gemm_one<true>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, act_block, y_f32, st)
-                   : launch_gemm_one<false>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, act_block, y_f32, st);
+        return arr ? launch_gemm_one<true, WOPS>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, act_block, y_f32, st)
+                   : launch_gemm_one<false, WOPS>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, act_block, y_f32, st);
     if (p.variant == 0)
-        return launch_gemm_t<4, 4, 8>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
+        return launch_gemm_t<4, 4, 8, WOPS>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
     if (p.variant == 1)
-        return launch_gemm_t<4, 2, 16>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
-    return launch_gemm_t<2, 4, 16>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
+        return launch_gemm_t<4, 2, 16, WOPS>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
+    return launch_gemm_t<2, 4, 16, WOPS>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, shift, y_f32, part, st);
+}
+
+// wops: the weight codes are in operand order (k_gemm_pack)
+static hipError_t launch_gemm_plan(const GemmPlan &p, int fmt, void *y, const void *codes, const void *scales,
+                                   const uint8_t *aq, int lda, const uint8_t *as_, int m, int n, int k, int act_block,
+                                   int y_f32, void *work, hipStream_t st, bool arr = false, bool wops = false) {
+    return wops ? launch_gemm_plan_w<true>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, act_block, y_f32, work, st, arr)
+                : launch_gemm_plan_w<false>(p, fmt, y, codes, scales, aq, lda, as_, m, n, k, act_block, y_f32, work, st, arr);
 }
 
 // variants 3 and 4 load scale words 16 bytes at a time; unaligned scale arrays take the other plans
@@ -610,9 +668,9 @@ static GemmPlan plan_for(int fmt, const void *scales, const uint8_t *as_, int m,
 
 static hipError_t launch_gemm(int fmt, void *y, const void *codes, const void *scales, const uint8_t *aq,
                               const uint8_t *as_, int m, int n, int k, int act_block, int y_f32, void *work,
-                              hipStream_t st) {
+                              hipStream_t st, bool wops = false) {
     return launch_gemm_plan(plan_for(fmt, scales, as_, m, n, k), fmt, y, codes, scales, aq, k, as_, m, n, k, act_block,
-                            y_f32, work, st);
+                            y_f32, work, st, false, wops);
 }
 
 // Rows of the activation codes in the workspace: a whole number of 16-row groups (operand order).
@@ -641,19 +699,26 @@ uint64_t stbl_amd_gemm_work_bytes(int m, int n, int k) {
     return part_reserve(m, n, k) + aq_bytes(m, k) + a256((uint64_t)m * (k / 32)) + 256;
 }
 
-int stbl_amd_gemm_q(int fmt, void *y, const void *codes, const void *scales, const void *aq, const void *as, int m,
-                    int n, int k, int act_block, int y_f32, void *work, hipStream_t st) {
-    if (int e = check_gemm("gemm_q", fmt, y, codes, scales, m, n, k, act_block, work)) return e;
-    if (!aq || !as || !aligned16(aq)) return abi_fail(hipErrorInvalidValue, "gemm_q: aq (16-byte aligned) and as needed");
+}  // extern "C"
+
+namespace stbl {
+
+static int gemm_q_any(const char *name, bool wops, int fmt, void *y, const void *codes, const void *scales,
+                      const void *aq, const void *as, int m, int n, int k, int act_block, int y_f32, void *work,
+                      hipStream_t st) {
+    if (int e = check_gemm(name, fmt, y, codes, scales, m, n, k, act_block, work)) return e;
+    if (wops && n % 16) return abi_fail(hipErrorInvalidValue, "%s: packed weights need n %% 16 == 0 (n=%d)", name, n);
+    if (!aq || !as || !aligned16(aq)) return abi_fail(hipErrorInvalidValue, "%s: aq (16-byte aligned) and as needed", name);
     return abi_status(launch_gemm(fmt, y, codes, scales, (const uint8_t *)aq, (const uint8_t *)as, m, n, k, act_block,
-                                  y_f32, work, st),
-                      "gemm_q launch");
+                                  y_f32, work, st, wops),
+                      name);
 }
 
-int stbl_amd_gemm(int fmt, void *y, const void *codes, const void *scales, const void *x, int m, int n, int k,
-                  int act_block, int y_f32, void *work, hipStream_t st) {
-    if (int e = check_gemm("gemm", fmt, y, codes, scales, m, n, k, act_block, work)) return e;
-    if (!x || !aligned16(x)) return abi_fail(hipErrorInvalidValue, "gemm: x must be 16-byte aligned");
+static int gemm_any(const char *name, bool wops, int fmt, void *y, const void *codes, const void *scales,
+                    const void *x, int m, int n, int k, int act_block, int y_f32, void *work, hipStream_t st) {
+    if (int e = check_gemm(name, fmt, y, codes, scales, m, n, k, act_block, work)) return e;
+    if (wops && n % 16) return abi_fail(hipErrorInvalidValue, "%s: packed weights need n %% 16 == 0 (n=%d)", name, n);
+    if (!x || !aligned16(x)) return abi_fail(hipErrorInvalidValue, "%s: x must be 16-byte aligned", name);
     uint8_t *aq = (uint8_t *)work + part_reserve(m, n, k);
     uint8_t *as_ = aq + aq_bytes(m, k);
     // the one-launch plans read activations this call quantizes in operand order (one contiguous
@@ -670,8 +735,44 @@ int stbl_amd_gemm(int fmt, void *y, const void *codes, const void *scales, const
     }
     hipError_t e = hipGetLastError();
     if (e == hipSuccess)
-        e = launch_gemm_plan(p, fmt, y, codes, scales, aq, k, as_, m, n, k, act_block, y_f32, work, st, arr);
-    return abi_status(e, "gemm launch");
+        e = launch_gemm_plan(p, fmt, y, codes, scales, aq, k, as_, m, n, k, act_block, y_f32, work, st, arr, wops);
+    return abi_status(e, name);
+}
+
+}  // namespace stbl
+
+extern "C" {
+
+int stbl_amd_gemm_q(int fmt, void *y, const void *codes, const void *scales, const void *aq, const void *as, int m,
+                    int n, int k, int act_block, int y_f32, void *work, hipStream_t st) {
+    return gemm_q_any("gemm_q", false, fmt, y, codes, scales, aq, as, m, n, k, act_block, y_f32, work, st);
+}
+
+int stbl_amd_gemm(int fmt, void *y, const void *codes, const void *scales, const void *x, int m, int n, int k,
+                  int act_block, int y_f32, void *work, hipStream_t st) {
+    return gemm_any("gemm", false, fmt, y, codes, scales, x, m, n, k, act_block, y_f32, work, st);
+}
+
+int stbl_amd_gemm_pack(int fmt, void *packed, const void *codes, int n, int k, hipStream_t st) {
+    if (fmt != 0 && fmt != 1) return abi_fail(hipErrorInvalidValue, "gemm_pack: unknown format %d", fmt);
+    if (!packed || !codes || n < 16 || n % 16 || n > kGemmMaxN || k < 128 || k % 128)
+        return abi_fail(hipErrorInvalidValue, "gemm_pack: need n %% 16 == 0 and k %% 128 == 0 (n=%d k=%d)", n, k);
+    if (!aligned16(packed) || !aligned16(codes) || packed == codes)
+        return abi_fail(hipErrorInvalidValue, "gemm_pack: codes and packed must be distinct 16-byte aligned buffers");
+    const size_t pieces = (size_t)n * k / (fmt == 0 ? 32 : 16);
+    hipLaunchKernelGGL(k_gemm_pack, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, st, (const uint8_t *)codes,
+                       (uint8_t *)packed, n, k, fmt == 0 ? 1 : 0, pieces);
+    return abi_status(hipGetLastError(), "gemm_pack launch");
+}
+
+int stbl_amd_gemm_q_packed(int fmt, void *y, const void *packed, const void *scales, const void *aq, const void *as,
+                           int m, int n, int k, int act_block, int y_f32, void *work, hipStream_t st) {
+    return gemm_q_any("gemm_q_packed", true, fmt, y, packed, scales, aq, as, m, n, k, act_block, y_f32, work, st);
+}
+
+int stbl_amd_gemm_packed(int fmt, void *y, const void *packed, const void *scales, const void *x, int m, int n, int k,
+                         int act_block, int y_f32, void *work, hipStream_t st) {
+    return gemm_any("gemm_packed", true, fmt, y, packed, scales, x, m, n, k, act_block, y_f32, work, st);
 }
 
 // act_quant(x, block, "ue8m0") of ref/kernel.py:35-45 with the codes and E8M0 scale bytes it feeds

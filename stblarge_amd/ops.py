@@ -516,6 +516,54 @@ def gemm_q(codes, scales, aq, a_s, fmt, act_block=128, out_f32=False, work=None)
     return y
 
 
+def gemm_pack(codes, fmt):
+    """The weight codes in MFMA operand order (stbl_amd_gemm_pack), for gemm_packed / gemm_q_packed:
+    a uint8 tensor of the codes' size; rows (n) a multiple of 16, K a multiple of 128."""
+    _need(codes, torch.uint8, "codes", 2)
+    n = codes.shape[0]
+    k = codes.shape[1] * (2 if fmt == FP4 else 1)
+    packed = torch.empty_like(codes)
+    _lib.check(_lib.load().stbl_amd_gemm_pack(fmt, _ptr(packed), _ptr(codes), n, k, _stream()), "gemm_pack")
+    return packed
+
+
+def gemm_packed(packed, scales, x, fmt, act_block=128, out_f32=False, work=None):
+    """gemm() with the weight codes from gemm_pack; the same result bit for bit."""
+    _need(x, torch.bfloat16, "x", 2)
+    m, k = x.shape
+    if m < 1:
+        raise ValueError("gemm_packed: x has no rows")
+    n = _gemm_shapes(packed, scales, fmt, k)
+    work = _work_for(work, min(m, GEMM_MAX_M), n, k, x.device)
+    y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=x.device)
+    for r0 in range(0, m, GEMM_MAX_M):
+        mc = min(GEMM_MAX_M, m - r0)
+        _lib.check(_lib.load().stbl_amd_gemm_packed(fmt, _ptr(y[r0:r0 + mc]), _ptr(packed), _ptr(scales),
+                                                    _ptr(x[r0:r0 + mc]), mc, n, k, act_block, int(out_f32), _ptr(work),
+                                                    _stream()), "gemm_packed")
+    return y
+
+
+def gemm_q_packed(packed, scales, aq, a_s, fmt, act_block=128, out_f32=False, work=None):
+    """gemm_q() with the weight codes from gemm_pack; the same result bit for bit."""
+    _need(aq, torch.uint8, "aq", 2)
+    _need(a_s, torch.uint8, "a_s", 2)
+    m, k = aq.shape
+    if m < 1:
+        raise ValueError("gemm_q_packed: aq has no rows")
+    if tuple(a_s.shape) != (m, k // act_block):
+        raise ValueError(f"a_s {tuple(a_s.shape)} does not match aq {tuple(aq.shape)} at block {act_block}")
+    n = _gemm_shapes(packed, scales, fmt, k)
+    work = _work_for(work, min(m, GEMM_MAX_M), n, k, aq.device)
+    y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=aq.device)
+    for r0 in range(0, m, GEMM_MAX_M):
+        mc = min(GEMM_MAX_M, m - r0)
+        _lib.check(_lib.load().stbl_amd_gemm_q_packed(fmt, _ptr(y[r0:r0 + mc]), _ptr(packed), _ptr(scales),
+                                                      _ptr(aq[r0:r0 + mc]), _ptr(a_s[r0:r0 + mc]), mc, n, k, act_block,
+                                                      int(out_f32), _ptr(work), _stream()), "gemm_q_packed")
+    return y
+
+
 def act_quant_e4m3(x, block=128):
     """(e4m3 codes uint8 [rows, k], E8M0 scale bytes uint8 [rows, k/block]) of bf16 x."""
     _need(x, torch.bfloat16, "x", 2)

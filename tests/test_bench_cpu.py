@@ -110,7 +110,7 @@ def test_whole_output_fits_the_driver_tail():
     import bench
 
     rows = _canned_rows()
-    while len(rows) < 80:  # a default run reports 76 rows; names of 40 characters
+    while len(rows) < 86:  # a default run reports 81 rows; names of 40 characters
         r = dict(rows["fp4_gemm_q_m64_2048x7168"])
         r["workload"] = f"workload_name_for_sizing_{len(rows):04d}x4096_m1"
         rows[r["workload"]] = r

@@ -206,3 +206,65 @@ def test_gemm_non_finite_activations(gpu, fmt):
         assert np.isnan(y32[nan_rows]).all() and np.isnan(y16.astype(np.float32)[nan_rows]).all()
         keep = np.delete(np.arange(m), nan_rows)
         _check(y32[keep], y16[keep], want[keep])
+
+
+def _pack_reference(codes, fmt):
+    # the operand-order layout, restated: per 16-column group G and 128-K step s, lane 16 g + r holds
+    # bytes [16g, 16g + 16) of column 16 G + r's step (FP4: 64-byte steps; FP8: 128-byte steps in two
+    # kilobyte pieces, bytes [64h + 16g, 64h + 16g + 16) in piece h)
+    n, kb = codes.shape
+    if fmt == 0:
+        return codes.reshape(n // 16, 16, kb // 64, 4, 16).transpose(0, 2, 3, 1, 4).reshape(-1)
+    return codes.reshape(n // 16, 16, kb // 128, 2, 4, 16).transpose(0, 2, 3, 4, 1, 5).reshape(-1)
+
+
+@pytest.mark.parametrize("fmt,n,k", [(0, 48, 384), (1, 32, 256), (0, 2048, 7168), (1, 7168, 2048)])
+def test_gemm_pack_layout(gpu, fmt, n, k):
+    rng = np.random.default_rng(n + k)
+    codes = rng.integers(0, 256, (n, k // 2 if fmt == 0 else k), dtype=np.uint8)
+    got = np_(ops.gemm_pack(torch.from_numpy(codes).to(gpu), fmt)).reshape(-1)
+    assert np.array_equal(got, _pack_reference(codes, fmt))
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("block", [32, 128])
+@pytest.mark.parametrize("m,n,k,shift", [(64, 2048, 7168, False), (64, 7168, 2048, False), (40, 2048, 6656, False),
+                                         (16, 7168, 2048, False), (37, 208, 384, False), (64, 7168, 2048, True),
+                                         (150, 1024, 2048, False)])
+def test_gemm_packed_matches_row_major(gpu, fmt, block, m, n, k, shift):
+    # every tile plan (one-launch 16 x 32 and 32 x 64 tiles, 64 x 32 tiles in one slice, split K,
+    # two 32-row groups for unaligned activation scales, 64-row launches) reads packed weights to the
+    # same outputs bit for bit, and so against the oracle as the row-major call is checked
+    if fmt == 1 and block == 32:
+        pytest.skip("FP8 weights pair with act_block 128 in the reference configuration")
+    w = data.weight(n, k, seed=n + k + m)
+    q = oracle.quant_fp4 if fmt == 0 else oracle.quant_fp8_b128
+    codes, scales = q(w.numpy())
+    x = data.activation(m, k, seed=m + 3)
+    dc, ds, xg = torch.from_numpy(codes).to(gpu), torch.from_numpy(scales).to(gpu), x.to(gpu)
+    pk = ops.gemm_pack(dc, fmt)
+    aq, a_s = ops.act_quant_e4m3(xg, block)
+    if shift:
+        buf = torch.zeros(a_s.numel() + 16, dtype=a_s.dtype, device=gpu)
+        a_s2 = buf[1:1 + a_s.numel()].view(a_s.shape)
+        a_s2.copy_(a_s)
+        a_s = a_s2
+    want_q = np_(ops.gemm_q(dc, ds, aq, a_s, fmt, block, out_f32=True))
+    assert bits_equal(np_(ops.gemm_q_packed(pk, ds, aq, a_s, fmt, block, out_f32=True)), want_q)
+    assert np.array_equal(np_(ops.gemm_q_packed(pk, ds, aq, a_s, fmt, block)), np_(ops.gemm_q(dc, ds, aq, a_s, fmt, block)))
+    assert bits_equal(np_(ops.gemm_packed(pk, ds, xg, fmt, block, out_f32=True)), np_(ops.gemm(dc, ds, xg, fmt, block, out_f32=True)))
+    if m == 64 and not shift:
+        deq = oracle.dequant_fp4(codes, scales) if fmt == 0 else oracle.dequant_fp8_b128(codes, scales)
+        assert rel_err(want_q, _oracle_gemm(x, deq, block)) <= 1e-3
+
+
+def test_gemm_pack_refuses_bad_shapes(gpu):
+    codes = torch.zeros((40, 64), dtype=torch.uint8, device=gpu)  # n % 16 != 0
+    with pytest.raises(RuntimeError):
+        ops.gemm_pack(codes, 0)
+    w = torch.zeros((40, 128), dtype=torch.uint8, device=gpu)
+    s = torch.zeros((40, 8), dtype=torch.uint8, device=gpu)
+    aq = torch.zeros((64, 256), dtype=torch.uint8, device=gpu)
+    a_s = torch.zeros((64, 2), dtype=torch.uint8, device=gpu)
+    with pytest.raises(RuntimeError):
+        ops.gemm_q_packed(w, s, aq, a_s, 0)
